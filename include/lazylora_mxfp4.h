@@ -1,0 +1,118 @@
+/*
+ * lazylora_mxfp4.h — C ABI of the MI355X (gfx950) MXFP4 routed-expert library.
+ *
+ * The first four entry points replace the reference's CPU kernels one for one
+ * (lazy_lora/native/mxfp4_gemm.c, bound by ctypes in lazy_lora/native/__init__.py:19-74);
+ * the routed-layer entry points replace the per-expert Python loops that drive them
+ * (lazy_lora/trainer/lazy_trainer.py:806-880).
+ *
+ * Conventions (same as the reference, mxfp4_gemm.c:12-18):
+ *   W is [R, K] row-major: packed [R, K/2] bytes (low nibble = even element), scales
+ *   [R, K/32] E8M0 bytes; value = e2m1(code) * 2^(s-127); a scale byte >= 253 contributes 0.
+ *   K must be a multiple of 32. All array pointers are DEVICE pointers (HBM), except where
+ *   noted. Every call is asynchronous on `stream` (0 = the null stream).
+ *
+ * Deviations from the reference signatures, all deliberate:
+ *   - every call returns int status (0 = ok, see MXFP4_E*) instead of void;
+ *   - every call takes a hipStream_t, and calls that need scratch take a caller-owned
+ *     device workspace plus its size (query with the *_workspace_size functions), so the
+ *     library itself never allocates device memory.
+ *
+ * Numerics: the forward products run on the fp4-native scaled MFMA with the activations
+ * split into two e4m3 terms; the transposed products decode the weights exactly to bf16 and
+ * split the activation gradients into two bf16 terms. Both accumulate in fp32. Results match
+ * the reference's fp32 CPU path within rel-L2 5e-3 (the tolerance stated for this path), and
+ * mxfp4_dequant matches it bit for bit.
+ */
+#ifndef LAZYLORA_MXFP4_H
+#define LAZYLORA_MXFP4_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXFP4_OK 0
+#define MXFP4_EINVAL (-1)     /* bad shape / pointer / flag; nothing was launched */
+#define MXFP4_EWORKSPACE (-2) /* workspace smaller than *_workspace_size() */
+#define MXFP4_EHIP (-3)       /* a HIP launch failed; see mxfp4_last_error() */
+
+/* Activation functions of the expert GLU. */
+#define MXFP4_ACT_SWIGLU 0 /* silu(gate) * up */
+#define MXFP4_ACT_SITU 1   /* 4 tanh(g/4) sigmoid(g) * 25 tanh(u/25): lazy_lora/core/situ_activation.py:47-75 */
+
+/* Dtype codes for routed-layer inputs. */
+#define MXFP4_F32 0
+#define MXFP4_BF16 1
+#define MXFP4_I32 2
+#define MXFP4_I64 3
+
+/* Flags for the routed layer. */
+#define MXFP4_MOE_SAVE 1          /* forward keeps gate|up and routing in the workspace */
+#define MXFP4_MOE_REUSE_FORWARD 2 /* backward reuses them instead of recomputing */
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char *mxfp4_last_error(void);
+
+/* Replaces int mxfp4_threads(void) (mxfp4_gemm.c:131-138): the parallel width of the
+ * device, here the compute-unit count of the current HIP device. */
+int mxfp4_threads(void);
+
+/* Replaces void mxfp4_dequant(float *out, const uint8_t *packed, const uint8_t *scales,
+ * int K, int R) (mxfp4_gemm.c:142-150): out[R, K] fp32 = W, bit-exact. */
+int mxfp4_dequant(float *out, const uint8_t *packed, const uint8_t *scales, int K, int R,
+                  hipStream_t stream);
+
+/* Replaces void mxfp4_gemm(float *y, const float *x, const uint8_t *packed,
+ * const uint8_t *scales, int M, int K, int R) (mxfp4_gemm.c:64-94):
+ * y[M, R] = x[M, K] . W^T, y fully overwritten. x, y fp32 row-major contiguous. */
+size_t mxfp4_gemm_workspace_size(int M, int K, int R);
+int mxfp4_gemm(float *y, const float *x, const uint8_t *packed, const uint8_t *scales, int M,
+               int K, int R, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Replaces void mxfp4_gemm_t(float *y, const float *dy, const uint8_t *packed,
+ * const uint8_t *scales, int M, int K, int R) (mxfp4_gemm.c:96-129):
+ * y[M, K] += dy[M, R] . W (accumulates into y, like the reference). */
+size_t mxfp4_gemm_t_workspace_size(int M, int K, int R);
+int mxfp4_gemm_t(float *y, const float *dy, const uint8_t *packed, const uint8_t *scales, int M,
+                 int K, int R, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Routed-expert layer forward, replacing LazyLoRATrainer._routed_experts_forward
+ * (lazy_lora/trainer/lazy_trainer.py:806-834) with LoRA off:
+ *   out[N, D] fp32 = sum over (t, slot) of topk_w[t, slot] * expert_e(h[t]),
+ *   expert_e(x) = W2_e . act(W1_e . x, W3_e . x),  e = topk_idx[t, slot].
+ * h: [N, D] fp32 or bf16 (h_dtype). topk_idx: [N, k] int32 or int64 (idx_dtype); ids outside
+ * [0, E) contribute nothing. topk_w: [N, k] fp32.
+ * Expert weights are stacked expert-major: w1p/w3p [E, F, D/2], w1s/w3s [E, F, D/32],
+ * w2p [E, D, F/2], w2s [E, D, F/32]. D and F must be multiples of 32. */
+size_t mxfp4_moe_workspace_size(int N, int k, int E, int D, int F);
+int mxfp4_moe_forward(float *out, const void *h, int h_dtype, const void *topk_idx, int idx_dtype,
+                      const float *topk_w, int N, int k, const uint8_t *w1p, const uint8_t *w1s,
+                      const uint8_t *w3p, const uint8_t *w3s, const uint8_t *w2p,
+                      const uint8_t *w2s, int E, int D, int F, int act_kind, int flags,
+                      void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Routed-expert layer backward, replacing _routed_experts_backward (lazy_trainer.py:836-880)
+ * with LoRA off: grad_h[N, D] fp32 = dL/dh, grad_w[N, k] fp32 = dL/dtopk_w for upstream
+ * grad_out[N, D] fp32. With MXFP4_MOE_REUSE_FORWARD the routing and gate|up saved by a
+ * forward call made with MXFP4_MOE_SAVE on the same inputs and workspace are reused;
+ * otherwise they are recomputed. */
+int mxfp4_moe_backward(float *grad_h, float *grad_w, const float *grad_out, const void *h,
+                       int h_dtype, const void *topk_idx, int idx_dtype, const float *topk_w,
+                       int N, int k, const uint8_t *w1p, const uint8_t *w1s, const uint8_t *w3p,
+                       const uint8_t *w3s, const uint8_t *w2p, const uint8_t *w2s, int E, int D,
+                       int F, int act_kind, int flags, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
+/* Copies the routing status word of a routed-layer workspace to *host_flags after
+ * synchronising `stream`: bit 0 set = some topk_idx entry was outside [0, E). */
+int mxfp4_moe_route_status(const void *workspace, int *host_flags, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAZYLORA_MXFP4_H */

@@ -1,0 +1,331 @@
+// C ABI entry points (declared in include/lazylora_mxfp4.h): argument checks, workspace
+// carving and launch sequences. No device memory is allocated here; callers pass workspaces.
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/lazylora_mxfp4.h"
+#include "mx_device.h"
+#include "mx_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, const char* detail = "")
+{
+  snprintf(g_err, sizeof(g_err), fmt, detail);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where)
+{
+  snprintf(g_err, sizeof(g_err), "%s: %s", where, hipGetErrorString(e));
+  return MXFP4_EHIP;
+}
+
+#define MX_TRY(expr, where)                          \
+  do {                                               \
+    hipError_t e__ = (expr);                         \
+    if (e__ != hipSuccess) return hip_fail(e__, where); \
+  } while (0)
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Two-term activation buffer for [rows, K].
+struct AQ {
+  size_t hi, lo, sc, end;
+};
+AQ aq_layout(size_t base, long long rows, int K)
+{
+  const long long kp = mx::aq_kpad(K);
+  AQ a;
+  a.hi = base;
+  a.lo = align_up(a.hi + (size_t)(rows * kp));
+  a.sc = align_up(a.lo + (size_t)(rows * kp));
+  a.end = align_up(a.sc + (size_t)(rows * mx::aq_scale_row_bytes(K)));
+  return a;
+}
+
+long long pad32(long long v) { return (v + 31) / 32 * 32; }
+
+// Routed-layer workspace: one layout for forward and backward so the backward can reuse
+// what the forward left behind.
+struct MoeLayout {
+  size_t meta, counts, offsets, cursor, tiles, pair_token, pair_w, pair_of;
+  AQ xq, actq;
+  size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part, end;
+  int max_tiles, n_ct_bwd;
+};
+
+MoeLayout moe_layout(int N, int k, int E, int D, int F)
+{
+  MoeLayout L;
+  const long long P = (long long)N * k;
+  L.max_tiles = (int)((P + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile + E);
+  L.n_ct_bwd = (F + mx::kBwdColsPerTile - 1) / mx::kBwdColsPerTile;
+  size_t o = 0;
+  L.meta = o; o = align_up(o + 16 * sizeof(int));
+  L.counts = o; o = align_up(o + sizeof(int) * (size_t)E);
+  L.offsets = o; o = align_up(o + sizeof(int) * (size_t)(E + 1));
+  L.cursor = o; o = align_up(o + sizeof(int) * (size_t)E);
+  L.tiles = o; o = align_up(o + sizeof(int4) * (size_t)L.max_tiles);
+  L.pair_token = o; o = align_up(o + sizeof(int) * (size_t)P);
+  L.pair_w = o; o = align_up(o + sizeof(float) * (size_t)P);
+  L.pair_of = o; o = align_up(o + sizeof(int) * (size_t)P);
+  L.xq = aq_layout(o, N, D); o = L.xq.end;
+  L.actq = aq_layout(o, P, F); o = L.actq.end;
+  L.saved = o; o = align_up(o + sizeof(float) * (size_t)(P * 2 * F));
+  L.ypair = o; o = align_up(o + sizeof(float) * (size_t)(P * D));
+  L.g_hi = o; o = align_up(o + 2 * (size_t)(N * (long long)D));
+  L.g_lo = o; o = align_up(o + 2 * (size_t)(N * (long long)D));
+  L.d_hi = o; o = align_up(o + 2 * (size_t)(P * 2 * F));
+  L.d_lo = o; o = align_up(o + 2 * (size_t)(P * 2 * F));
+  L.gw_part = o; o = align_up(o + sizeof(float) * (size_t)(P * L.n_ct_bwd));
+  L.end = o;
+  return L;
+}
+
+template <typename T>
+T* at(void* ws, size_t off) { return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off); }
+
+int check_moe_args(const void* h, int h_dtype, const void* idx, int idx_dtype, const float* w, int N, int k,
+                   const uint8_t* const* wts, int E, int D, int F, int act_kind)
+{
+  if (N < 0 || k <= 0 || E <= 0 || D <= 0 || F <= 0) return fail(MXFP4_EINVAL, "moe: N, k, E, D, F must be positive%s");
+  if (D % 32 || F % 32) return fail(MXFP4_EINVAL, "moe: D and F must be multiples of 32%s");
+  if (h_dtype != MXFP4_F32 && h_dtype != MXFP4_BF16) return fail(MXFP4_EINVAL, "moe: h must be fp32 or bf16%s");
+  if (idx_dtype != MXFP4_I32 && idx_dtype != MXFP4_I64) return fail(MXFP4_EINVAL, "moe: topk_idx must be int32 or int64%s");
+  if (act_kind != MXFP4_ACT_SWIGLU && act_kind != MXFP4_ACT_SITU) return fail(MXFP4_EINVAL, "moe: unknown act_kind%s");
+  if (N > 0 && (!h || !idx || !w)) return fail(MXFP4_EINVAL, "moe: null input pointer%s");
+  for (int i = 0; i < 6; ++i) {
+    if (!wts[i]) return fail(MXFP4_EINVAL, "moe: null expert weight pointer%s");
+    if (i % 2 == 0 && !aligned16(wts[i])) return fail(MXFP4_EINVAL, "moe: packed weights must be 16-byte aligned%s");
+  }
+  if ((long long)N * k > (1ll << 30)) return fail(MXFP4_EINVAL, "moe: too many (token, slot) pairs%s");
+  return MXFP4_OK;
+}
+
+// Routing + quantised x + gate/up (+GLU) into the workspace.
+int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const float* w, int N, int k,
+              const uint8_t* const* wts, int E, int D, int F, int act_kind, bool save, void* ws, const MoeLayout& L,
+              hipStream_t s)
+{
+  const long long P = (long long)N * k;
+  MX_TRY(mx::launch_route(idx, idx_dtype == MXFP4_I64, w, N, k, E, at<int>(ws, L.counts), at<int>(ws, L.offsets),
+                          at<int>(ws, L.cursor), at<int4>(ws, L.tiles), at<int>(ws, L.meta), at<int>(ws, L.pair_token),
+                          at<float>(ws, L.pair_w), at<int>(ws, L.pair_of), s),
+         "route");
+  MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, at<uint8_t>(ws, L.xq.hi), at<uint8_t>(ws, L.xq.lo),
+                               at<uint8_t>(ws, L.xq.sc), s),
+         "quantise h");
+  if (F % mx::kChunk) {  // padding blocks of the act buffer are read by the down product
+    MX_TRY(mx::launch_zero(at<void>(ws, L.actq.hi), L.actq.end - L.actq.hi, s), "zero act");
+  }
+  mx::FwdArgs a = {};
+  a.wp0 = wts[0]; a.ws0 = wts[1]; a.wp1 = wts[2]; a.ws1 = wts[3];
+  a.wp_estride = (long long)F * D / 2;
+  a.ws_estride = (long long)F * D / 32;
+  a.R = F; a.K = D;
+  a.a_hi = at<uint8_t>(ws, L.xq.hi); a.a_lo = at<uint8_t>(ws, L.xq.lo); a.a_sc = at<uint8_t>(ws, L.xq.sc);
+  a.a_row_map = at<int>(ws, L.pair_token);
+  a.tiles = at<int4>(ws, L.tiles); a.n_tiles = at<int>(ws, L.meta);
+  a.n_ct = F / 32;
+  a.q_hi = at<uint8_t>(ws, L.actq.hi); a.q_lo = at<uint8_t>(ws, L.actq.lo); a.q_sc = at<uint8_t>(ws, L.actq.sc);
+  a.save = save ? at<float>(ws, L.saved) : nullptr;
+  a.act_kind = act_kind;
+  (void)P;
+  MX_TRY(mx::launch_fwd(a, mx::kFwdGateUp, L.max_tiles, s), "gate/up product");
+  return MXFP4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mxfp4_last_error(void) { return g_err; }
+
+int mxfp4_threads(void)
+{
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 1;
+  return cus > 0 ? cus : 1;
+}
+
+int mxfp4_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R, hipStream_t stream)
+{
+  if (K <= 0 || R < 0 || K % 32) return fail(MXFP4_EINVAL, "dequant: K must be a positive multiple of 32%s");
+  if (R > 0 && (!out || !packed || !scales)) return fail(MXFP4_EINVAL, "dequant: null pointer%s");
+  MX_TRY(mx::launch_dequant(out, packed, scales, K, R, stream), "dequant");
+  return MXFP4_OK;
+}
+
+size_t mxfp4_gemm_workspace_size(int M, int K, int R)
+{
+  (void)R;
+  if (M <= 0 || K <= 0) return 0;
+  return aq_layout(0, M, K).end;
+}
+
+int mxfp4_gemm(float* y, const float* x, const uint8_t* packed, const uint8_t* scales, int M, int K, int R,
+               void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+  if (M < 0 || R < 0 || K <= 0 || K % 32) return fail(MXFP4_EINVAL, "gemm: K must be a positive multiple of 32%s");
+  if (M == 0 || R == 0) return MXFP4_OK;
+  if (!y || !x || !packed || !scales) return fail(MXFP4_EINVAL, "gemm: null pointer%s");
+  if (!aligned16(packed)) return fail(MXFP4_EINVAL, "gemm: packed must be 16-byte aligned%s");
+  if (((uintptr_t)x & 7) != 0) return fail(MXFP4_EINVAL, "gemm: x must be 8-byte aligned%s");
+  const AQ q = aq_layout(0, M, K);
+  if (!workspace || workspace_bytes < q.end) return fail(MXFP4_EWORKSPACE, "gemm: workspace too small%s");
+  MX_TRY(mx::launch_quant_rows(x, 0, K, M, K, at<uint8_t>(workspace, q.hi), at<uint8_t>(workspace, q.lo),
+                               at<uint8_t>(workspace, q.sc), stream),
+         "gemm: quantise x");
+  mx::FwdArgs a = {};
+  a.wp0 = packed; a.ws0 = scales;
+  a.R = R; a.K = K;
+  a.a_hi = at<uint8_t>(workspace, q.hi); a.a_lo = at<uint8_t>(workspace, q.lo); a.a_sc = at<uint8_t>(workspace, q.sc);
+  a.M = M;
+  a.n_ct = (R + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
+  a.y = y; a.ldy = R;
+  const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
+  MX_TRY(mx::launch_fwd(a, mx::kFwdPlain, tiles, stream), "gemm: product");
+  return MXFP4_OK;
+}
+
+size_t mxfp4_gemm_t_workspace_size(int M, int K, int R)
+{
+  (void)K;
+  if (M <= 0 || R <= 0) return 0;
+  return 2 * align_up(2 * (size_t)M * (size_t)pad32(R));
+}
+
+int mxfp4_gemm_t(float* y, const float* dy, const uint8_t* packed, const uint8_t* scales, int M, int K, int R,
+                 void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+  if (M < 0 || R < 0 || K <= 0 || K % 32) return fail(MXFP4_EINVAL, "gemm_t: K must be a positive multiple of 32%s");
+  if (M == 0 || R == 0) return MXFP4_OK;
+  if (!y || !dy || !packed || !scales) return fail(MXFP4_EINVAL, "gemm_t: null pointer%s");
+  if (!aligned16(packed)) return fail(MXFP4_EINVAL, "gemm_t: packed must be 16-byte aligned%s");
+  const size_t need = mxfp4_gemm_t_workspace_size(M, K, R);
+  if (!workspace || workspace_bytes < need) return fail(MXFP4_EWORKSPACE, "gemm_t: workspace too small%s");
+  const long long rp = pad32(R);
+  uint16_t* hi = at<uint16_t>(workspace, 0);
+  uint16_t* lo = at<uint16_t>(workspace, need / 2);
+  MX_TRY(mx::launch_split_bf16(dy, R, M, R, (int)rp, hi, lo, stream), "gemm_t: split dy");
+  mx::BwdArgs a = {};
+  a.wp0 = packed; a.ws0 = scales;
+  a.nseg = 1; a.R = R; a.C = K;
+  a.a_hi = hi; a.a_lo = lo; a.lda = rp;
+  a.M = M;
+  a.n_ct = (K + mx::kBwdColsPerTile - 1) / mx::kBwdColsPerTile;
+  a.y = y; a.ldy = K; a.accumulate = 1;
+  const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
+  MX_TRY(mx::launch_bwd(a, mx::kBwdPlain, tiles, stream), "gemm_t: product");
+  return MXFP4_OK;
+}
+
+size_t mxfp4_moe_workspace_size(int N, int k, int E, int D, int F)
+{
+  if (N < 0 || k <= 0 || E <= 0 || D <= 0 || F <= 0) return 0;
+  return moe_layout(N, k, E, D, F).end;
+}
+
+int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
+                      const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p,
+                      const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, int E, int D, int F, int act_kind,
+                      int flags, void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+  const uint8_t* wts[6] = {w1p, w1s, w3p, w3s, w2p, w2s};
+  int rc = check_moe_args(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind);
+  if (rc) return rc;
+  if (N > 0 && !out) return fail(MXFP4_EINVAL, "moe_forward: null output%s");
+  const MoeLayout L = moe_layout(N, k, E, D, F);
+  if (!workspace || workspace_bytes < L.end) return fail(MXFP4_EWORKSPACE, "moe_forward: workspace too small%s");
+  if (N == 0) return MXFP4_OK;
+  rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, (flags & MXFP4_MOE_SAVE) != 0,
+                 workspace, L, stream);
+  if (rc) return rc;
+  mx::FwdArgs a = {};
+  a.wp0 = w2p; a.ws0 = w2s;
+  a.wp_estride = (long long)F * D / 2;
+  a.ws_estride = (long long)F * D / 32;
+  a.R = D; a.K = F;
+  a.a_hi = at<uint8_t>(workspace, L.actq.hi); a.a_lo = at<uint8_t>(workspace, L.actq.lo);
+  a.a_sc = at<uint8_t>(workspace, L.actq.sc);
+  a.tiles = at<int4>(workspace, L.tiles); a.n_tiles = at<int>(workspace, L.meta);
+  a.n_ct = (D + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
+  a.y = at<float>(workspace, L.ypair); a.ldy = D;
+  a.row_w = at<float>(workspace, L.pair_w);
+  MX_TRY(mx::launch_fwd(a, mx::kFwdDown, L.max_tiles, stream), "moe_forward: down product");
+  MX_TRY(mx::launch_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D, stream),
+         "moe_forward: combine");
+  return MXFP4_OK;
+}
+
+int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, const void* h, int h_dtype,
+                       const void* topk_idx, int idx_dtype, const float* topk_w, int N, int k, const uint8_t* w1p,
+                       const uint8_t* w1s, const uint8_t* w3p, const uint8_t* w3s, const uint8_t* w2p,
+                       const uint8_t* w2s, int E, int D, int F, int act_kind, int flags, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream)
+{
+  const uint8_t* wts[6] = {w1p, w1s, w3p, w3s, w2p, w2s};
+  int rc = check_moe_args(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind);
+  if (rc) return rc;
+  if (N > 0 && (!grad_h || !grad_w || !grad_out)) return fail(MXFP4_EINVAL, "moe_backward: null pointer%s");
+  const MoeLayout L = moe_layout(N, k, E, D, F);
+  if (!workspace || workspace_bytes < L.end) return fail(MXFP4_EWORKSPACE, "moe_backward: workspace too small%s");
+  if (N == 0) return MXFP4_OK;
+  if (!(flags & MXFP4_MOE_REUSE_FORWARD)) {
+    rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, true, workspace, L, stream);
+    if (rc) return rc;
+  }
+  // grad_out -> bf16 hi + lo, the A operand of the W2 transposed product
+  MX_TRY(mx::launch_split_bf16(grad_out, D, N, D, D, at<uint16_t>(workspace, L.g_hi), at<uint16_t>(workspace, L.g_lo),
+                               stream),
+         "moe_backward: split grad_out");
+  mx::BwdArgs b = {};
+  b.wp0 = w2p; b.ws0 = w2s;
+  b.wp_estride = (long long)F * D / 2;
+  b.ws_estride = (long long)F * D / 32;
+  b.nseg = 1; b.R = D; b.C = F;
+  b.a_hi = at<uint16_t>(workspace, L.g_hi); b.a_lo = at<uint16_t>(workspace, L.g_lo); b.lda = D;
+  b.a_row_map = at<int>(workspace, L.pair_token);
+  b.tiles = at<int4>(workspace, L.tiles); b.n_tiles = at<int>(workspace, L.meta);
+  b.n_ct = L.n_ct_bwd;
+  b.row_w = at<float>(workspace, L.pair_w);
+  b.saved = at<float>(workspace, L.saved);
+  b.act_kind = act_kind;
+  b.d_hi = at<uint16_t>(workspace, L.d_hi); b.d_lo = at<uint16_t>(workspace, L.d_lo);
+  b.gw_part = at<float>(workspace, L.gw_part);
+  MX_TRY(mx::launch_bwd(b, mx::kBwdDownT, L.max_tiles, stream), "moe_backward: W2 transposed product");
+
+  mx::BwdArgs c = {};
+  c.wp0 = w1p; c.ws0 = w1s; c.wp1 = w3p; c.ws1 = w3s;
+  c.wp_estride = (long long)F * D / 2;
+  c.ws_estride = (long long)F * D / 32;
+  c.nseg = 2; c.R = F; c.C = D;
+  c.a_hi = at<uint16_t>(workspace, L.d_hi); c.a_lo = at<uint16_t>(workspace, L.d_lo); c.lda = 2LL * F;
+  c.tiles = at<int4>(workspace, L.tiles); c.n_tiles = at<int>(workspace, L.meta);
+  c.n_ct = (D + mx::kBwdColsPerTile - 1) / mx::kBwdColsPerTile;
+  c.y = at<float>(workspace, L.ypair); c.ldy = D;
+  MX_TRY(mx::launch_bwd(c, mx::kBwdGateUpT, L.max_tiles, stream), "moe_backward: W1|W3 transposed product");
+  MX_TRY(mx::launch_combine_bwd(grad_h, grad_w, at<float>(workspace, L.ypair), D, at<float>(workspace, L.gw_part),
+                                L.n_ct_bwd, at<int>(workspace, L.pair_of), N, k, D, stream),
+         "moe_backward: combine");
+  return MXFP4_OK;
+}
+
+int mxfp4_moe_route_status(const void* workspace, int* host_flags, hipStream_t stream)
+{
+  if (!workspace || !host_flags) return fail(MXFP4_EINVAL, "route_status: null pointer%s");
+  MX_TRY(hipStreamSynchronize(stream), "route_status: sync");
+  int meta[2] = {0, 0};
+  MX_TRY(hipMemcpy(meta, workspace, sizeof(meta), hipMemcpyDeviceToHost), "route_status: copy");
+  *host_flags = meta[1];
+  return MXFP4_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,192 @@
+// Device-side building blocks shared by the MXFP4 kernels (gfx950 / MI355X only).
+//
+// Conventions used by every kernel in this directory:
+//  * A weight matrix W is logically [R, K] and stored the way LazyLoRA's checkpoints and
+//    lazy_lora/native/mxfp4_gemm.c:12-15 store it: packed [R, K/2] bytes, low nibble = even
+//    element, plus scales [R, K/32] E8M0 bytes. A scale byte >= 253 makes its 32-element
+//    group contribute zero (mxfp4_gemm.c:16-18).
+//  * Activations that feed the forward products are held as a two-term e4m3 split
+//    ("AQ" layout, see below): x ~= (hi + lo) with each term carrying its own E8M0 scale per
+//    32-element block. hi alone keeps 4 significant bits; hi + lo keeps ~8, which puts the
+//    rounding error of an activation below that of bf16.
+//  * The forward products run on v_mfma_scale_f32_16x16x128_f8f6f4 with A = e4m3 activations
+//    and B = the packed fp4 weights exactly as stored, so weights are never decoded in the
+//    forward pass. Lane layouts (measured on the hardware):
+//      B (fp4, 4 VGPRs): lane (j = l%16, g = l/16) holds logical K [32g, 32g+32) of column j,
+//                        i.e. one whole 16-byte MX block; its scale is the lane's own byte.
+//      A (fp8, 8 VGPRs): lane (i = l%16, g) holds logical K [16g, 16g+16) in bytes 0-15 and
+//                        [64+16g, 64+16g+16) in bytes 16-31; the lane's scale byte applies
+//                        to logical block g of row i.
+//      C: lane (j, g) holds rows 4g..4g+3 of column j.
+//    op_sel q (0..3) picks byte q of the 32-bit scale register for A and B alike.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+#define MX_DEV __device__ __forceinline__
+
+namespace mx {
+
+constexpr int kGroup = 32;        // elements per MX block
+constexpr int kChunk = 512;       // K elements per "super-chunk" of the forward main loop
+constexpr int kChunkBlocks = 16;  // MX blocks per super-chunk
+
+// ------------------------------------------------------------------ AQ activation layout
+// An activation matrix [rows, K] is stored as
+//   hi, lo : [rows, Kp] bytes (e4m3), Kp = K rounded up to 512, zero beyond K
+//   sc     : [rows, Kp/32, 2] scale bytes, grouped as [row][blk/4][plane(hi,lo)][blk%4]
+// Inside each 512-element super-chunk the bytes are permuted so that the A operand of MFMA
+// q (q = 0..3) for lane group g is the 32 contiguous bytes at offset 128*g + 32*q. The
+// forward loop assigns actual block 16*c + 4*b + q to logical block b of MFMA q, so
+// lane g's B operands for q = 0..3 are 4 consecutive MX blocks of one weight row (64
+// contiguous bytes, scales in one dword), and its A operands are one 128-byte run.
+MX_DEV int aq_pos(int k_local)  // k_local in [0, 512): byte position inside the super-chunk
+{
+  const int b = k_local >> 5, h = (k_local >> 4) & 1, j = k_local & 15;
+  const int a = b >> 2, q = b & 3;
+  const int g = 2 * (a & 1) + h;
+  return 128 * g + 32 * q + 16 * (a >> 1) + j;
+}
+__host__ __device__ inline long long aq_kpad(int K) { return ((long long)K + kChunk - 1) / kChunk * kChunk; }
+__host__ __device__ inline long long aq_scale_row_bytes(int K) { return aq_kpad(K) / kGroup * 2; }
+MX_DEV long long aq_scale_off(int row, int K, int blk, int plane)
+{
+  return (long long)row * aq_scale_row_bytes(K) + (blk >> 2) * 8 + plane * 4 + (blk & 3);
+}
+
+// ------------------------------------------------------------------ small helpers
+MX_DEV float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
+MX_DEV uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+// max over the 16 lanes of a lane group (lanes 16n..16n+15)
+MX_DEV float group16_max(float v)
+{
+  v = fmaxf(v, __shfl_xor(v, 1, 64));
+  v = fmaxf(v, __shfl_xor(v, 2, 64));
+  v = fmaxf(v, __shfl_xor(v, 4, 64));
+  v = fmaxf(v, __shfl_xor(v, 8, 64));
+  return v;
+}
+MX_DEV float group16_sum(float v)
+{
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  v += __shfl_xor(v, 8, 64);
+  return v;
+}
+
+// Two-term e4m3 quantisation of one 32-element block held 2 values per lane over 16
+// consecutive lanes. hi uses scale 2^(s_hi-127) chosen from the block maximum so that
+// |x / scale| < 256 (e4m3 max is 448); lo quantises the exact residual the same way.
+// Returns bytes (hi0 | hi1 << 8) and (lo0 | lo1 << 8) and the two scale bytes.
+struct Quant2 {
+  uint32_t hi, lo;
+  uint32_t s_hi, s_lo;
+};
+MX_DEV Quant2 quant2_block16(float v0, float v1)
+{
+  Quant2 r;
+  const float amax = group16_max(fmaxf(fabsf(v0), fabsf(v1)));
+  const int eb = (int)((f_bits(amax) >> 23) & 0xFF);
+  const int sb = eb > 7 ? eb - 7 : 0;
+  const float inv = bits_f((uint32_t)(254 - sb) << 23);       // 2^(127 - sb)
+  const float y0 = v0 * inv, y1 = v1 * inv;
+  const uint32_t q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false) & 0xFFFFu;
+  const float d0 = y0 - __builtin_amdgcn_cvt_f32_fp8((int)q, 0);
+  const float d1 = y1 - __builtin_amdgcn_cvt_f32_fp8((int)q, 1);
+  const float dmax = group16_max(fmaxf(fabsf(d0), fabsf(d1)));
+  const int ed = (int)((f_bits(dmax) >> 23) & 0xFF);
+  uint32_t ql = 0;
+  int sl = 127;
+  if (ed >= 27) {  // residual above 2^-100 of the hi scale: worth a second term
+    const int t = sb + ed - 134;
+    sl = t > 0 ? t : 0;
+    const float m = bits_f((uint32_t)(127 + sb - sl) << 23);  // 2^(sb - sl)
+    ql = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(d0 * m, d1 * m, 0, false) & 0xFFFFu;
+  }
+  r.hi = q;
+  r.lo = ql;
+  r.s_hi = (uint32_t)sb;
+  r.s_lo = (uint32_t)sl;
+  return r;
+}
+
+// True when any of the 4 scale bytes of w is >= 253.
+MX_DEV bool any_damaged_scale(uint32_t w)
+{
+  return ((w & 0xFFu) >= 253u) | (((w >> 8) & 0xFFu) >= 253u) | (((w >> 16) & 0xFFu) >= 253u) |
+         ((w >> 24) >= 253u);
+}
+
+// Scaled MFMA, A = e4m3 (format 0), B = fp4 (format 4). QA / QB pick the scale bytes.
+template <int QA, int QB>
+MX_DEV f32x4 mfma_f8f4(const i32x8& a, const i32x4& b, f32x4 c, int sa, int sb)
+{
+  const i32x8 b8 = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b8, c, 0, 4, QA, sa, QB, sb);
+}
+
+MX_DEV f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, f32x4 c)
+{
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+MX_DEV i32x4 ldg16(const void* p) { return *reinterpret_cast<const i32x4*>(p); }
+MX_DEV i32x8 ldg32(const void* p)
+{
+  const i32x4 a = reinterpret_cast<const i32x4*>(p)[0];
+  const i32x4 b = reinterpret_cast<const i32x4*>(p)[1];
+  return i32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// bf16 helpers (round to nearest even, as v_cvt_pk_bf16_f32 does)
+MX_DEV uint32_t pack_bf16(float a, float b)
+{
+  const __bf16 x = (__bf16)a, y = (__bf16)b;
+  return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+}
+MX_DEV float bf16_lo(uint32_t u) { return bits_f(u << 16); }
+MX_DEV float bf16_hi(uint32_t u) { return bits_f(u & 0xFFFF0000u); }
+
+// ------------------------------------------------------------------ GLU epilogues
+// kind 0: SwiGLU  silu(g) * u
+// kind 1: SiTU-GLU  4 tanh(g/4) sigmoid(g) * 25 tanh(u/25)  (lazy_lora/core/situ_activation.py:47-75)
+constexpr float kSituBeta = 4.0f;
+constexpr float kSituLinearBeta = 25.0f;
+
+MX_DEV float sigmoid_f(float v) { return 1.0f / (1.0f + __expf(-v)); }
+MX_DEV float tanh_f(float v) { return tanhf(v); }
+
+MX_DEV float glu_fwd(float g, float u, int kind)
+{
+  const float s = sigmoid_f(g);
+  if (kind == 0) return g * s * u;
+  return kSituBeta * tanh_f(g / kSituBeta) * s * (kSituLinearBeta * tanh_f(u / kSituLinearBeta));
+}
+
+// (d gate, d up) for upstream grad go (situ_activation.py:78-134 for kind 1)
+MX_DEV void glu_bwd(float go, float g, float u, int kind, float& dg, float& du)
+{
+  const float s = sigmoid_f(g);
+  if (kind == 0) {
+    dg = go * u * (s * (1.0f + g * (1.0f - s)));
+    du = go * g * s;
+    return;
+  }
+  const float t = tanh_f(g / kSituBeta);
+  const float a = kSituBeta * t * s;
+  const float da = (1.0f - t * t) * s + kSituBeta * t * s * (1.0f - s);
+  const float tu = tanh_f(u / kSituLinearBeta);
+  dg = go * (kSituLinearBeta * tu) * da;
+  du = go * a * (1.0f - tu * tu);
+}
+
+}  // namespace mx

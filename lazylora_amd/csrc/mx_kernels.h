@@ -1,0 +1,105 @@
+// Kernel argument blocks and launch helpers shared by the .hip translation units.
+// Host-visible; no torch types.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mx {
+
+// ---------------------------------------------------------------- forward products
+enum FwdMode : int {
+  kFwdPlain = 0,   // y[row, n] = A[row] . W[n]
+  kFwdGateUp = 1,  // act = GLU(A . W1^T, A . W3^T) -> two-term e4m3 act (+ optional fp32 gate|up)
+  kFwdDown = 2,    // y_pair[p, n] = tw[p] * (act[p] . W2[n])
+};
+
+struct FwdArgs {
+  const uint8_t* wp0;  // packed W (or W1 for kFwdGateUp), expert-major
+  const uint8_t* ws0;
+  const uint8_t* wp1;  // W3 for kFwdGateUp
+  const uint8_t* ws1;
+  long long wp_estride;  // bytes between experts in wp*
+  long long ws_estride;  // bytes between experts in ws*
+  int R, K;              // each W is [R, K]
+  // A operand in the two-term e4m3 layout, row length K
+  const uint8_t* a_hi;
+  const uint8_t* a_lo;
+  const uint8_t* a_sc;
+  const int* a_row_map;  // tile row -> A row; null = identity
+  // work: tiles[t] = {expert, first row, row count <= 16, 0}; null = dense, rows 16t.. of M
+  const int4* tiles;
+  const int* n_tiles;
+  int M;
+  int n_ct;  // column tiles per row tile
+  // outputs
+  float* y;
+  long long ldy;
+  const float* row_w;    // kFwdDown: combine weight per row
+  uint8_t* q_hi;         // kFwdGateUp: act in the two-term layout, row length R (= F)
+  uint8_t* q_lo;
+  uint8_t* q_sc;
+  float* save;           // kFwdGateUp: [rows, 2R] gate | up in fp32, or null
+  int act_kind;
+};
+
+// ---------------------------------------------------------------- transposed products
+enum BwdMode : int {
+  kBwdPlain = 0,   // y[row, c] (+)= sum_r A[row, r] W[r, c]
+  kBwdDownT = 1,   // h = g . W2 -> grad_w partials, GLU backward -> bf16 d_gate | d_up
+  kBwdGateUpT = 2, // y_pair[p, c] = [d_gate | d_up] . [W1 ; W3]
+};
+
+struct BwdArgs {
+  const uint8_t* wp0;
+  const uint8_t* ws0;
+  const uint8_t* wp1;  // second row segment (W3), or null
+  const uint8_t* ws1;
+  long long wp_estride;
+  long long ws_estride;
+  int nseg;      // 1 or 2 row segments
+  int R, C;      // each segment is [R, C]
+  const uint16_t* a_hi;  // bf16 [rows, lda], contraction index in [0, nseg*R), zero padded
+  const uint16_t* a_lo;
+  long long lda;
+  const int* a_row_map;
+  const int4* tiles;
+  const int* n_tiles;
+  int M;
+  int n_ct;  // column tiles of 256
+  float* y;
+  long long ldy;
+  int accumulate;
+  // kBwdDownT
+  const float* row_w;
+  const float* saved;  // [rows, 2C] gate | up
+  int act_kind;
+  uint16_t* d_hi;      // [rows, 2C]
+  uint16_t* d_lo;
+  float* gw_part;      // [rows, n_ct]
+};
+
+constexpr int kFwdRowsPerTile = 16;
+constexpr int kFwdColsPerTile = 64;  // kFwdPlain / kFwdDown; kFwdGateUp covers 32 features
+constexpr int kBwdColsPerTile = 256;
+
+hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s);
+hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
+
+// ---------------------------------------------------------------- elementwise / routing
+hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, uint8_t* hi,
+                             uint8_t* lo, uint8_t* sc, hipStream_t s);
+hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int Kpad, uint16_t* hi,
+                             uint16_t* lo, hipStream_t s);
+hipError_t launch_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R,
+                          hipStream_t s);
+hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, int N, int k, int E,
+                        int* counts, int* offsets, int* cursor, int4* tiles, int* meta, int* pair_token,
+                        float* pair_w, int* pair_of, hipStream_t s);
+hipError_t launch_combine(float* out, const float* ypair, long long ldy, const int* pair_of, int N, int k,
+                          int D, hipStream_t s);
+hipError_t launch_combine_bwd(float* grad_h, float* grad_w, const float* dxpair, long long ldy,
+                              const float* gw_part, int n_ct, const int* pair_of, int N, int k, int D,
+                              hipStream_t s);
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+
+}  // namespace mx

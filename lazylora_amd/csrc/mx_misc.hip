@@ -1,0 +1,318 @@
+// Elementwise, routing and combine kernels around the MXFP4 products.
+#include "mx_device.h"
+#include "mx_kernels.h"
+
+namespace mx {
+
+namespace {
+
+// ---------------------------------------------------------------- activation quantisation
+// One 16-lane group per 32-element block; writes the two-term AQ layout, zero padding to Kp.
+template <bool BF16>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const void* x, long long ldx, int rows, int K,
+                                                         uint8_t* hi, uint8_t* lo, uint8_t* sc)
+{
+  const long long kp = aq_kpad(K);
+  const int nbp = (int)(kp / kGroup);
+  const long long gid = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int l16 = threadIdx.x & 15;
+  const bool in_range = gid < (long long)rows * nbp;
+  const int row = in_range ? (int)(gid / nbp) : 0;
+  const int blk = in_range ? (int)(gid - (long long)row * nbp) : 0;
+  const int k = blk * kGroup + 2 * l16;
+  float v0 = 0.f, v1 = 0.f;
+  if (in_range && k < K) {
+    if (BF16) {
+      const uint32_t u = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + row * ldx + k);
+      v0 = bf16_lo(u);
+      v1 = bf16_hi(u);
+    } else {
+      const float2 f = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(x) + row * ldx + k);
+      v0 = f.x;
+      v1 = f.y;
+    }
+  }
+  const Quant2 q = quant2_block16(v0, v1);
+  if (!in_range) return;
+  const long long off = (long long)row * kp + (k >> 9) * kChunk + aq_pos(k & 511);
+  *reinterpret_cast<uint16_t*>(hi + off) = (uint16_t)q.hi;
+  *reinterpret_cast<uint16_t*>(lo + off) = (uint16_t)q.lo;
+  if (l16 == 0) {
+    sc[aq_scale_off(row, K, blk, 0)] = (uint8_t)q.s_hi;
+    sc[aq_scale_off(row, K, blk, 1)] = (uint8_t)q.s_lo;
+  }
+}
+
+// ---------------------------------------------------------------- fp32 -> bf16 hi + lo
+__global__ __launch_bounds__(256) void split_bf16_kernel(const float* x, long long ldx, int rows, int K,
+                                                         int Kpad, uint16_t* hi, uint16_t* lo)
+{
+  const long long idx = ((long long)blockIdx.x * 256 + threadIdx.x) * 2;
+  const long long total = (long long)rows * Kpad;
+  if (idx >= total) return;
+  const int row = (int)(idx / Kpad);
+  const int k = (int)(idx - (long long)row * Kpad);
+  float v0 = 0.f, v1 = 0.f;
+  if (k < K) v0 = x[row * ldx + k];
+  if (k + 1 < K) v1 = x[row * ldx + k + 1];
+  const uint32_t h = pack_bf16(v0, v1);
+  const uint32_t l = pack_bf16(v0 - bf16_lo(h), v1 - bf16_hi(h));
+  *reinterpret_cast<uint32_t*>(hi + idx) = h;
+  *reinterpret_cast<uint32_t*>(lo + idx) = l;
+}
+
+// ---------------------------------------------------------------- exact dequantisation
+// out[R, K] fp32 = decoded W (lazy_lora/native/mxfp4_gemm.c:142-150). The hardware fp4 -> bf16
+// conversion is exact for scale bytes 0..252 (bf16 widens to fp32 by a 16-bit shift); bytes
+// >= 253 give +-0 with the code's sign, as LUT[code] * 0.0f does.
+__global__ __launch_bounds__(256) void dequant_kernel(float* out, const uint8_t* packed, const uint8_t* scales,
+                                                      int K, int R)
+{
+  const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;  // one 32-element block
+  const int nb = K / kGroup;
+  if (blk >= (long long)R * nb) return;
+  const int r = (int)(blk / nb);
+  const int b = (int)(blk - (long long)r * nb);
+  const uint8_t* src = packed + (long long)r * (K / 2) + b * 16;
+  uint32_t words[4];
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    const i32x4 v = ldg16(src);
+    words[0] = (uint32_t)v[0]; words[1] = (uint32_t)v[1]; words[2] = (uint32_t)v[2]; words[3] = (uint32_t)v[3];
+  } else {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      words[d] = (uint32_t)src[4 * d] | ((uint32_t)src[4 * d + 1] << 8) | ((uint32_t)src[4 * d + 2] << 16) |
+                 ((uint32_t)src[4 * d + 3] << 24);
+  }
+  const uint32_t s = scales[(long long)r * nb + b];
+  float* dst = out + (long long)r * K + b * kGroup;
+  if (s >= 253u) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int n = 0; n < 8; ++n) dst[8 * d + n] = bits_f(((words[d] >> (4 * n)) & 8u) << 28);
+    return;
+  }
+  const float scale = bits_f(s << 23);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t p[4];
+    p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 0));
+    p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 1));
+    p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 2));
+    p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 3));
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      dst[8 * d + 2 * n] = bf16_lo(p[n]);
+      dst[8 * d + 2 * n + 1] = bf16_hi(p[n]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- routing
+// (token, slot) pairs are bucketed by expert: counts -> exclusive offsets -> placement.
+// The order of pairs inside a bucket is left to atomics; nothing downstream depends on it,
+// because every row of a product is computed independently and the combine gathers each
+// token's slots in slot order.
+__device__ __forceinline__ int read_idx(const void* idx, int idx64, long long p)
+{
+  return idx64 ? (int)reinterpret_cast<const long long*>(idx)[p] : reinterpret_cast<const int*>(idx)[p];
+}
+
+__global__ __launch_bounds__(256) void route_count_kernel(const void* idx, int idx64, int P, int E, int* counts,
+                                                          int* meta)
+{
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= P) return;
+  const long long raw = idx64 ? reinterpret_cast<const long long*>(idx)[p] : reinterpret_cast<const int*>(idx)[p];
+  if (raw < 0 || raw >= E) {
+    atomicOr(&meta[1], 1);
+    return;
+  }
+  atomicAdd(&counts[(int)raw], 1);
+}
+
+// Single work-group: exclusive scan of counts and of per-expert tile counts, tile list.
+__global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int E, int* offsets, int* cursor,
+                                                          int4* tiles, int* meta)
+{
+  __shared__ int s_rows[1024];
+  __shared__ int s_tiles[1024];
+  const int t = threadIdx.x;
+  const int per = (E + 1023) / 1024;
+  const int e0 = min(t * per, E), e1 = min(e0 + per, E);
+  int rows = 0, nt = 0;
+  for (int e = e0; e < e1; ++e) {
+    rows += counts[e];
+    nt += (counts[e] + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  }
+  s_rows[t] = rows;
+  s_tiles[t] = nt;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {  // Hillis-Steele inclusive scan
+    const int a = t >= d ? s_rows[t - d] : 0;
+    const int b = t >= d ? s_tiles[t - d] : 0;
+    __syncthreads();
+    s_rows[t] += a;
+    s_tiles[t] += b;
+    __syncthreads();
+  }
+  int row_off = s_rows[t] - rows, tile_off = s_tiles[t] - nt;
+  for (int e = e0; e < e1; ++e) {
+    const int c = counts[e];
+    offsets[e] = row_off;
+    cursor[e] = row_off;
+    for (int m = 0; m < c; m += kFwdRowsPerTile) tiles[tile_off++] = make_int4(e, row_off + m, min(kFwdRowsPerTile, c - m), 0);
+    row_off += c;
+  }
+  if (t == 1023) {
+    offsets[E] = s_rows[1023];
+    meta[0] = s_tiles[1023];
+  }
+}
+
+__global__ __launch_bounds__(256) void route_place_kernel(const void* idx, int idx64, const float* w, int P, int k,
+                                                          int E, int* cursor, int* pair_token, float* pair_w,
+                                                          int* pair_of)
+{
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= P) return;
+  const long long raw = idx64 ? reinterpret_cast<const long long*>(idx)[p] : reinterpret_cast<const int*>(idx)[p];
+  if (raw < 0 || raw >= E) {
+    pair_of[p] = -1;
+    return;
+  }
+  const int pos = atomicAdd(&cursor[(int)raw], 1);
+  pair_token[pos] = p / k;
+  pair_w[pos] = w[p];
+  pair_of[p] = pos;
+}
+
+// ---------------------------------------------------------------- combines
+// out[t, :] = sum over the token's slots, in slot order, of the pair rows (already weighted).
+__global__ __launch_bounds__(256) void combine_kernel(float* out, const float* ypair, long long ldy,
+                                                      const int* pair_of, int N, int k, int D)
+{
+  const int t = blockIdx.y;
+  const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (t >= N || d >= D) return;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s = 0; s < k; ++s) {
+    const int p = pair_of[t * k + s];
+    if (p < 0) continue;
+    const float4 v = *reinterpret_cast<const float4*>(ypair + (long long)p * ldy + d);
+    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  }
+  *reinterpret_cast<float4*>(out + (long long)t * D + d) = acc;
+}
+
+__global__ __launch_bounds__(256) void combine_bwd_kernel(float* grad_h, float* grad_w, const float* dxpair,
+                                                          long long ldy, const float* gw_part, int n_ct,
+                                                          const int* pair_of, int N, int k, int D)
+{
+  const int t = blockIdx.y;
+  const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (t >= N) return;
+  if (blockIdx.x == 0 && threadIdx.x < k) {
+    const int s = threadIdx.x;
+    const int p = pair_of[t * k + s];
+    float gsum = 0.f;
+    if (p >= 0)
+      for (int c = 0; c < n_ct; ++c) gsum += gw_part[(long long)p * n_ct + c];
+    grad_w[t * k + s] = gsum;
+  }
+  if (d >= D) return;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s = 0; s < k; ++s) {
+    const int p = pair_of[t * k + s];
+    if (p < 0) continue;
+    const float4 v = *reinterpret_cast<const float4*>(dxpair + (long long)p * ldy + d);
+    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  }
+  *reinterpret_cast<float4*>(grad_h + (long long)t * D + d) = acc;
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, long long n_words)
+{
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n_words; i += (long long)gridDim.x * 256) p[i] = 0u;
+}
+
+}  // namespace
+
+hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, uint8_t* hi, uint8_t* lo,
+                             uint8_t* sc, hipStream_t s)
+{
+  const long long groups = (long long)rows * (aq_kpad(K) / kGroup);
+  if (groups == 0) return hipSuccess;
+  dim3 grid((unsigned)((groups + 15) / 16)), block(256);
+  if (x_bf16) hipLaunchKernelGGL(quant_rows_kernel<true>, grid, block, 0, s, x, ldx, rows, K, hi, lo, sc);
+  else hipLaunchKernelGGL(quant_rows_kernel<false>, grid, block, 0, s, x, ldx, rows, K, hi, lo, sc);
+  return hipGetLastError();
+}
+
+hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int Kpad, uint16_t* hi, uint16_t* lo,
+                             hipStream_t s)
+{
+  const long long pairs = (long long)rows * Kpad / 2;
+  if (pairs == 0) return hipSuccess;
+  dim3 grid((unsigned)((pairs + 255) / 256)), block(256);
+  hipLaunchKernelGGL(split_bf16_kernel, grid, block, 0, s, x, ldx, rows, K, Kpad, hi, lo);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R, hipStream_t s)
+{
+  const long long blocks = (long long)R * (K / kGroup);
+  if (blocks == 0) return hipSuccess;
+  dim3 grid((unsigned)((blocks + 255) / 256)), block(256);
+  hipLaunchKernelGGL(dequant_kernel, grid, block, 0, s, out, packed, scales, K, R);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s)
+{
+  const long long words = (long long)(bytes / 4);
+  if (words == 0) return hipSuccess;
+  long long blocks = (words + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, reinterpret_cast<uint32_t*>(p), words);
+  return hipGetLastError();
+}
+
+hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, int N, int k, int E, int* counts,
+                        int* offsets, int* cursor, int4* tiles, int* meta, int* pair_token, float* pair_w,
+                        int* pair_of, hipStream_t s)
+{
+  const int P = N * k;
+  hipError_t e = launch_zero(counts, sizeof(int) * (size_t)E, s);
+  if (e != hipSuccess) return e;
+  e = launch_zero(meta, sizeof(int) * 4, s);
+  if (e != hipSuccess) return e;
+  if (P > 0) hipLaunchKernelGGL(route_count_kernel, dim3((P + 255) / 256), dim3(256), 0, s, topk_idx, idx64, P, E, counts, meta);
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, s, counts, E, offsets, cursor, tiles, meta);
+  if (P > 0)
+    hipLaunchKernelGGL(route_place_kernel, dim3((P + 255) / 256), dim3(256), 0, s, topk_idx, idx64, topk_w, P, k, E,
+                       cursor, pair_token, pair_w, pair_of);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(float* out, const float* ypair, long long ldy, const int* pair_of, int N, int k, int D,
+                          hipStream_t s)
+{
+  if (N == 0 || D == 0) return hipSuccess;
+  dim3 grid((unsigned)((D / 4 + 255) / 256), (unsigned)N), block(256);
+  hipLaunchKernelGGL(combine_kernel, grid, block, 0, s, out, ypair, ldy, pair_of, N, k, D);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine_bwd(float* grad_h, float* grad_w, const float* dxpair, long long ldy, const float* gw_part,
+                              int n_ct, const int* pair_of, int N, int k, int D, hipStream_t s)
+{
+  if (N == 0) return hipSuccess;
+  dim3 grid((unsigned)((D / 4 + 255) / 256 > 0 ? (D / 4 + 255) / 256 : 1), (unsigned)N), block(256);
+  hipLaunchKernelGGL(combine_bwd_kernel, grid, block, 0, s, grad_h, grad_w, dxpair, ldy, gw_part, n_ct, pair_of, N,
+                     k, D);
+  return hipGetLastError();
+}
+
+}  // namespace mx

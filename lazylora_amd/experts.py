@@ -1,0 +1,67 @@
+"""
+One routed-expert layer's packed MXFP4 weights, resident in HBM.
+
+The reference hands experts over one at a time as ExpertWeightBundle objects holding
+(w1|w3|w2).weight_packed / weight_scale tensors
+(lazy_lora/streaming/expert_streamer.py:27-50, :229-246). On MI355X a whole layer fits in HBM
+many times over (one layer of the BASELINE shape is 20.96 GB of 288 GB), so the layer is kept
+as six stacked, expert-major tensors and every routed-layer call reads experts by index:
+
+    w1p, w3p : [E, F, D/2] uint8    w1s, w3s : [E, F, D/32] uint8     (gate / up, W is [F, D])
+    w2p      : [E, D, F/2] uint8    w2s      : [E, D, F/32] uint8     (down, W is [D, F])
+
+Roles follow the reference: w1 = gate, w3 = up, w2 = down (expert_streamer.py:229-246).
+"""
+from typing import Iterable, Optional, Sequence
+
+import torch
+
+
+class ExpertLayer:
+    def __init__(self, w1p, w1s, w3p, w3s, w2p, w2s, device: Optional[torch.device] = None):
+        tensors = [w1p, w1s, w3p, w3s, w2p, w2s]
+        for t in tensors:
+            if t.dtype != torch.uint8:
+                raise ValueError(f"expert tensors must be uint8, got {t.dtype}")
+            if t.dim() != 3:
+                raise ValueError(f"expert tensors must be stacked [E, rows, cols], got {tuple(t.shape)}")
+        E, F, Dh = w1p.shape
+        D = Dh * 2
+        if D % 32 or F % 32:
+            raise ValueError(f"D={D} and F={F} must be multiples of 32")
+        want = {
+            "w1p": (E, F, D // 2), "w1s": (E, F, D // 32), "w3p": (E, F, D // 2), "w3s": (E, F, D // 32),
+            "w2p": (E, D, F // 2), "w2s": (E, D, F // 32),
+        }
+        for (name, shape), t in zip(want.items(), tensors):
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name} must be {shape}, got {tuple(t.shape)}")
+        if device is None:
+            device = w1p.device if w1p.is_cuda else torch.device("cuda", torch.cuda.current_device())
+        self.device = torch.device(device)
+        self.E, self.D, self.F = E, D, F
+        (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s) = [
+            t.to(self.device, non_blocking=True).contiguous() for t in tensors]
+
+    @classmethod
+    def from_bundles(cls, bundles: Sequence, device=None) -> "ExpertLayer":
+        """Stack per-expert bundles with gate/up/down_packed and _scale attributes."""
+        def stack(attr):
+            return torch.stack([getattr(b, attr) for b in bundles])
+        return cls(stack("gate_packed"), stack("gate_scale"), stack("up_packed"), stack("up_scale"),
+                   stack("down_packed"), stack("down_scale"), device=device)
+
+    def pointers(self):
+        return (self.w1p.data_ptr(), self.w1s.data_ptr(), self.w3p.data_ptr(), self.w3s.data_ptr(),
+                self.w2p.data_ptr(), self.w2s.data_ptr())
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() for t in (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s))
+
+    def expert_bytes(self) -> int:
+        """Packed bytes of one expert (all three matrices, codes + scales)."""
+        return self.nbytes // self.E
+
+    def tensors(self) -> Iterable[torch.Tensor]:
+        return (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s)

@@ -1,0 +1,282 @@
+"""
+MXFP4 expert kernels on MI355X, with the Python interface of lazy_lora/native/__init__.py.
+
+`kernel()` returns an `MXFP4Kernel` whose `gemm`, `gemm_t` and `dequant` take and return the
+same shapes as the reference's (lazy_lora/native/__init__.py:36-74); the arithmetic runs in
+hand-written gfx950 HIP kernels (liblazylora_mxfp4.so, C ABI in include/lazylora_mxfp4.h).
+`routed_forward` / `routed_backward` run a whole routed-expert layer in one call each.
+
+Differences from the reference, all deliberate:
+  * results are placed on the input's device; CPU inputs are copied to the GPU and the
+    result is copied back, so the unmodified CPU trainer also works;
+  * shape errors raise ValueError (the reference asserts), and K % 32 != 0 is rejected
+    (the reference floors K/32 and reads uninitialised memory);
+  * a missing or unloadable library raises RuntimeError instead of returning None: a
+    silent fallback would hide that the GPU path is not running. LAZYLORA_NO_NATIVE=1
+    still returns None, as the reference's opt-out does (native/__init__.py:79-80).
+"""
+import ctypes
+import os
+from typing import Optional, Tuple
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblazylora_mxfp4.so")
+
+ACT_SWIGLU = 0
+ACT_SITU = 1
+_ACTS = {"swiglu": ACT_SWIGLU, "situ": ACT_SITU, "situ_glu": ACT_SITU, ACT_SWIGLU: ACT_SWIGLU, ACT_SITU: ACT_SITU}
+
+F32, BF16, I32, I64 = 0, 1, 2, 3
+MOE_SAVE = 1
+MOE_REUSE_FORWARD = 2
+
+_lib = None
+_kernel = None
+
+
+def _load_library() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m lazylora_amd.build` "
+            "(or __graft_entry__.build()) before using the MI355X kernels")
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, ci, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    lib.mxfp4_last_error.restype = ctypes.c_char_p
+    lib.mxfp4_last_error.argtypes = []
+    lib.mxfp4_threads.restype = ci
+    lib.mxfp4_threads.argtypes = []
+    lib.mxfp4_dequant.restype = ci
+    lib.mxfp4_dequant.argtypes = [vp, vp, vp, ci, ci, vp]
+    lib.mxfp4_gemm_workspace_size.restype = sz
+    lib.mxfp4_gemm_workspace_size.argtypes = [ci, ci, ci]
+    lib.mxfp4_gemm.restype = ci
+    lib.mxfp4_gemm.argtypes = [vp, vp, vp, vp, ci, ci, ci, vp, sz, vp]
+    lib.mxfp4_gemm_t_workspace_size.restype = sz
+    lib.mxfp4_gemm_t_workspace_size.argtypes = [ci, ci, ci]
+    lib.mxfp4_gemm_t.restype = ci
+    lib.mxfp4_gemm_t.argtypes = [vp, vp, vp, vp, ci, ci, ci, vp, sz, vp]
+    lib.mxfp4_moe_workspace_size.restype = sz
+    lib.mxfp4_moe_workspace_size.argtypes = [ci, ci, ci, ci, ci]
+    lib.mxfp4_moe_forward.restype = ci
+    lib.mxfp4_moe_forward.argtypes = [vp, vp, ci, vp, ci, vp, ci, ci, vp, vp, vp, vp, vp, vp,
+                                      ci, ci, ci, ci, ci, vp, sz, vp]
+    lib.mxfp4_moe_backward.restype = ci
+    lib.mxfp4_moe_backward.argtypes = [vp, vp, vp, vp, ci, vp, ci, vp, ci, ci, vp, vp, vp, vp, vp, vp,
+                                       ci, ci, ci, ci, ci, vp, sz, vp]
+    lib.mxfp4_moe_route_status.restype = ci
+    lib.mxfp4_moe_route_status.argtypes = [vp, vp, vp]
+    _lib = lib
+    return lib
+
+
+def _check(rc: int, lib) -> None:
+    if rc != 0:
+        msg = lib.mxfp4_last_error().decode(errors="replace")
+        if rc == -1:
+            raise ValueError(msg)
+        raise RuntimeError(f"MXFP4 kernel failed ({rc}): {msg}")
+
+
+def _device_for(t: torch.Tensor) -> torch.device:
+    if t.is_cuda:
+        return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError("the MXFP4 kernels need a HIP device (torch.cuda.is_available() is False)")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _u8(t: torch.Tensor, dev: torch.device, name: str) -> torch.Tensor:
+    if t.dtype != torch.uint8:
+        raise ValueError(f"{name} must be uint8, got {t.dtype}")
+    t = t.to(dev, non_blocking=True).contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+class MXFP4Kernel:
+    """The reference's MXFP4Kernel (lazy_lora/native/__init__.py:19-74) on MI355X."""
+
+    def __init__(self, lib):
+        self.lib = lib
+
+    # -- single-expert products --------------------------------------------------------------
+    def gemm(self, x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+        """y[M, R] = x[M, K] @ W^T for packed W[R, K] (mxfp4_gemm.c:64-94). fp32 result."""
+        if x.dim() != 2:
+            raise ValueError(f"x must be 2-D [M, K], got {tuple(x.shape)}")
+        M, K = x.shape
+        R = packed.shape[0]
+        _check_weight(packed, scales, R, K)
+        dev = _device_for(x)
+        xd = x.to(dev, non_blocking=True).contiguous().float()
+        p, s = _u8(packed, dev, "packed"), _u8(scales, dev, "scales")
+        y = torch.empty((M, R), dtype=torch.float32, device=dev)
+        if M and R:
+            nws = self.lib.mxfp4_gemm_workspace_size(M, K, R)
+            ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+            _check(self.lib.mxfp4_gemm(y.data_ptr(), xd.data_ptr(), p.data_ptr(), s.data_ptr(), M, K, R,
+                                       ws.data_ptr(), nws, _stream(dev)), self.lib)
+        return y if x.is_cuda else y.cpu()
+
+    def gemm_t(self, dy: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+        """y[M, K] = dy[M, R] @ W for packed W[R, K] (mxfp4_gemm.c:96-129). fp32 result."""
+        if dy.dim() != 2:
+            raise ValueError(f"dy must be 2-D [M, R], got {tuple(dy.shape)}")
+        M, R = dy.shape
+        if packed.dim() != 2:
+            raise ValueError(f"packed must be 2-D [R, K/2], got {tuple(packed.shape)}")
+        K = packed.shape[1] * 2
+        if packed.shape[0] != R:
+            raise ValueError(f"dy has {R} columns but W has {packed.shape[0]} rows")
+        _check_weight(packed, scales, R, K)
+        dev = _device_for(dy)
+        dyd = dy.to(dev, non_blocking=True).contiguous().float()
+        p, s = _u8(packed, dev, "packed"), _u8(scales, dev, "scales")
+        y = torch.zeros((M, K), dtype=torch.float32, device=dev)
+        if M and R:
+            nws = self.lib.mxfp4_gemm_t_workspace_size(M, K, R)
+            ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+            _check(self.lib.mxfp4_gemm_t(y.data_ptr(), dyd.data_ptr(), p.data_ptr(), s.data_ptr(), M, K, R,
+                                         ws.data_ptr(), nws, _stream(dev)), self.lib)
+        return y if dy.is_cuda else y.cpu()
+
+    def dequant(self, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+        """W[R, K] fp32 from the packed bytes, bit-exact (mxfp4_gemm.c:142-150)."""
+        if packed.dim() != 2:
+            raise ValueError(f"packed must be 2-D [R, K/2], got {tuple(packed.shape)}")
+        R, K = packed.shape[0], packed.shape[1] * 2
+        _check_weight(packed, scales, R, K)
+        dev = _device_for(packed)
+        p, s = _u8(packed, dev, "packed"), _u8(scales, dev, "scales")
+        w = torch.empty((R, K), dtype=torch.float32, device=dev)
+        if R:
+            _check(self.lib.mxfp4_dequant(w.data_ptr(), p.data_ptr(), s.data_ptr(), K, R, _stream(dev)), self.lib)
+        return w if packed.is_cuda else w.cpu()
+
+    def threads(self) -> int:
+        """Parallel width of the device (compute units), the analogue of mxfp4_threads()."""
+        return int(self.lib.mxfp4_threads())
+
+    # -- routed layer ------------------------------------------------------------------------
+    def routed_forward(self, h: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                       experts, act="swiglu", save_for_backward: bool = False,
+                       workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """sum_e w_e(token) * expert_e(h) for one routed-expert layer; fp32 [N, D].
+
+        Mirrors LazyLoRATrainer._routed_experts_forward (lazy_lora/trainer/lazy_trainer.py:806-834)
+        with LoRA off. `experts` is an ExpertLayer (stacked packed weights in HBM).
+        """
+        call = _RoutedCall(self.lib, h, topk_indices, topk_weights, experts, act, workspace)
+        out = torch.empty((call.N, call.D), dtype=torch.float32, device=call.dev)
+        _check(self.lib.mxfp4_moe_forward(
+            out.data_ptr(), call.h.data_ptr(), call.h_dtype, call.idx.data_ptr(), call.idx_dtype,
+            call.w.data_ptr(), call.N, call.k, *experts.pointers(), experts.E, call.D, call.F, call.act,
+            MOE_SAVE if save_for_backward else 0, call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
+        return out
+
+    def routed_backward(self, h: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                        experts, grad_out: torch.Tensor, act="swiglu", reuse_forward: bool = False,
+                        workspace: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(dL/dh [N, D] fp32, dL/dtopk_weights [N, k] fp32) for upstream grad_out [N, D].
+
+        Mirrors _routed_experts_backward (lazy_trainer.py:836-880) with LoRA off. With
+        reuse_forward=True the workspace must come from a routed_forward(save_for_backward=True)
+        call on the same inputs; the routing and gate/up products are then not recomputed.
+        """
+        call = _RoutedCall(self.lib, h, topk_indices, topk_weights, experts, act, workspace)
+        if grad_out.shape != (call.N, call.D):
+            raise ValueError(f"grad_out must be [{call.N}, {call.D}], got {tuple(grad_out.shape)}")
+        g = grad_out.to(call.dev, non_blocking=True).contiguous().float()
+        grad_h = torch.empty((call.N, call.D), dtype=torch.float32, device=call.dev)
+        grad_w = torch.empty((call.N, call.k), dtype=torch.float32, device=call.dev)
+        _check(self.lib.mxfp4_moe_backward(
+            grad_h.data_ptr(), grad_w.data_ptr(), g.data_ptr(), call.h.data_ptr(), call.h_dtype,
+            call.idx.data_ptr(), call.idx_dtype, call.w.data_ptr(), call.N, call.k, *experts.pointers(),
+            experts.E, call.D, call.F, call.act, MOE_REUSE_FORWARD if reuse_forward else 0,
+            call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
+        return grad_h, grad_w
+
+    def moe_workspace_bytes(self, N: int, k: int, E: int, D: int, F: int) -> int:
+        return int(self.lib.mxfp4_moe_workspace_size(N, k, E, D, F))
+
+    def route_status(self, workspace: torch.Tensor) -> int:
+        """Routing flags left in a routed-layer workspace (bit 0: expert id out of range). Syncs."""
+        flags = ctypes.c_int(0)
+        _check(self.lib.mxfp4_moe_route_status(workspace.data_ptr(), ctypes.addressof(flags),
+                                               _stream(workspace.device)), self.lib)
+        return flags.value
+
+
+def _check_weight(packed: torch.Tensor, scales: torch.Tensor, R: int, K: int) -> None:
+    if packed.dim() != 2 or packed.shape[0] != R or packed.shape[1] * 2 != K:
+        raise ValueError(f"packed must be [{R}, {K // 2}], got {tuple(packed.shape)}")
+    if K % 32:
+        raise ValueError(f"K = {K} is not a multiple of the MX block size 32")
+    if tuple(scales.shape) != (R, K // 32):
+        raise ValueError(f"scales must be [{R}, {K // 32}], got {tuple(scales.shape)}")
+
+
+class _RoutedCall:
+    """Validated, device-resident arguments of one routed-layer call."""
+
+    def __init__(self, lib, h, topk_indices, topk_weights, experts, act, workspace):
+        if h.dim() != 2:
+            raise ValueError(f"h must be [N, D], got {tuple(h.shape)}")
+        self.N, self.D = h.shape
+        if self.D != experts.D:
+            raise ValueError(f"h has width {self.D} but the experts take {experts.D}")
+        if topk_indices.dim() != 2 or topk_indices.shape[0] != self.N:
+            raise ValueError(f"topk_indices must be [{self.N}, k], got {tuple(topk_indices.shape)}")
+        if tuple(topk_weights.shape) != tuple(topk_indices.shape):
+            raise ValueError("topk_weights and topk_indices must have the same shape")
+        if act not in _ACTS:
+            raise ValueError(f"unknown activation {act!r}")
+        self.k = topk_indices.shape[1]
+        self.F = experts.F
+        self.act = _ACTS[act]
+        self.dev = experts.device
+        if h.dtype == torch.bfloat16:
+            self.h_dtype = BF16
+        elif h.dtype == torch.float32:
+            self.h_dtype = F32
+        else:
+            raise ValueError(f"h must be float32 or bfloat16, got {h.dtype}")
+        self.h = h.to(self.dev, non_blocking=True).contiguous()
+        if topk_indices.dtype == torch.int64:
+            self.idx_dtype = I64
+        elif topk_indices.dtype == torch.int32:
+            self.idx_dtype = I32
+        else:
+            raise ValueError(f"topk_indices must be int32 or int64, got {topk_indices.dtype}")
+        if not topk_indices.is_cuda and topk_indices.numel():
+            lo, hi = int(topk_indices.min()), int(topk_indices.max())
+            if lo < 0 or hi >= experts.E:
+                raise ValueError(f"expert ids must lie in [0, {experts.E}), got [{lo}, {hi}]")
+        self.idx = topk_indices.to(self.dev, non_blocking=True).contiguous()
+        self.w = topk_weights.to(self.dev, non_blocking=True).contiguous().float()
+        self.nws = int(lib.mxfp4_moe_workspace_size(self.N, self.k, experts.E, self.D, self.F))
+        if workspace is None:
+            workspace = torch.empty(max(self.nws, 1), dtype=torch.uint8, device=self.dev)
+        elif workspace.numel() < self.nws or workspace.dtype != torch.uint8:
+            raise ValueError(f"workspace must be uint8 with at least {self.nws} bytes")
+        self.ws = workspace
+
+
+def kernel() -> Optional[MXFP4Kernel]:
+    """The MXFP4 kernel object, or None when LAZYLORA_NO_NATIVE=1 (native/__init__.py:77-97)."""
+    global _kernel
+    if os.environ.get("LAZYLORA_NO_NATIVE", "") == "1":
+        return None
+    if _kernel is None:
+        _kernel = MXFP4Kernel(_load_library())
+    return _kernel

@@ -1,0 +1,75 @@
+"""
+The routed-expert map of one MoE layer as a single autograd node, on MI355X.
+
+Mirrors RoutedExpertsFunction and the two expert sweeps of the reference trainer
+(lazy_lora/trainer/lazy_trainer.py:45-77, :806-880) with LoRA off: forward returns the fp32
+routed sum, backward returns (dL/dh_latent cast to h's dtype, dL/dtopk_weights). The expert
+loops run on the GPU in a few launches each (routing histogram/scan/placement, fused
+gate/up/GLU, down product with the combine weight, deterministic combine; and the three
+transposed products with the GLU derivative in backward).
+
+As in the reference, a `cached` routed sum short-circuits the forward (the backward replay,
+lazy_trainer.py:60-66); here the backward can additionally reuse the forward's gate/up
+activations when the same workspace is kept (save_for_backward=True), which removes the
+recompute of the gate/up products that the reference performs (:859).
+"""
+from typing import Optional
+
+import torch
+
+from lazylora_amd.experts import ExpertLayer
+from lazylora_amd.native import kernel
+
+
+def _native():
+    k = kernel()
+    if k is None:
+        raise RuntimeError("LAZYLORA_NO_NATIVE=1: the MI355X routed-expert path is disabled")
+    return k
+
+
+def routed_experts_forward(h_latent: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                           layer: ExpertLayer, act: str = "swiglu", save_for_backward: bool = False,
+                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sum_e w_e(token) * expert_e(h_latent) in fp32 (lazy_trainer.py:806-834)."""
+    return _native().routed_forward(h_latent, topk_indices, topk_weights, layer, act=act,
+                                    save_for_backward=save_for_backward, workspace=workspace)
+
+
+def routed_experts_backward(h_latent: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                            layer: ExpertLayer, grad_out: torch.Tensor, act: str = "swiglu",
+                            reuse_forward: bool = False, workspace: Optional[torch.Tensor] = None):
+    """(dL/dh_latent, dL/dtopk_weights) (lazy_trainer.py:836-880); grad_h in h's dtype."""
+    gh, gw = _native().routed_backward(h_latent, topk_indices, topk_weights, layer, grad_out, act=act,
+                                       reuse_forward=reuse_forward, workspace=workspace)
+    return gh.to(h_latent.dtype), gw.to(topk_weights.dtype)
+
+
+class RoutedExpertsFunction(torch.autograd.Function):
+    """autograd node: (h_latent, topk_weights, topk_indices, layer, act, cached) -> routed sum."""
+
+    @staticmethod
+    def forward(ctx, h_latent, topk_weights, topk_indices, layer, act="swiglu", cached=None):
+        k = _native()
+        ws = torch.empty(max(k.moe_workspace_bytes(h_latent.shape[0], topk_indices.shape[1], layer.E,
+                                                   layer.D, layer.F), 1),
+                         dtype=torch.uint8, device=layer.device)
+        if cached is not None:
+            out = cached.to(torch.float32)
+            reuse = False
+        else:
+            out = k.routed_forward(h_latent, topk_indices, topk_weights, layer, act=act,
+                                   save_for_backward=True, workspace=ws)
+            reuse = True
+        ctx.save_for_backward(h_latent, topk_weights, topk_indices)
+        ctx.layer, ctx.act, ctx.ws, ctx.reuse = layer, act, ws, reuse
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        h_latent, topk_weights, topk_indices = ctx.saved_tensors
+        grad_h, grad_w = routed_experts_backward(h_latent, topk_indices, topk_weights, ctx.layer,
+                                                 grad_out, act=ctx.act, reuse_forward=ctx.reuse,
+                                                 workspace=ctx.ws)
+        ctx.ws = None
+        return grad_h, grad_w, None, None, None, None

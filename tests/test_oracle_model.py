@@ -1,0 +1,149 @@
+"""Pins the oracle's GLUs, router and routed-layer composition against the reference's vendored
+fixtures (tests/golden/*.json, checked by the reference at 1e-5 abs + 1e-4 rel, and 2e-4 abs
+for the composite MoE block: lazy_lora/tests/test_reference_ops.py:52-53, :309), against torch's
+own SiLU, and against central differences for every backward."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def load(name):
+    with open(os.path.join(GOLDEN, f"{name}.json")) as f:
+        return json.load(f)
+
+
+def arr(entry):
+    return np.asarray(entry["data"], np.float64).reshape(entry["shape"])
+
+
+def assert_matches(got, want, abs_tol=1e-5, rel_tol=1e-4):
+    got, want = np.asarray(got, np.float64).ravel(), np.asarray(want, np.float64).ravel()
+    assert got.shape == want.shape
+    diff = np.abs(got - want)
+    assert np.all(diff <= abs_tol + rel_tol * np.abs(want)), f"max abs diff {diff.max():.3e}"
+
+
+def test_situ_glu_fixture():
+    fx = load("situ_glu")
+    x = arr(fx["in"])
+    d = x.shape[-1] // 2
+    assert fx["beta"] == oracle.SITU_BETA and fx["linear_beta"] == oracle.SITU_LINEAR_BETA
+    assert_matches(oracle.glu_forward(x[..., :d], x[..., d:], "situ"), arr(fx["out"]))
+
+
+def test_swiglu_matches_torch_silu():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(0)
+    g, u = rng.standard_normal((2, 64, 32)) * 4
+    want = (torch.nn.functional.silu(torch.from_numpy(g)) * torch.from_numpy(u)).numpy()
+    assert np.allclose(oracle.glu_forward(g, u, "swiglu"), want, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("act", ["swiglu", "situ"])
+def test_glu_backward_central_differences(act):
+    rng = np.random.default_rng(1)
+    g, u, go = rng.standard_normal((3, 200)) * 3
+    dg, du = oracle.glu_backward(go, g, u, act)
+    eps = 1e-6
+    fd_g = (oracle.glu_forward(g + eps, u, act) - oracle.glu_forward(g - eps, u, act)) / (2 * eps) * go
+    fd_u = (oracle.glu_forward(g, u + eps, act) - oracle.glu_forward(g, u - eps, act)) / (2 * eps) * go
+    assert np.allclose(dg, fd_g, rtol=1e-6, atol=1e-8)
+    assert np.allclose(du, fd_u, rtol=1e-6, atol=1e-8)
+
+
+def test_router_fixture():
+    fx = load("router")
+    idx, w = oracle.router_forward(arr(fx["in"]), arr(fx["gate_weight"]), arr(fx["bias"]), top_k=fx["top_k"])
+    want_idx = arr(fx["topk_idx"]).astype(np.int64)
+    want_w = arr(fx["topk_weight"])
+    got = {(r, int(i)): float(v) for r, (ii, ww) in enumerate(zip(idx, w)) for i, v in zip(ii, ww)}
+    want = {(r, int(i)): float(v) for r, (ii, ww) in enumerate(zip(want_idx, want_w)) for i, v in zip(ii, ww)}
+    assert sorted(got) == sorted(want)
+    assert_matches([got[k] for k in sorted(got)], [want[k] for k in sorted(want)])
+    # the fixture is built so that the selection bias changes the choice in some rows
+    plain, _ = oracle.router_forward(arr(fx["in"]), arr(fx["gate_weight"]), None, top_k=fx["top_k"])
+    changed = sum(set(a) != set(b) for a, b in zip(plain.tolist(), idx.tolist()))
+    assert changed == fx["rows_where_bias_changed_selection"]
+
+
+def test_moe_block_fixture():
+    """The latent MoE block of moe.json through the oracle's routed composition with the
+    fixture's dense expert weights (they are not MXFP4-representable)."""
+    fx = load("moe")
+    x = arr(fx["in"])
+    hidden = fx["hidden"]
+    s_act = oracle.glu_forward(x @ arr(fx["shared_w1_weight"]).T, x @ arr(fx["shared_w3_weight"]).T, "situ")
+    shared = s_act @ arr(fx["shared_w2_weight"]).T
+    idx, w = oracle.router_forward(x, arr(fx["gate_weight"]), arr(fx["e_score_correction_bias"]),
+                                   top_k=fx["top_k"], routed_scaling_factor=fx["routed_scale"])
+    flat = x.reshape(-1, hidden)
+    h_lat = flat @ arr(fx["down_weight"]).T
+
+    def dense(e):
+        return tuple(arr(fx[f"experts_{e}_{m}_weight"]) for m in ("w1", "w3", "w2"))
+
+    routed = oracle.routed_forward(h_lat, idx, w, None, act="situ", dense=dense)
+    if fx["latent_norm"]:
+        routed = oracle.rms_norm(routed, arr(fx["norm_weight"]), eps=fx["rms_eps"])
+    got = shared + (routed @ arr(fx["up_weight"]).T).reshape(shared.shape)
+    assert_matches(got, arr(fx["out"]), abs_tol=2e-4)
+
+
+@pytest.mark.parametrize("act", ["swiglu", "situ"])
+def test_routed_backward_central_differences(act):
+    rng = np.random.default_rng(2)
+    ex = oracle.random_experts(rng, 4, 64, 32, 124, 128)
+    N, k = 6, 2
+    h = rng.standard_normal((N, 64))
+    idx, w = oracle.softmax_topk(rng.standard_normal((N, 4)), k)
+    w = w.astype(np.float64)
+    g = rng.standard_normal((N, 64))
+    gh, gw = oracle.routed_backward(h, idx, w, ex, g, act)
+
+    def loss(hh, ww):
+        return float((oracle.routed_forward(hh, idx, ww, ex, act) * g).sum())
+
+    eps = 1e-6
+    fd_h = np.zeros_like(h)
+    for i in range(N):
+        for j in range(0, 64, 7):
+            d = np.zeros_like(h)
+            d[i, j] = eps
+            fd_h[i, j] = (loss(h + d, w) - loss(h - d, w)) / (2 * eps)
+    mask = np.zeros_like(h, bool)
+    mask[:, ::7] = True
+    assert np.allclose(gh[mask], fd_h[mask], rtol=1e-5, atol=1e-7)
+    fd_w = np.zeros_like(w)
+    for i in range(N):
+        for s in range(k):
+            d = np.zeros_like(w)
+            d[i, s] = eps
+            fd_w[i, s] = (loss(h, w + d) - loss(h, w - d)) / (2 * eps)
+    assert np.allclose(gw, fd_w, rtol=1e-5, atol=1e-7)
+
+
+def test_routed_invariants(clib):
+    rng = np.random.default_rng(3)
+    ex = oracle.random_experts(rng, 8, 256, 128, 119, 123)
+    N = 64
+    h = rng.standard_normal((N, 256)).astype(np.float32)
+    idx, w = oracle.softmax_topk(rng.standard_normal((N, 8)).astype(np.float32), 2)
+    a = clib.moe_forward(h, idx, w, ex)
+    # expert visiting order only changes fp32 rounding (the reference visits in disk order)
+    b = clib.moe_forward(h, idx, w, ex, order=np.unique(idx)[::-1])
+    assert oracle.rel_l2(a, b) < 1e-6
+    # float64 composition agrees
+    assert oracle.rel_l2(a, oracle.routed_forward(h, idx, w, ex)) < 1e-6
+    # experts nobody chose contribute nothing; a token's output is linear in its weights
+    assert np.allclose(clib.moe_forward(h, idx, 2 * w, ex), 2 * a, rtol=1e-6, atol=1e-6)
+    # C backward agrees with the float64 backward
+    g = rng.standard_normal((N, 256)).astype(np.float32)
+    gh, gw = clib.moe_backward(h, idx, w, ex, g)
+    gh64, gw64 = oracle.routed_backward(h, idx, w, ex, g)
+    assert oracle.rel_l2(gh, gh64) < 1e-6 and oracle.rel_l2(gw, gw64) < 1e-6
