@@ -1,0 +1,233 @@
+"""
+bench.py — routed-expert MXFP4 layer, forward + backward, on one MI355X.
+
+Workload ("config 4"): one MoE layer of 896 experts, each
+w1/w3 [2048, 7168] and w2 [7168, 2048] in MXFP4 (uniform e2m1 codes, E8M0 scales
+2^-10..2^-6), 1024 tokens of d_model 7168 (fp32 ~N(0,1)), router logits ~N(0,1) -> top-8 with
+renormalised softmax weights, upstream gradient ~N(0,1) fp32. One step = the routed forward
+(saving gate/up for the backward) + the manual backward (dX through the transposed experts,
+GLU derivative, routing-weight gradient). Weights and inputs are resident in HBM before the
+timed region starts; nothing is skipped inside it.
+
+Prints one JSON line. `value` is MoE-layer fwd+bwd tokens/s; `roofline` is the dominant
+kernel's algorithmic weight bytes per launch over its mean duration, measured with HIP events
+recorded by the library on the launch stream inside the timed region; `cpu_baseline` is this
+repo's C restatement of the reference CPU path timed on a bounded sample of the same layer.
+
+    python bench.py [--steps 20] [--warmup 3] [--routing uniform|zipf] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MXFP4 expert-GEMM HBM GB/s (% of peak); MoE-layer fwd+bwd tokens/s"
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+E, D, F, N, TOPK = 896, 7168, 2048, 1024, 8
+SCALE_LO, SCALE_HI = 117, 121  # E8M0 2^-10 .. 2^-6
+
+# algorithmic bytes of one matrix kind per expert: packed codes + E8M0 scales
+GATEUP_BYTES = 2 * (F * D // 2 + F * D // 32)  # w1 + w3: 15,597,568
+DOWN_BYTES = D * F // 2 + D * F // 32           # w2: 7,798,784
+EXPERT_BYTES = GATEUP_BYTES + DOWN_BYTES        # 23,396,352
+PHASE_BYTES = {"fwd_gateup": GATEUP_BYTES, "fwd_down": DOWN_BYTES,
+               "bwd_down_t": DOWN_BYTES, "bwd_gateup_t": GATEUP_BYTES}
+PHASE_KERNEL = {"fwd_gateup": "fwd_kernel<kFwdGateUp>", "fwd_down": "fwd_kernel<kFwdDown>",
+                "bwd_down_t": "bwd_kernel<kBwdDownT>", "bwd_gateup_t": "bwd_kernel<kBwdGateUpT>"}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_layer(seed: int):
+    from lazylora_amd.experts import ExpertLayer
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+
+    def codes(*shape):
+        return torch.randint(0, 256, shape, dtype=torch.uint8, device="cuda", generator=gen)
+
+    def scales(*shape):
+        return torch.randint(SCALE_LO, SCALE_HI + 1, shape, dtype=torch.uint8, device="cuda", generator=gen)
+
+    return ExpertLayer(codes(E, F, D // 2), scales(E, F, D // 32), codes(E, F, D // 2), scales(E, F, D // 32),
+                       codes(E, D, F // 2), scales(E, D, F // 32))
+
+
+def make_inputs(seed: int, routing: str):
+    rng = np.random.default_rng(seed)
+    h = rng.standard_normal((N, D), dtype=np.float32)
+    logits = rng.standard_normal((N, E), dtype=np.float32)
+    if routing == "zipf":  # per-expert offset -1.1 * ln(rank), rank a seeded permutation
+        logits += (-1.1 * np.log(rng.permutation(E) + 1)).astype(np.float32)[None, :]
+    g = rng.standard_normal((N, D), dtype=np.float32)
+    lt = torch.from_numpy(logits).cuda()
+    val, idx = torch.topk(lt, TOPK, dim=-1, sorted=True)
+    w = torch.softmax(val.double(), dim=-1).float()
+    return torch.from_numpy(h).cuda(), idx.contiguous(), w.contiguous(), torch.from_numpy(g).cuda()
+
+
+def cpu_baseline(layer, H, I, W, G, n_active, budget_s: float):
+    """This repo's C restatement of the reference path (oracle/mxfp4_oracle.c, bit-identical to
+    lazy_lora/native/mxfp4_gemm.c where that runs) on a sample of the layer's experts, each with
+    its full token bucket: forward sweep + backward sweep (which recomputes the forward, as the
+    reference does). Extrapolated to the whole layer."""
+    import oracle
+    lib = oracle.oracle_lib()
+    idx = I.cpu().numpy()
+    active = np.unique(idx)
+    h, w, g = H.cpu().numpy(), W.cpu().numpy(), G.cpu().numpy()
+
+    def run(ids):
+        sel = torch.from_numpy(ids).cuda()
+        ex = oracle.ExpertSet(*[t[sel].cpu().numpy() for t in layer.tensors()])
+        remap = np.full(E, -1, np.int64)
+        remap[ids] = np.arange(len(ids))
+        sidx = remap[idx]
+        t0 = time.perf_counter()
+        lib.moe_forward(h, sidx, w, ex, "swiglu", order=np.arange(len(ids)))
+        lib.moe_backward(h, sidx, w, ex, g, "swiglu", order=np.arange(len(ids)))
+        return time.perf_counter() - t0
+
+    rng = np.random.default_rng(7)
+    probe = rng.choice(active, size=2, replace=False)
+    t_probe = run(np.sort(probe)) / 2
+    n = int(min(max(budget_s / max(t_probe, 1e-6), 4), 96))
+    ids = np.sort(rng.choice(active, size=n, replace=False))
+    t = run(ids)
+    layer_s = t / n * n_active
+    return {"value": N / layer_s, "unit": "tokens/s", "cores": lib.threads(), "kind": "port",
+            "sample": (f"C restatement (oracle/mxfp4_oracle.c, -O3 -mavx2 -mfma -fopenmp) fwd+bwd of {n} of "
+                       f"{n_active} active experts with their full token buckets ({t:.1f} s), "
+                       f"extrapolated x{n_active / n:.1f} to the layer")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--routing", choices=["uniform", "zipf"], default="uniform")
+    ap.add_argument("--act", choices=["swiglu", "situ"], default="swiglu")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device copy (reference kernel for rocprof byte counters)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the routed-expert path is measured on one "
+                                   "MI355X (expert-parallel sharding is a design note, not implemented)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs the MI355X")
+
+    from lazylora_amd.native import kernel
+    k = kernel()
+    torch.cuda.set_device(0)
+    t_setup = time.time()
+    layer = make_layer(0)
+    H, I, W, G = make_inputs(1, args.routing)
+    n_active = int(torch.unique(I).numel())
+    ws = torch.empty(k.moe_workspace_bytes(N, TOPK, E, D, F), dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    log(f"[bench] layer {layer.nbytes / 1e9:.2f} GB in HBM, {n_active} active experts, setup {time.time() - t_setup:.1f}s")
+
+    def step():
+        k.routed_forward(H, I, W, layer, act=args.act, save_for_backward=True, workspace=ws)
+        return k.routed_backward(H, I, W, layer, G, act=args.act, reuse_forward=True, workspace=ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done")
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    k.set_timing(True)
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(end)
+    calls = k.phase_times()
+    k.set_timing(False)
+    ms_step = ms_total / args.steps
+    log(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step")
+
+    phase_ms = {}
+    for call in calls:
+        for name, ms in call:
+            phase_ms.setdefault(name, []).append(ms)
+    phase_avg = {n: float(np.mean(v)) for n, v in phase_ms.items()}
+    for n, v in sorted(phase_avg.items(), key=lambda kv: -kv[1]):
+        extra = ""
+        if n in PHASE_BYTES:
+            extra = f"  {PHASE_BYTES[n] * n_active / (v * 1e-3) / 1e9:8.1f} GB/s algorithmic"
+        log(f"[bench]   {n:14s} {v:8.3f} ms{extra}")
+
+    dom = max((n for n in phase_avg if n in PHASE_BYTES), key=lambda n: phase_avg[n])
+    dom_bytes = PHASE_BYTES[dom] * n_active
+    dom_gbs = dom_bytes / (phase_avg[dom] * 1e-3) / 1e9
+    step_bytes = 2 * EXPERT_BYTES * n_active  # one forward pass + one transposed pass over the weights
+    step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline (C restatement of the reference path) ...")
+        cpu = cpu_baseline(layer, H, I, W, G, n_active, args.cpu_seconds)
+        log(f"[bench] CPU baseline {cpu['value']:.2f} tokens/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": N / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4",
+        "data": "synthetic",
+        "config": {
+            "workload": "config 4: routed-expert MoE layer fwd+bwd, 896 experts (w1/w3 2048x7168, w2 7168x2048 "
+                        "MXFP4), 1024 tokens x 7168, top-8",
+            "routing": args.routing, "act": args.act, "active_experts": n_active,
+            "arithmetic": "MXFP4 weights x two-term e4m3 activations (fwd, fp4-native scaled MFMA) / exact bf16 "
+                          "decode x two-term bf16 gradients (bwd, bf16 MFMA), fp32 accumulate",
+            "weight_bytes_per_step": step_bytes,
+        },
+        "weight_GBps": step_gbs,
+        "weight_frac_of_hbm_peak": step_gbs / PEAK_HBM_GBS,
+        "phases_ms": {n: round(v, 4) for n, v in phase_avg.items()},
+        "roofline": {"bound": "hbm", "achieved": dom_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": dom_gbs / PEAK_HBM_GBS, "traffic": None, "kernel": PHASE_KERNEL[dom],
+                     "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_ms": phase_avg[dom]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

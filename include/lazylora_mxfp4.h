@@ -111,6 +111,17 @@ int mxfp4_moe_backward(float *grad_h, float *grad_w, const float *grad_out, cons
  * synchronising `stream`: bit 0 set = some topk_idx entry was outside [0, E). */
 int mxfp4_moe_route_status(const void *workspace, int *host_flags, hipStream_t stream);
 
+/* Phase timing of the routed-layer calls made on the calling thread, the counterpart of the
+ * reference's LAZYLORA_PROFILE timings (lazy_lora/trainer/lazy_trainer.py:192-194). While
+ * enabled, every mxfp4_moe_forward/backward call records HIP events on its stream around
+ * each phase (routing, quantisation, each product, combine) into a ring of 128 calls; nothing
+ * synchronises. mxfp4_moe_timing(1) also clears the ring. mxfp4_moe_phase_times waits for call
+ * number `call` (0-based since enabling) and writes up to max_phases elapsed times in ms and
+ * phase names (static strings); it returns the phase count or a negative MXFP4_E* code. */
+int mxfp4_moe_timing(int enable);
+int mxfp4_moe_timed_calls(void);
+int mxfp4_moe_phase_times(int call, float *ms, const char **names, int max_phases);
+
 #ifdef __cplusplus
 }
 #endif

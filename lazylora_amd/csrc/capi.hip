@@ -29,6 +29,57 @@ int hip_fail(hipError_t e, const char* where)
     if (e__ != hipSuccess) return hip_fail(e__, where); \
   } while (0)
 
+// Optional phase timing of the routed-layer calls (the analogue of the reference's
+// LAZYLORA_PROFILE per-phase timings, lazy_lora/trainer/lazy_trainer.py:192-194). While
+// enabled, each call records a HIP event on its stream before its first launch and after each
+// phase, into the next slot of a ring of kRing calls. Nothing synchronises until the times
+// are read, so timing can stay on inside a timed loop.
+struct PhaseTimer {
+  static constexpr int kRing = 128;
+  static constexpr int kMaxPhases = 12;
+  bool on = false;
+  int calls = 0;  // calls recorded since enabled
+  int cur = -1;   // ring slot of the call in progress
+  int n[kRing] = {};
+  const char* names[kRing][kMaxPhases] = {};
+  hipEvent_t ev[kRing][kMaxPhases + 1] = {};
+  bool created = false;
+
+  hipError_t enable(bool e)
+  {
+    on = e;
+    calls = 0;
+    cur = -1;
+    if (e && !created) {
+      for (int c = 0; c < kRing; ++c)
+        for (int p = 0; p <= kMaxPhases; ++p) {
+          hipError_t r = hipEventCreate(&ev[c][p]);
+          if (r != hipSuccess) return r;
+        }
+      created = true;
+    }
+    return hipSuccess;
+  }
+  hipError_t begin(hipStream_t s)
+  {
+    if (!on) return hipSuccess;
+    cur = calls % kRing;
+    ++calls;
+    n[cur] = 0;
+    return hipEventRecord(ev[cur][0], s);
+  }
+  hipError_t mark(const char* name, hipStream_t s)
+  {
+    if (!on || cur < 0 || n[cur] >= kMaxPhases) return hipSuccess;
+    names[cur][n[cur]] = name;
+    ++n[cur];
+    return hipEventRecord(ev[cur][n[cur]], s);
+  }
+};
+thread_local PhaseTimer g_timer;
+
+#define MX_PHASE(name, s) MX_TRY(g_timer.mark(name, s), "phase timer")
+
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
@@ -118,9 +169,11 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
                           at<int>(ws, L.cursor), at<int4>(ws, L.tiles), at<int>(ws, L.meta), at<int>(ws, L.pair_token),
                           at<float>(ws, L.pair_w), at<int>(ws, L.pair_of), s),
          "route");
+  MX_PHASE("route", s);
   MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, at<uint8_t>(ws, L.xq.hi), at<uint8_t>(ws, L.xq.lo),
                                at<uint8_t>(ws, L.xq.sc), s),
          "quantise h");
+  MX_PHASE("quant_h", s);
   if (F % mx::kChunk) {  // padding blocks of the act buffer are read by the down product
     MX_TRY(mx::launch_zero(at<void>(ws, L.actq.hi), L.actq.end - L.actq.hi, s), "zero act");
   }
@@ -138,6 +191,7 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   a.act_kind = act_kind;
   (void)P;
   MX_TRY(mx::launch_fwd(a, mx::kFwdGateUp, L.max_tiles, s), "gate/up product");
+  MX_PHASE("fwd_gateup", s);
   return MXFP4_OK;
 }
 
@@ -245,6 +299,7 @@ int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_i
   const MoeLayout L = moe_layout(N, k, E, D, F);
   if (!workspace || workspace_bytes < L.end) return fail(MXFP4_EWORKSPACE, "moe_forward: workspace too small%s");
   if (N == 0) return MXFP4_OK;
+  MX_TRY(g_timer.begin(stream), "phase timer");
   rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, (flags & MXFP4_MOE_SAVE) != 0,
                  workspace, L, stream);
   if (rc) return rc;
@@ -260,8 +315,10 @@ int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_i
   a.y = at<float>(workspace, L.ypair); a.ldy = D;
   a.row_w = at<float>(workspace, L.pair_w);
   MX_TRY(mx::launch_fwd(a, mx::kFwdDown, L.max_tiles, stream), "moe_forward: down product");
+  MX_PHASE("fwd_down", stream);
   MX_TRY(mx::launch_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D, stream),
          "moe_forward: combine");
+  MX_PHASE("fwd_combine", stream);
   return MXFP4_OK;
 }
 
@@ -278,6 +335,7 @@ int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, cons
   const MoeLayout L = moe_layout(N, k, E, D, F);
   if (!workspace || workspace_bytes < L.end) return fail(MXFP4_EWORKSPACE, "moe_backward: workspace too small%s");
   if (N == 0) return MXFP4_OK;
+  MX_TRY(g_timer.begin(stream), "phase timer");
   if (!(flags & MXFP4_MOE_REUSE_FORWARD)) {
     rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, true, workspace, L, stream);
     if (rc) return rc;
@@ -286,6 +344,7 @@ int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, cons
   MX_TRY(mx::launch_split_bf16(grad_out, D, N, D, D, at<uint16_t>(workspace, L.g_hi), at<uint16_t>(workspace, L.g_lo),
                                stream),
          "moe_backward: split grad_out");
+  MX_PHASE("split_grad", stream);
   mx::BwdArgs b = {};
   b.wp0 = w2p; b.ws0 = w2s;
   b.wp_estride = (long long)F * D / 2;
@@ -301,6 +360,7 @@ int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, cons
   b.d_hi = at<uint16_t>(workspace, L.d_hi); b.d_lo = at<uint16_t>(workspace, L.d_lo);
   b.gw_part = at<float>(workspace, L.gw_part);
   MX_TRY(mx::launch_bwd(b, mx::kBwdDownT, L.max_tiles, stream), "moe_backward: W2 transposed product");
+  MX_PHASE("bwd_down_t", stream);
 
   mx::BwdArgs c = {};
   c.wp0 = w1p; c.ws0 = w1s; c.wp1 = w3p; c.ws1 = w3s;
@@ -312,10 +372,36 @@ int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, cons
   c.n_ct = (D + mx::kBwdColsPerTile - 1) / mx::kBwdColsPerTile;
   c.y = at<float>(workspace, L.ypair); c.ldy = D;
   MX_TRY(mx::launch_bwd(c, mx::kBwdGateUpT, L.max_tiles, stream), "moe_backward: W1|W3 transposed product");
+  MX_PHASE("bwd_gateup_t", stream);
   MX_TRY(mx::launch_combine_bwd(grad_h, grad_w, at<float>(workspace, L.ypair), D, at<float>(workspace, L.gw_part),
                                 L.n_ct_bwd, at<int>(workspace, L.pair_of), N, k, D, stream),
          "moe_backward: combine");
+  MX_PHASE("bwd_combine", stream);
   return MXFP4_OK;
+}
+
+int mxfp4_moe_timing(int enable)
+{
+  MX_TRY(g_timer.enable(enable != 0), "moe_timing: create events");
+  return MXFP4_OK;
+}
+
+int mxfp4_moe_timed_calls(void) { return g_timer.calls; }
+
+int mxfp4_moe_phase_times(int call, float* ms, const char** names, int max_phases)
+{
+  if (call < 0 || call >= g_timer.calls || call < g_timer.calls - PhaseTimer::kRing)
+    return fail(MXFP4_EINVAL, "moe_phase_times: call not in the timing ring%s");
+  const int slot = call % PhaseTimer::kRing;
+  const int n = g_timer.n[slot];
+  if (n > 0) MX_TRY(hipEventSynchronize(g_timer.ev[slot][n]), "moe_phase_times: sync");
+  for (int p = 0; p < n && p < max_phases; ++p) {
+    float t = 0.f;
+    MX_TRY(hipEventElapsedTime(&t, g_timer.ev[slot][p], g_timer.ev[slot][p + 1]), "moe_phase_times: elapsed");
+    if (ms) ms[p] = t;
+    if (names) names[p] = g_timer.names[slot][p];
+  }
+  return n;
 }
 
 int mxfp4_moe_route_status(const void* workspace, int* host_flags, hipStream_t stream)

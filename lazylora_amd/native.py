@@ -70,6 +70,12 @@ def _load_library() -> ctypes.CDLL:
                                        ci, ci, ci, ci, ci, vp, sz, vp]
     lib.mxfp4_moe_route_status.restype = ci
     lib.mxfp4_moe_route_status.argtypes = [vp, vp, vp]
+    lib.mxfp4_moe_timing.restype = ci
+    lib.mxfp4_moe_timing.argtypes = [ci]
+    lib.mxfp4_moe_timed_calls.restype = ci
+    lib.mxfp4_moe_timed_calls.argtypes = []
+    lib.mxfp4_moe_phase_times.restype = ci
+    lib.mxfp4_moe_phase_times.argtypes = [ci, vp, vp, ci]
     _lib = lib
     return lib
 
@@ -208,6 +214,24 @@ class MXFP4Kernel:
 
     def moe_workspace_bytes(self, N: int, k: int, E: int, D: int, F: int) -> int:
         return int(self.lib.mxfp4_moe_workspace_size(N, k, E, D, F))
+
+    def set_timing(self, enable: bool) -> None:
+        """Record per-phase HIP events inside routed-layer calls on this thread (no syncs)."""
+        _check(self.lib.mxfp4_moe_timing(1 if enable else 0), self.lib)
+
+    def phase_times(self):
+        """[(phase name, ms), ...] for every call recorded since set_timing(True) (at most the
+        last 128 calls). Waits for those calls to finish."""
+        out = []
+        n_calls = int(self.lib.mxfp4_moe_timed_calls())
+        ms = (ctypes.c_float * 16)()
+        names = (ctypes.c_char_p * 16)()
+        for c in range(max(0, n_calls - 128), n_calls):
+            n = self.lib.mxfp4_moe_phase_times(c, ctypes.addressof(ms), ctypes.addressof(names), 16)
+            if n < 0:
+                _check(n, self.lib)
+            out.append([(names[i].decode(), float(ms[i])) for i in range(n)])
+        return out
 
     def route_status(self, workspace: torch.Tensor) -> int:
         """Routing flags left in a routed-layer workspace (bit 0: expert id out of range). Syncs."""
