@@ -85,20 +85,8 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Two-term activation buffer for [rows, K].
-struct AQ {
-  size_t hi, lo, sc, end;
-};
-AQ aq_layout(size_t base, long long rows, int K)
-{
-  const long long kp = mx::aq_kpad(K);
-  AQ a;
-  a.hi = base;
-  a.lo = align_up(a.hi + (size_t)(rows * kp));
-  a.sc = align_up(a.lo + (size_t)(rows * kp));
-  a.end = align_up(a.sc + (size_t)(rows * mx::aq_scale_row_bytes(K)));
-  return a;
-}
+// Bytes of the two-term activation operand (AT layout) for `tiles` work tiles of row length K.
+size_t at_bytes(long long tiles, int K) { return align_up((size_t)(tiles * mx::at_tile_bytes(K))); }
 
 long long pad32(long long v) { return (v + 31) / 32 * 32; }
 
@@ -106,7 +94,7 @@ long long pad32(long long v) { return (v + 31) / 32 * 32; }
 // what the forward left behind.
 struct MoeLayout {
   size_t meta, counts, offsets, cursor, tiles, pair_token, pair_w, pair_of;
-  AQ xq, actq;
+  size_t at_x, at_act;
   size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part, end;
   int max_tiles, n_ct_bwd;
 };
@@ -126,8 +114,8 @@ MoeLayout moe_layout(int N, int k, int E, int D, int F)
   L.pair_token = o; o = align_up(o + sizeof(int) * (size_t)P);
   L.pair_w = o; o = align_up(o + sizeof(float) * (size_t)P);
   L.pair_of = o; o = align_up(o + sizeof(int) * (size_t)P);
-  L.xq = aq_layout(o, N, D); o = L.xq.end;
-  L.actq = aq_layout(o, P, F); o = L.actq.end;
+  L.at_x = o; o += at_bytes(L.max_tiles, D);
+  L.at_act = o; o += at_bytes(L.max_tiles, F);
   L.saved = o; o = align_up(o + sizeof(float) * (size_t)(P * 2 * F));
   L.ypair = o; o = align_up(o + sizeof(float) * (size_t)(P * D));
   L.g_hi = o; o = align_up(o + 2 * (size_t)(N * (long long)D));
@@ -170,23 +158,22 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
                           at<float>(ws, L.pair_w), at<int>(ws, L.pair_of), s),
          "route");
   MX_PHASE("route", s);
-  MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, at<uint8_t>(ws, L.xq.hi), at<uint8_t>(ws, L.xq.lo),
-                               at<uint8_t>(ws, L.xq.sc), s),
+  MX_TRY(mx::launch_quant_tiles(h, h_dtype == MXFP4_BF16, D, N, D, at<int4>(ws, L.tiles), at<int>(ws, L.meta),
+                                L.max_tiles, at<int>(ws, L.pair_token), at<uint8_t>(ws, L.at_x), s),
          "quantise h");
   MX_PHASE("quant_h", s);
   if (F % mx::kChunk) {  // padding blocks of the act buffer are read by the down product
-    MX_TRY(mx::launch_zero(at<void>(ws, L.actq.hi), L.actq.end - L.actq.hi, s), "zero act");
+    MX_TRY(mx::launch_zero(at<void>(ws, L.at_act), at_bytes(L.max_tiles, F), s), "zero act");
   }
   mx::FwdArgs a = {};
   a.wp0 = wts[0]; a.ws0 = wts[1]; a.wp1 = wts[2]; a.ws1 = wts[3];
   a.wp_estride = (long long)F * D / 2;
   a.ws_estride = (long long)F * D / 32;
   a.R = F; a.K = D;
-  a.a_hi = at<uint8_t>(ws, L.xq.hi); a.a_lo = at<uint8_t>(ws, L.xq.lo); a.a_sc = at<uint8_t>(ws, L.xq.sc);
-  a.a_row_map = at<int>(ws, L.pair_token);
+  a.a_tiles = at<uint8_t>(ws, L.at_x);
   a.tiles = at<int4>(ws, L.tiles); a.n_tiles = at<int>(ws, L.meta);
   a.n_ct = F / 32;
-  a.q_hi = at<uint8_t>(ws, L.actq.hi); a.q_lo = at<uint8_t>(ws, L.actq.lo); a.q_sc = at<uint8_t>(ws, L.actq.sc);
+  a.q_tiles = at<uint8_t>(ws, L.at_act);
   a.save = save ? at<float>(ws, L.saved) : nullptr;
   a.act_kind = act_kind;
   (void)P;
@@ -221,7 +208,7 @@ size_t mxfp4_gemm_workspace_size(int M, int K, int R)
 {
   (void)R;
   if (M <= 0 || K <= 0) return 0;
-  return aq_layout(0, M, K).end;
+  return at_bytes((M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile, K);
 }
 
 int mxfp4_gemm(float* y, const float* x, const uint8_t* packed, const uint8_t* scales, int M, int K, int R,
@@ -232,19 +219,17 @@ int mxfp4_gemm(float* y, const float* x, const uint8_t* packed, const uint8_t* s
   if (!y || !x || !packed || !scales) return fail(MXFP4_EINVAL, "gemm: null pointer%s");
   if (!aligned16(packed)) return fail(MXFP4_EINVAL, "gemm: packed must be 16-byte aligned%s");
   if (((uintptr_t)x & 7) != 0) return fail(MXFP4_EINVAL, "gemm: x must be 8-byte aligned%s");
-  const AQ q = aq_layout(0, M, K);
-  if (!workspace || workspace_bytes < q.end) return fail(MXFP4_EWORKSPACE, "gemm: workspace too small%s");
-  MX_TRY(mx::launch_quant_rows(x, 0, K, M, K, at<uint8_t>(workspace, q.hi), at<uint8_t>(workspace, q.lo),
-                               at<uint8_t>(workspace, q.sc), stream),
+  const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
+  if (!workspace || workspace_bytes < at_bytes(tiles, K)) return fail(MXFP4_EWORKSPACE, "gemm: workspace too small%s");
+  MX_TRY(mx::launch_quant_tiles(x, 0, K, M, K, nullptr, nullptr, tiles, nullptr, at<uint8_t>(workspace, 0), stream),
          "gemm: quantise x");
   mx::FwdArgs a = {};
   a.wp0 = packed; a.ws0 = scales;
   a.R = R; a.K = K;
-  a.a_hi = at<uint8_t>(workspace, q.hi); a.a_lo = at<uint8_t>(workspace, q.lo); a.a_sc = at<uint8_t>(workspace, q.sc);
+  a.a_tiles = at<uint8_t>(workspace, 0);
   a.M = M;
   a.n_ct = (R + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
   a.y = y; a.ldy = R;
-  const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
   MX_TRY(mx::launch_fwd(a, mx::kFwdPlain, tiles, stream), "gemm: product");
   return MXFP4_OK;
 }
@@ -308,8 +293,7 @@ int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_i
   a.wp_estride = (long long)F * D / 2;
   a.ws_estride = (long long)F * D / 32;
   a.R = D; a.K = F;
-  a.a_hi = at<uint8_t>(workspace, L.actq.hi); a.a_lo = at<uint8_t>(workspace, L.actq.lo);
-  a.a_sc = at<uint8_t>(workspace, L.actq.sc);
+  a.a_tiles = at<uint8_t>(workspace, L.at_act);
   a.tiles = at<int4>(workspace, L.tiles); a.n_tiles = at<int>(workspace, L.meta);
   a.n_ct = (D + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
   a.y = at<float>(workspace, L.ypair); a.ldy = D;

@@ -5,7 +5,7 @@
 // Each step a work-group (256 threads) cooperatively loads a 32-row x 256-column slab of W
 // (every thread one 16-byte MX block = 32 columns of one row), decodes it with
 // v_cvt_scalef32_pk_bf16_fp4 (bit-exact: e2m1 * 2^(s-127) is exact in bf16), and writes it
-// row-major into LDS. Each wave then owns 64 output columns and pulls its B operands with
+// row-major (padded, see slab_off) into LDS. Each wave then owns 64 output columns and pulls its B operands with
 // ds_read_b64_tr_b16, which hands lane i of a 16-lane group column i of four consecutive
 // rows. A (activation gradients) is split into bf16 hi + lo terms, so the products carry
 // ~16 significant bits of the activation against the exact weights. The slab in LDS is
@@ -21,7 +21,19 @@ namespace mx {
 namespace {
 
 constexpr int kSlabRows = 32;
-constexpr int kSlabPitch = kBwdColsPerTile + 16;  // bf16 elements per LDS row (+32 B: spreads banks)
+// LDS slab layout (bytes): a 32-column block of a row takes 64 B + 16 B of padding, a row
+// 8 blocks + 32 B. With the 80 B block stride the 8 lanes of a ds_write_b128 phase (one row,
+// 8 blocks) land on 8 distinct bank groups; with the 672 B row pitch (168 dwords, = 8 banks
+// mod 32 and 40 mod 64) the 4 rows one 16-lane group reads with ds_read_b64_tr_b16 do too.
+constexpr int kBlockBytes = 80;
+constexpr int kRowBytes = 8 * kBlockBytes + 32;
+constexpr int kSlabBytes = kSlabRows * kRowBytes;
+
+__device__ __forceinline__ int slab_off(int row, int col)  // col in bf16 elements
+{
+  return row * kRowBytes + (col >> 5) * kBlockBytes + (col & 31) * 2;
+}
+constexpr int kPrefetch = 8;                      // weight slabs in flight per work-group (even)
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
@@ -53,7 +65,8 @@ __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tile
   return true;
 }
 
-// 16 fp4 bytes (32 codes of one row) -> 32 bf16 in 16 dwords, scale byte s applied exactly.
+// 16 fp4 bytes (32 codes of one row) -> 32 bf16 in 16 dwords, scale byte s applied exactly;
+// s >= 253 gives zeros.
 __device__ __forceinline__ void decode_block_bf16(const i32x4& raw, uint32_t s, uint32_t (&out)[16])
 {
   const bool dead = s >= 253u;
@@ -71,38 +84,44 @@ __device__ __forceinline__ void decode_block_bf16(const i32x4& raw, uint32_t s, 
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
 {
-  __shared__ __attribute__((aligned(16))) uint16_t slab[2][kSlabRows][kSlabPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t slab[2][kSlabBytes];
   __shared__ float dotred[4][16];
 
   WorkItem w;
   if (!decode_work(a.tiles, a.n_tiles, a.M, a.n_ct, w)) return;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, g = lane >> 4;
   const int c0 = w.ct * kBwdColsPerTile;
   const int rtot = a.nseg * a.R;
   const int nsteps = (rtot + kSlabRows - 1) / kSlabRows;
+  // the ring below is unrolled kPrefetch-fold; padding steps load nothing useful (zero weights)
+  const int nsteps_pad = (nsteps + kPrefetch - 1) / kPrefetch * kPrefetch;
 
   // loader role: one 16-byte MX block per thread per step
   const int lr = tid >> 3;         // slab row
   const int lc = tid & 7;          // 32-column block inside the tile
   const int lcol = c0 + lc * 32;
-  const bool lcol_ok = lcol < a.C;
+  const int lcol_c = lcol < a.C ? lcol : 0;
   const int cbs = a.C / kGroup;    // scale bytes per W row
   const long long wpitch = a.C / 2;
+  const long long wbase = (long long)w.expert * a.wp_estride + lcol_c / 2;
+  const long long sbase = (long long)w.expert * a.ws_estride + lcol_c / kGroup;
 
-  auto load_raw = [&](int step, i32x4& raw, uint32_t& sc) {
-    const int r = step * kSlabRows + lr;
-    raw = i32x4{0, 0, 0, 0};
-    sc = 127u;
-    if (lcol_ok && r < rtot) {
-      const int seg = r >= a.R ? 1 : 0;
-      const int rr = r - seg * a.R;
-      const uint8_t* P = seg ? a.wp1 : a.wp0;
-      const uint8_t* S = seg ? a.ws1 : a.ws0;
-      raw = ldg16(P + (long long)w.expert * a.wp_estride + (long long)rr * wpitch + lcol / 2);
-      sc = S[(long long)w.expert * a.ws_estride + (long long)rr * cbs + lcol / kGroup];
-    }
+  // Always issues the two loads, with row and column clamped into the matrix, so the wait
+  // counters stay exact and nothing touches the loaded data before its decode step. Clamped
+  // blocks are harmless: columns >= C are never stored, and rows >= nseg*R meet zero
+  // activations (zero padding of A, or the padding steps below). Rows >= R read the second
+  // segment (W3 after W1).
+  auto load_raw = [&](int step, i32x4& raw, uint8_t& sc) {
+    const int r = min(step * kSlabRows + lr, rtot - 1);
+    const bool seg = r >= a.R;
+    const int rr = seg ? r - a.R : r;
+    const uint8_t* P = seg ? a.wp1 : a.wp0;
+    const uint8_t* S = seg ? a.ws1 : a.ws0;
+    raw = ldg16(P + wbase + (long long)rr * wpitch);
+    sc = S[sbase + (long long)rr * cbs];
   };
 
   // A operand rows (rows past the tile end repeat the last row; never stored)
@@ -115,38 +134,63 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
 #pragma unroll
   for (int cg = 0; cg < 4; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  i32x4 raw;
-  uint32_t sc;
-  load_raw(0, raw, sc);
-  for (int s = 0; s < nsteps; ++s) {
-    const int buf = s & 1;
-    {
-      uint32_t dec[16];
-      decode_block_bf16(raw, sc, dec);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(&slab[buf][lr][lc * 32]);
+  // Pipeline: the raw blocks of the next kPrefetch steps are in flight in a register ring.
+  // Within a step the next step's A loads are issued before the ring refill, so waiting for
+  // A (vmcnt is an in-order counter) never waits for the far-ahead weight loads.
+  i32x4 ring[kPrefetch];
+  uint8_t rsc[kPrefetch];
+  // Issue order is pinned (A first, then the ring slot by slot) so the loop head can wait
+  // for slot 0 alone, whether it is entered from here or from the back edge.
+  i32x4 ahv = ldg16(pah), alv = ldg16(pal);
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<i32x4*>(dst + 4 * q) =
-            i32x4{(int)dec[4 * q], (int)dec[4 * q + 1], (int)dec[4 * q + 2], (int)dec[4 * q + 3]};
-    }
-    __syncthreads();
-    if (s + 1 < nsteps) load_raw(s + 1, raw, sc);
+  for (int p = 0; p < kPrefetch; ++p) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_raw(p, ring[p], rsc[p]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
-    const i32x4 ahv = ldg16(pah + s * kSlabRows);
-    const i32x4 alv = ldg16(pal + s * kSlabRows);
-    const bf16x8 ah = __builtin_bit_cast(bf16x8, ahv);
-    const bf16x8 al = __builtin_bit_cast(bf16x8, alv);
+  for (int s0 = 0; s0 < nsteps_pad; s0 += kPrefetch) {
 #pragma unroll
-    for (int cg = 0; cg < 4; ++cg) {
-      const int col = wave * 64 + cg * 16 + 4 * (li & 3);
-      const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_i16x4*)(&slab[buf][8 * g + (li >> 2)][col]));
-      const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_i16x4*)(&slab[buf][8 * g + 4 + (li >> 2)][col]));
-      const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
-      const bf16x8 b = __builtin_bit_cast(bf16x8, bs);
-      acc[cg] = mfma_bf16(ah, b, acc[cg]);
-      acc[cg] = mfma_bf16(al, b, acc[cg]);
+    for (int p = 0; p < kPrefetch; ++p) {
+      const int s = s0 + p;
+      const int buf = p & 1;  // kPrefetch is even, so this is s & 1
+      // keep later steps' use of the ring (and so their waits) below this point
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        uint32_t dec[16];
+        decode_block_bf16(ring[p], rsc[p], dec);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(&slab[buf][slab_off(lr, lc * 32)]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<i32x4*>(dst + 4 * q) =
+              i32x4{(int)dec[4 * q], (int)dec[4 * q + 1], (int)dec[4 * q + 2], (int)dec[4 * q + 3]};
+      }
+      __syncthreads();
+      const int sn = min(s + 1, nsteps - 1);
+      const i32x4 ahn = ldg16(pah + sn * kSlabRows);
+      const i32x4 aln = ldg16(pal + sn * kSlabRows);
+      __builtin_amdgcn_sched_barrier(0);
+      load_raw(s + kPrefetch, ring[p], rsc[p]);
+      __builtin_amdgcn_sched_barrier(0);
+
+      // padding steps (s >= nsteps) see clamped weights: zero their activations instead
+      const bool real = s < nsteps;
+      const bf16x8 ah = __builtin_bit_cast(bf16x8, real ? ahv : i32x4{0, 0, 0, 0});
+      const bf16x8 al = __builtin_bit_cast(bf16x8, real ? alv : i32x4{0, 0, 0, 0});
+#pragma unroll
+      for (int cg = 0; cg < 4; ++cg) {
+        const int col = wave * 64 + cg * 16 + 4 * (li & 3);
+        const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(&slab[buf][slab_off(8 * g + (li >> 2), col)]));
+        const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(&slab[buf][slab_off(8 * g + 4 + (li >> 2), col)]));
+        const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+        const bf16x8 b = __builtin_bit_cast(bf16x8, bs);
+        acc[cg] = mfma_bf16(ah, b, acc[cg]);
+        acc[cg] = mfma_bf16(al, b, acc[cg]);
+      }
+      ahv = ahn;
+      alv = aln;
     }
   }
 

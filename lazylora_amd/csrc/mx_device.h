@@ -6,7 +6,7 @@
 //    element, plus scales [R, K/32] E8M0 bytes. A scale byte >= 253 makes its 32-element
 //    group contribute zero (mxfp4_gemm.c:16-18).
 //  * Activations that feed the forward products are held as a two-term e4m3 split
-//    ("AQ" layout, see below): x ~= (hi + lo) with each term carrying its own E8M0 scale per
+//    ("AT" layout, see below): x ~= (hi + lo) with each term carrying its own E8M0 scale per
 //    32-element block. hi alone keeps 4 significant bits; hi + lo keeps ~8, which puts the
 //    rounding error of an activation below that of bf16.
 //  * The forward products run on v_mfma_scale_f32_16x16x128_f8f6f4 with A = e4m3 activations
@@ -38,27 +38,41 @@ constexpr int kGroup = 32;        // elements per MX block
 constexpr int kChunk = 512;       // K elements per "super-chunk" of the forward main loop
 constexpr int kChunkBlocks = 16;  // MX blocks per super-chunk
 
-// ------------------------------------------------------------------ AQ activation layout
-// An activation matrix [rows, K] is stored as
-//   hi, lo : [rows, Kp] bytes (e4m3), Kp = K rounded up to 512, zero beyond K
-//   sc     : [rows, Kp/32, 2] scale bytes, grouped as [row][blk/4][plane(hi,lo)][blk%4]
-// Inside each 512-element super-chunk the bytes are permuted so that the A operand of MFMA
-// q (q = 0..3) for lane group g is the 32 contiguous bytes at offset 128*g + 32*q. The
-// forward loop assigns actual block 16*c + 4*b + q to logical block b of MFMA q, so
-// lane g's B operands for q = 0..3 are 4 consecutive MX blocks of one weight row (64
-// contiguous bytes, scales in one dword), and its A operands are one 128-byte run.
-MX_DEV int aq_pos(int k_local)  // k_local in [0, 512): byte position inside the super-chunk
+// ------------------------------------------------------------------ AT activation layout
+// The A operand of the forward products is stored tile-major, in exactly the order the MFMA
+// lanes consume it, so every activation load instruction of a wave reads 1 KiB contiguous.
+// Rows are grouped in tiles of 16 (the work tiles of the product; unused slots hold zeros).
+// K is cut into super-chunks of 512 elements (16 MX blocks). The forward loop gives MFMA q
+// (q = 0..3) of super-chunk c the blocks 16c + 4b + q as its logical blocks b = 0..3, so a
+// weight lane's 4 operands are 4 consecutive MX blocks of one row.
+//
+// Per (tile, super-chunk) there are 16 KiB of codes and 512 B of scales:
+//   codes  [q 0..3][plane hi/lo][piece 0..1][lane 0..63][16 B]
+//   scales [lane 0..63][plane hi/lo][4 B: byte q = scale of block 16c + 4g + q]
+// Lane l = 16g + i serves row i of the tile. Its MFMA-q operand is piece 0 (logical K
+// [16g, 16g+16): block b = g/2, elements 16(g%2)..+16) then piece 1 (logical K [64+16g, ..):
+// block b = 2 + g/2). Its scale register holds the scale of logical block b = g.
+constexpr int kAtCodeBytes = 16384;
+constexpr int kAtChunkBytes = kAtCodeBytes + 512;
+
+__host__ __device__ inline int at_nchunks(int K) { return (K + kChunk - 1) / kChunk; }
+__host__ __device__ inline long long at_tile_bytes(int K) { return (long long)at_nchunks(K) * kAtChunkBytes; }
+
+// Byte offset, inside a tile, of elements e..e+1 (e even) of a row slot i and K index k,
+// for one plane; and of the scale byte of the 32-element block holding k.
+MX_DEV long long at_code_off(int i, int k, int plane)
 {
-  const int b = k_local >> 5, h = (k_local >> 4) & 1, j = k_local & 15;
-  const int a = b >> 2, q = b & 3;
-  const int g = 2 * (a & 1) + h;
-  return 128 * g + 32 * q + 16 * (a >> 1) + j;
+  const int c = k >> 9, b = (k >> 5) & 15, e = k & 31;
+  const int q = b & 3, gl = b >> 2;             // logical block of MFMA q
+  const int piece = gl >> 1;
+  const int g = 2 * (gl & 1) + (e >> 4);        // lane group holding these 16 elements
+  return (long long)c * kAtChunkBytes + ((q * 2 + plane) * 2 + piece) * 1024 + (16 * g + i) * 16 + (e & 15);
 }
-__host__ __device__ inline long long aq_kpad(int K) { return ((long long)K + kChunk - 1) / kChunk * kChunk; }
-__host__ __device__ inline long long aq_scale_row_bytes(int K) { return aq_kpad(K) / kGroup * 2; }
-MX_DEV long long aq_scale_off(int row, int K, int blk, int plane)
+MX_DEV long long at_scale_off(int i, int k, int plane)
 {
-  return (long long)row * aq_scale_row_bytes(K) + (blk >> 2) * 8 + plane * 4 + (blk & 3);
+  const int c = k >> 9, b = (k >> 5) & 15;
+  const int q = b & 3, g = b >> 2;
+  return (long long)c * kAtChunkBytes + kAtCodeBytes + (16 * g + i) * 8 + plane * 4 + q;
 }
 
 // ------------------------------------------------------------------ small helpers
@@ -140,12 +154,15 @@ MX_DEV f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, f32x4 c)
 }
 
 MX_DEV i32x4 ldg16(const void* p) { return *reinterpret_cast<const i32x4*>(p); }
-MX_DEV i32x8 ldg32(const void* p)
+
+// Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes from src land at
+// lds + 16 l. lds must be the same for the whole wave. Completion is counted by vmcnt.
+MX_DEV void dma16(const void* src, void* lds)
 {
-  const i32x4 a = reinterpret_cast<const i32x4*>(p)[0];
-  const i32x4 b = reinterpret_cast<const i32x4*>(p)[1];
-  return i32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
+MX_DEV void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+MX_DEV void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // bf16 helpers (round to nearest even, as v_cvt_pk_bf16_f32 does)
 MX_DEV uint32_t pack_bf16(float a, float b)

@@ -1,18 +1,28 @@
 // Forward MXFP4 products on the fp4-native scaled MFMA (gfx950).
 //
-// One work-group computes a 16-row x 64-column output tile (kFwdGateUp: 16 rows x 32 gate
-// features + the same 32 up features). Its four waves split the K dimension in super-chunks
-// of 512 elements and reduce through LDS at the end, so every weight byte is read once per
-// row tile and no wave waits on another inside the main loop.
+// Each wave computes one 16-row x 64-column output tile over the whole K range
+// (kFwdGateUp: 16 rows x 32 gate features + the same 32 up features). A work-group holds the
+// four waves of four neighbouring column tiles of the same row tile: they share the tile's
+// activations, which the work-group copies into LDS once per super-chunk. Every weight byte
+// is read once per row tile.
 //
-// Per super-chunk c and lane (j = lane % 16, g = lane / 16), for each of the 4 column groups:
+// Per super-chunk c (512 K elements) and lane (j = lane % 16, g = lane / 16), for each of the
+// 4 column groups of 16 weight rows:
 //   B: 64 contiguous bytes of weight row n = 4 MX blocks 16c+4g+q (q = 0..3), one dword of
 //      scales. MFMA q consumes block 16c+4g+q from lane group g, so op_sel q picks its scale.
-//   A: 128 contiguous bytes of the two-term activation row (hi, and again lo), arranged by
-//      the AQ layout so that bytes [32q, 32q+32) are exactly MFMA q's A operand.
+//   A: the two-term activations of the tile in the AT layout: for each (q, plane, piece) one
+//      contiguous KiB, and one 8-byte scale pair per lane.
 // Weights are consumed as stored: the MFMA applies the E8M0 scales and the e2m1 codes itself.
 // A scale byte >= 253 zeroes its block (lazy_lora/native/mxfp4_gemm.c:16-18) before it can
 // reach the MFMA, where 255 would be NaN and 253/254 would overflow.
+//
+// Fast path (K a multiple of 512), one step per super-chunk:
+//   wait for this step's data, barrier -> read A(c) and this chunk's weight scales from LDS
+//   -> request B(c+1) into the other register buffer and DMA A(c+1) into the other LDS
+//   buffer -> 32 MFMAs on chunk c while the requests are in flight.
+// Weight scales are staged per wave in LDS, 8 super-chunks (128 B of every row) at a time:
+// reading each chunk's 16 B straight from memory would fetch every 128 B scale line up to
+// 8 times, because the weight stream evicts it from L2 between chunks.
 #include "mx_device.h"
 #include "mx_kernels.h"
 
@@ -20,23 +30,40 @@ namespace mx {
 
 namespace {
 
+constexpr int kWavesPerGroup = 4;
+constexpr int kAtLdsBytes = kAtCodeBytes + 1024;   // one super-chunk of A; its scale DMA writes 1 KiB
+constexpr int kScaleWin = 8;                       // super-chunks per staged scale window
+constexpr int kScaleRowBytes = 16 * kScaleWin;     // 128 B of scales per weight row
+constexpr int kScaleWaveBytes = 64 * kScaleRowBytes;
+
+struct FwdLds {
+  uint8_t a[2][kAtLdsBytes];
+  uint8_t s[kWavesPerGroup][kScaleWaveBytes];
+};
+
 struct WorkItem {
-  int expert, row0, nrows, ct;
+  int tile, expert, row0, nrows, ct;
+  bool active;  // false: this wave's column tile is past the end; it only helps with the copies
 };
 
 // Work-groups are issued round-robin over the 8 XCDs (blockIdx % 8). Give each XCD one
-// contiguous run of work items so the tiles of one expert share that XCD's L2.
-__device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, int M, int n_ct,
+// contiguous run of work items so the tiles of one expert share that XCD's L2. Returns false
+// for the whole work-group at once.
+__device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, int M, int n_ct, int wave,
                                             WorkItem& w)
 {
   const int ntiles = tiles ? *n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
-  const int total = ntiles * n_ct;
+  const int n_cg = (n_ct + kWavesPerGroup - 1) / kWavesPerGroup;
+  const int total = ntiles * n_cg;
   const int per_xcd = (total + 7) >> 3;
   const int slot = (int)(blockIdx.x >> 3);
   const int item = (int)(blockIdx.x & 7) * per_xcd + slot;
   if (slot >= per_xcd || item >= total) return false;
-  const int t = item / n_ct;
-  w.ct = item - t * n_ct;
+  const int t = item / n_cg;
+  w.tile = t;
+  const int ct = (item - t * n_cg) * kWavesPerGroup + wave;
+  w.active = ct < n_ct;
+  w.ct = w.active ? ct : n_ct - 1;
   if (tiles) {
     const int4 tt = tiles[t];
     w.expert = tt.x;
@@ -62,72 +89,158 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[4], const i32x8& ah, cons
   }
 }
 
-template <int MODE, bool ALIGNED>
+// Zero every weight block whose scale byte is >= 253 and give it scale 2^0. Branch-free, so
+// the block (and the compiler's placement of loads and waits) stays in one piece.
+__device__ __forceinline__ void sanitize(i32x4 (&b)[4][4], uint32_t (&s)[4])
+{
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool dead = ((s[grp] >> (8 * q)) & 0xFFu) >= 253u;
+      b[grp][q] = dead ? i32x4{0, 0, 0, 0} : b[grp][q];
+      s[grp] = dead ? (s[grp] & ~(0xFFu << (8 * q))) | (127u << (8 * q)) : s[grp];
+    }
+}
+
+__device__ __forceinline__ i32x8 cat8(const i32x4& x, const i32x4& y)
+{
+  return i32x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+
+template <int MODE, bool FAST>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
 {
-  __shared__ float red[4][16][68];
-
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps control flow scalar
   WorkItem w;
-  if (!decode_work(a.tiles, a.n_tiles, a.M, a.n_ct, w)) return;
+  if (!decode_work(a.tiles, a.n_tiles, a.M, a.n_ct, wave, w)) return;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int nb = a.K / kGroup;
+  const int nsc = at_nchunks(a.K);
+  const uint8_t* const at_tile = a.a_tiles + (long long)w.tile * at_tile_bytes(a.K);
 
-  // A row held by this lane (rows past the tile end repeat the last row; never stored)
-  const int ri = w.row0 + min(j, w.nrows - 1);
-  const int arow = a.a_row_map ? a.a_row_map[ri] : ri;
-  const long long kp = aq_kpad(a.K);
-  const uint8_t* ahi = a.a_hi + (long long)arow * kp + g * 128;
-  const uint8_t* alo = a.a_lo + (long long)arow * kp + g * 128;
-  const uint8_t* asc = a.a_sc + (long long)arow * aq_scale_row_bytes(a.K) + g * 8;
+  // first weight row of column group grp, and that group's packed / scale bases
+  auto grp_row = [&](int grp) {
+    return MODE == kFwdGateUp ? w.ct * 32 + (grp & 1) * 16 : w.ct * kFwdColsPerTile + grp * 16;
+  };
+  auto grp_wp = [&](int grp) {
+    return (MODE == kFwdGateUp && grp >= 2 ? a.wp1 : a.wp0) + (long long)w.expert * a.wp_estride;
+  };
+  auto grp_ws = [&](int grp) {
+    return (MODE == kFwdGateUp && grp >= 2 ? a.ws1 : a.ws0) + (long long)w.expert * a.ws_estride;
+  };
 
-  const uint8_t* bp[4];
-  const uint8_t* bs[4];
+  // weight row n of group grp at wrow[grp] (uniform) + boff[grp] (this lane's 32-bit offset)
+  const uint8_t* wrow[4];
+  uint32_t boff[4];
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
-    const uint8_t* P = a.wp0;
-    const uint8_t* S = a.ws0;
-    int n;
-    if (MODE == kFwdGateUp) {
-      if (grp >= 2) {
-        P = a.wp1;
-        S = a.ws1;
-      }
-      n = w.ct * 32 + (grp & 1) * 16 + j;
-    } else {
-      n = w.ct * kFwdColsPerTile + grp * 16 + j;
-    }
-    n = min(n, a.R - 1);
-    bp[grp] = P + (long long)w.expert * a.wp_estride + (long long)n * (a.K / 2) + g * 64;
-    bs[grp] = S + (long long)w.expert * a.ws_estride + (long long)n * nb + g * 4;
+    const int rb = min(grp_row(grp), a.R - 1);  // rows past the end repeat the last row
+    wrow[grp] = grp_wp(grp) + (long long)rb * (a.K / 2);
+    boff[grp] = (uint32_t)(min(j, a.R - 1 - rb) * (a.K / 2) + g * 64);
   }
-
-  const int nsc = (nb + kChunkBlocks - 1) / kChunkBlocks;
-  const int c_begin = wave * nsc / 4, c_end = (wave + 1) * nsc / 4;
 
   f32x4 acc[4];
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) acc[grp] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int c = c_begin; c < c_end; ++c) {
-    i32x4 b[4][4];
-    uint32_t sb[4];
-    const bool full = ALIGNED && (c * kChunkBlocks + kChunkBlocks <= nb);
+  auto load_b = [&](int c, i32x4 (&b)[4][4]) {
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b[grp][q] = ldg16(wrow[grp] + c * 256 + boff[grp] + 16 * q);
+  };
+
+  if constexpr (FAST) {
+    __shared__ FwdLds lds;
+    uint8_t* const sw = lds.s[wave];
+
+    // A(c) -> lds.a[buf]: wave w copies KiB units 4w..4w+3 of the codes; wave 0 also copies
+    // the 512 B of scales (its upper 32 lanes repeat them into the spare half KiB)
+    auto issue_a = [&](int c, int buf) {
+      const uint8_t* src = at_tile + (long long)c * kAtChunkBytes;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int unit = 4 * wave + u;
+        dma16(src + unit * 1024 + lane * 16, &lds.a[buf][unit * 1024]);
+      }
+      if (wave == 0) dma16(src + kAtCodeBytes + (lane & 31) * 16, &lds.a[buf][kAtCodeBytes]);
+    };
+    // scale window win -> sw: instruction i covers rows 8i..8i+7 of this wave's 64, lane l
+    // copies 16 B (one super-chunk) of row 8i + l/8, chunk 8 win + l%8 (clamped to the row)
+    auto issue_scales = [&](int win) {
+      const int cc = min(win * kScaleWin + (lane & 7), nsc - 1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int grp = i >> 1;
+        const int n = min(grp_row(grp) + 8 * (i & 1) + (lane >> 3), a.R - 1);
+        dma16(grp_ws(grp) + (long long)n * nb + cc * 16, sw + i * 1024);
+      }
+    };
+    auto step = [&](int c, i32x4 (&cur)[4][4], i32x4 (&nxt)[4][4]) {
+      wait_vm0();
+      __syncthreads();
+      // everything this chunk needs from LDS, before any new copy into LDS is requested
+      uint32_t sb[4];
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp)
+        sb[grp] = *reinterpret_cast<const uint32_t*>(sw + (grp * 16 + j) * kScaleRowBytes + (c % kScaleWin) * 16 + g * 4);
+      const uint8_t* la = &lds.a[c & 1][lane * 16];
+      i32x8 ah[4], al[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        ah[q] = cat8(*reinterpret_cast<const i32x4*>(la + q * 4096), *reinterpret_cast<const i32x4*>(la + q * 4096 + 1024));
+        al[q] = cat8(*reinterpret_cast<const i32x4*>(la + q * 4096 + 2048), *reinterpret_cast<const i32x4*>(la + q * 4096 + 3072));
+      }
+      const uint2 s2 = *reinterpret_cast<const uint2*>(&lds.a[c & 1][kAtCodeBytes + lane * 8]);
+      wait_lgkm0();
+      __builtin_amdgcn_sched_barrier(0);
+      if (c + 1 < nsc) {
+        load_b(c + 1, nxt);
+        issue_a(c + 1, (c + 1) & 1);
+        if ((c + 1) % kScaleWin == 0) issue_scales((c + 1) / kScaleWin);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      sanitize(cur, sb);
+      mfma_step<0>(acc, ah[0], al[0], cur, sb, (int)s2.x, (int)s2.y);
+      mfma_step<1>(acc, ah[1], al[1], cur, sb, (int)s2.x, (int)s2.y);
+      mfma_step<2>(acc, ah[2], al[2], cur, sb, (int)s2.x, (int)s2.y);
+      mfma_step<3>(acc, ah[3], al[3], cur, sb, (int)s2.x, (int)s2.y);
+    };
+
+    i32x4 b0[4][4], b1[4][4];
+    issue_a(0, 0);
+    issue_scales(0);
+    load_b(0, b0);
+    for (int c = 0;;) {
+      step(c, b0, b1);
+      if (++c >= nsc) break;
+      step(c, b1, b0);
+      if (++c >= nsc) break;
+    }
+  } else {
+    // any K (a multiple of 32): straight loads, blocks past the end of the row load nothing
+    // and carry a zero operand with scale 2^0 (their activations are zero too)
+    const uint8_t* bs[4];
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
-      if (full) {
-        const uint8_t* p = bp[grp] + c * 256;
+      const int n = min(grp_row(grp) + j, a.R - 1);
+      bs[grp] = grp_ws(grp) + (long long)n * nb + g * 4;
+    }
+    const uint8_t* at = at_tile + lane * 16;
+    for (int c = 0; c < nsc; ++c) {
+      i32x4 b[4][4];
+      uint32_t sb[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b[grp][q] = ldg16(p + 16 * q);
-        sb[grp] = *reinterpret_cast<const uint32_t*>(bs[grp] + c * 16);
-      } else {
+      for (int grp = 0; grp < 4; ++grp) {
         sb[grp] = 0;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int blk = c * kChunkBlocks + g * 4 + q;
           if (blk < nb) {
-            b[grp][q] = ldg16(bp[grp] + c * 256 + 16 * q);
+            b[grp][q] = ldg16(wrow[grp] + c * 256 + boff[grp] + 16 * q);
             sb[grp] |= (uint32_t)bs[grp][c * 16 + q] << (8 * q);
           } else {
             b[grp][q] = i32x4{0, 0, 0, 0};
@@ -135,84 +248,70 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
           }
         }
       }
-      if (any_damaged_scale(sb[grp])) {
+      const uint8_t* p = at + (long long)c * kAtChunkBytes;
+      i32x8 ah[4], al[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (((sb[grp] >> (8 * q)) & 0xFFu) >= 253u) {
-            b[grp][q] = i32x4{0, 0, 0, 0};
-            sb[grp] = (sb[grp] & ~(0xFFu << (8 * q))) | (127u << (8 * q));
-          }
-        }
+      for (int q = 0; q < 4; ++q) {
+        ah[q] = cat8(ldg16(p + q * 4096), ldg16(p + q * 4096 + 1024));
+        al[q] = cat8(ldg16(p + q * 4096 + 2048), ldg16(p + q * 4096 + 3072));
       }
+      const uint2 s2 = *reinterpret_cast<const uint2*>(at_tile + (long long)c * kAtChunkBytes + kAtCodeBytes + lane * 8);
+      sanitize(b, sb);
+      mfma_step<0>(acc, ah[0], al[0], b, sb, (int)s2.x, (int)s2.y);
+      mfma_step<1>(acc, ah[1], al[1], b, sb, (int)s2.x, (int)s2.y);
+      mfma_step<2>(acc, ah[2], al[2], b, sb, (int)s2.x, (int)s2.y);
+      mfma_step<3>(acc, ah[3], al[3], b, sb, (int)s2.x, (int)s2.y);
     }
-    const uint8_t* ph = ahi + (long long)c * kChunk;
-    const uint8_t* pl = alo + (long long)c * kChunk;
-    const i32x8 ah0 = ldg32(ph), ah1 = ldg32(ph + 32), ah2 = ldg32(ph + 64), ah3 = ldg32(ph + 96);
-    const i32x8 al0 = ldg32(pl), al1 = ldg32(pl + 32), al2 = ldg32(pl + 64), al3 = ldg32(pl + 96);
-    const uint2 s2 = *reinterpret_cast<const uint2*>(asc + (long long)c * 32);
-    mfma_step<0>(acc, ah0, al0, b, sb, (int)s2.x, (int)s2.y);
-    mfma_step<1>(acc, ah1, al1, b, sb, (int)s2.x, (int)s2.y);
-    mfma_step<2>(acc, ah2, al2, b, sb, (int)s2.x, (int)s2.y);
-    mfma_step<3>(acc, ah3, al3, b, sb, (int)s2.x, (int)s2.y);
   }
 
-  // split-K reduction: lane (j, g) holds rows 4g..4g+3 of column grp*16 + j
-#pragma unroll
-  for (int grp = 0; grp < 4; ++grp)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) red[wave][4 * g + v][grp * 16 + j] = acc[grp][v];
-  __syncthreads();
+  if (!w.active) return;
 
-  const int i = tid >> 4;  // tile row handled in the epilogue
-  const bool row_ok = i < w.nrows;
-  const int row = w.row0 + (row_ok ? i : 0);
-
+  // epilogue, straight from the accumulators: lane (j, g) holds rows 4g+v (v = 0..3) of
+  // columns grp*16 + j
   if (MODE == kFwdGateUp) {
-    const int fj = (tid & 15) * 2;
-    const float g0 = red[0][i][fj] + red[1][i][fj] + red[2][i][fj] + red[3][i][fj];
-    const float g1 = red[0][i][fj + 1] + red[1][i][fj + 1] + red[2][i][fj + 1] + red[3][i][fj + 1];
-    const float u0 = red[0][i][32 + fj] + red[1][i][32 + fj] + red[2][i][32 + fj] + red[3][i][32 + fj];
-    const float u1 = red[0][i][33 + fj] + red[1][i][33 + fj] + red[2][i][33 + fj] + red[3][i][33 + fj];
-    const float a0 = glu_fwd(g0, u0, a.act_kind), a1 = glu_fwd(g1, u1, a.act_kind);
+    // rows 4g+v: gate features j and 16+j (groups 0, 1), up features the same (groups 2, 3)
     const int F = a.R;
-    const int f = w.ct * 32 + fj;
-    if (a.save && row_ok) {
-      float* sv = a.save + (long long)row * 2 * F;
-      *reinterpret_cast<float2*>(sv + f) = make_float2(g0, g1);
-      *reinterpret_cast<float2*>(sv + F + f) = make_float2(u0, u1);
-    }
-    const Quant2 qv = quant2_block16(a0, a1);  // all 16 lanes of the row take part
-    if (row_ok) {
-      const long long fp = aq_kpad(F);
-      const long long off = (long long)row * fp + (f >> 9) * kChunk + aq_pos(f & 511);
-      *reinterpret_cast<uint16_t*>(a.q_hi + off) = (uint16_t)qv.hi;
-      *reinterpret_cast<uint16_t*>(a.q_lo + off) = (uint16_t)qv.lo;
-      if ((tid & 15) == 0) {
-        a.q_sc[aq_scale_off(row, F, w.ct, 0)] = (uint8_t)qv.s_hi;
-        a.q_sc[aq_scale_off(row, F, w.ct, 1)] = (uint8_t)qv.s_lo;
+    const int f0 = w.ct * 32;
+    uint8_t* qt = a.q_tiles + (long long)w.tile * at_tile_bytes(F);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int i = 4 * g + v;
+      const float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
+      const float a0 = glu_fwd(ga, ua, a.act_kind), a1 = glu_fwd(gb, ub, a.act_kind);
+      if (a.save && i < w.nrows) {
+        float* sv = a.save + (long long)(w.row0 + i) * 2 * F;
+        sv[f0 + j] = ga;
+        sv[f0 + 16 + j] = gb;
+        sv[F + f0 + j] = ua;
+        sv[F + f0 + 16 + j] = ub;
+      }
+      // act -> the down product's A operand (AT layout, same tile). Unused row slots carry
+      // zeros (their inputs were zero), which is what the layout expects.
+      const Quant2 q = quant2_block16(a0, a1);  // the 16 lanes of row i hold its 32 features
+      qt[at_code_off(i, f0 + j, 0)] = (uint8_t)q.hi;
+      qt[at_code_off(i, f0 + 16 + j, 0)] = (uint8_t)(q.hi >> 8);
+      qt[at_code_off(i, f0 + j, 1)] = (uint8_t)q.lo;
+      qt[at_code_off(i, f0 + 16 + j, 1)] = (uint8_t)(q.lo >> 8);
+      if (j == 0) {
+        qt[at_scale_off(i, f0, 0)] = (uint8_t)q.s_hi;
+        qt[at_scale_off(i, f0, 1)] = (uint8_t)q.s_lo;
       }
     }
     return;
   }
 
-  const int cq = (tid & 15) * 4;
-  float v[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = red[0][i][cq + e] + red[1][i][cq + e] + red[2][i][cq + e] + red[3][i][cq + e];
-  if (!row_ok) return;
-  if (MODE == kFwdDown) {
-    const float tw = a.row_w[row];
+  for (int v = 0; v < 4; ++v) {
+    const int i = 4 * g + v;
+    if (i >= w.nrows) continue;
+    const int row = w.row0 + i;
+    const float tw = MODE == kFwdDown ? a.row_w[row] : 1.0f;
+    float* yr = a.y + (long long)row * a.ldy;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] *= tw;
-  }
-  const int col = w.ct * kFwdColsPerTile + cq;
-  float* yr = a.y + (long long)row * a.ldy;
-  if (col + 3 < a.R && ((a.ldy & 3) == 0)) {
-    *reinterpret_cast<float4*>(yr + col) = make_float4(v[0], v[1], v[2], v[3]);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (col + e < a.R) yr[col + e] = v[e];
+    for (int grp = 0; grp < 4; ++grp) {
+      const int col = w.ct * kFwdColsPerTile + grp * 16 + j;
+      if (col < a.R) yr[col] = acc[grp][v] * tw;
+    }
   }
 }
 
@@ -220,18 +319,19 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
 
 hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
 {
-  const long long total = (long long)max_tiles * a.n_ct;
+  const long long n_cg = (a.n_ct + kWavesPerGroup - 1) / kWavesPerGroup;
+  const long long total = (long long)max_tiles * n_cg;
   if (total <= 0) return hipSuccess;
   const long long blocks = (total + 7) / 8 * 8;
-  const bool aligned = (a.K % 128) == 0;
-  dim3 grid((unsigned)blocks), block(256);
-#define MX_LAUNCH(M, AL) hipLaunchKernelGGL((fwd_kernel<M, AL>), grid, block, 0, s, a)
+  const bool fast = (a.K % kChunk) == 0;
+  dim3 grid((unsigned)blocks), block(64 * kWavesPerGroup);
+#define MX_LAUNCH(M, F) hipLaunchKernelGGL((fwd_kernel<M, F>), grid, block, 0, s, a)
   if (mode == kFwdPlain) {
-    if (aligned) MX_LAUNCH(kFwdPlain, true); else MX_LAUNCH(kFwdPlain, false);
+    if (fast) MX_LAUNCH(kFwdPlain, true); else MX_LAUNCH(kFwdPlain, false);
   } else if (mode == kFwdGateUp) {
-    if (aligned) MX_LAUNCH(kFwdGateUp, true); else MX_LAUNCH(kFwdGateUp, false);
+    if (fast) MX_LAUNCH(kFwdGateUp, true); else MX_LAUNCH(kFwdGateUp, false);
   } else {
-    if (aligned) MX_LAUNCH(kFwdDown, true); else MX_LAUNCH(kFwdDown, false);
+    if (fast) MX_LAUNCH(kFwdDown, true); else MX_LAUNCH(kFwdDown, false);
   }
 #undef MX_LAUNCH
   return hipGetLastError();

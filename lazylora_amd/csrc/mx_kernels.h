@@ -21,11 +21,9 @@ struct FwdArgs {
   long long wp_estride;  // bytes between experts in wp*
   long long ws_estride;  // bytes between experts in ws*
   int R, K;              // each W is [R, K]
-  // A operand in the two-term e4m3 layout, row length K
-  const uint8_t* a_hi;
-  const uint8_t* a_lo;
-  const uint8_t* a_sc;
-  const int* a_row_map;  // tile row -> A row; null = identity
+  // A operand: two-term e4m3 activations in the AT layout, one block of at_tile_bytes(K)
+  // per work tile (tile t of the list below)
+  const uint8_t* a_tiles;
   // work: tiles[t] = {expert, first row, row count <= 16, 0}; null = dense, rows 16t.. of M
   const int4* tiles;
   const int* n_tiles;
@@ -35,9 +33,7 @@ struct FwdArgs {
   float* y;
   long long ldy;
   const float* row_w;    // kFwdDown: combine weight per row
-  uint8_t* q_hi;         // kFwdGateUp: act in the two-term layout, row length R (= F)
-  uint8_t* q_lo;
-  uint8_t* q_sc;
+  uint8_t* q_tiles;      // kFwdGateUp: act in the AT layout with K = R (= F), same tiles
   float* save;           // kFwdGateUp: [rows, 2R] gate | up in fp32, or null
   int act_kind;
 };
@@ -86,8 +82,13 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
 
 // ---------------------------------------------------------------- elementwise / routing
-hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, uint8_t* hi,
-                             uint8_t* lo, uint8_t* sc, hipStream_t s);
+// Two-term quantisation of activation rows into the AT layout of the work tiles. Tile t slot i
+// holds row tiles[t].y + i (through row_map when given: the token of a (token, slot) pair);
+// with tiles == null the tiles are dense: tile t holds rows 16t.. of `rows`. Unused slots get
+// zeros. max_tiles bounds the grid; the live tile count is read from n_tiles on the device.
+hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
+                              const int* n_tiles, int max_tiles, const int* row_map, uint8_t* out,
+                              hipStream_t s);
 hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int Kpad, uint16_t* hi,
                              uint16_t* lo, hipStream_t s);
 hipError_t launch_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R,

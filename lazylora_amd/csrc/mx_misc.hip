@@ -7,39 +7,55 @@ namespace mx {
 namespace {
 
 // ---------------------------------------------------------------- activation quantisation
-// One 16-lane group per 32-element block; writes the two-term AQ layout, zero padding to Kp.
+// One 16-lane group per (tile, row slot, super-chunk); it walks the 16 blocks of the chunk
+// and writes their two-term e4m3 codes and scales into the AT layout. Slots past the tile's
+// row count, and K positions past the row end, get zeros.
 template <bool BF16>
-__global__ __launch_bounds__(256) void quant_rows_kernel(const void* x, long long ldx, int rows, int K,
-                                                         uint8_t* hi, uint8_t* lo, uint8_t* sc)
+__global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long long ldx, int rows, int K,
+                                                          const int4* tiles, const int* n_tiles, const int* row_map,
+                                                          uint8_t* out)
 {
-  const long long kp = aq_kpad(K);
-  const int nbp = (int)(kp / kGroup);
-  const long long gid = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int nsc = at_nchunks(K);
+  const long long gid = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);  // (tile, slot, chunk)
   const int l16 = threadIdx.x & 15;
-  const bool in_range = gid < (long long)rows * nbp;
-  const int row = in_range ? (int)(gid / nbp) : 0;
-  const int blk = in_range ? (int)(gid - (long long)row * nbp) : 0;
-  const int k = blk * kGroup + 2 * l16;
-  float v0 = 0.f, v1 = 0.f;
-  if (in_range && k < K) {
-    if (BF16) {
-      const uint32_t u = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + row * ldx + k);
-      v0 = bf16_lo(u);
-      v1 = bf16_hi(u);
-    } else {
-      const float2 f = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(x) + row * ldx + k);
-      v0 = f.x;
-      v1 = f.y;
-    }
+  const int ntiles = tiles ? *n_tiles : (rows + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  if (gid >= (long long)ntiles * kFwdRowsPerTile * nsc) return;  // whole 16-lane groups leave together
+  const int t = (int)(gid / (kFwdRowsPerTile * nsc));
+  const int rem = (int)(gid - (long long)t * kFwdRowsPerTile * nsc);
+  const int i = rem / nsc, c = rem - i * nsc;
+  int row0, nrows;
+  if (tiles) {
+    const int4 tt = tiles[t];
+    row0 = tt.y;
+    nrows = tt.z;
+  } else {
+    row0 = t * kFwdRowsPerTile;
+    nrows = min(kFwdRowsPerTile, rows - row0);
   }
-  const Quant2 q = quant2_block16(v0, v1);
-  if (!in_range) return;
-  const long long off = (long long)row * kp + (k >> 9) * kChunk + aq_pos(k & 511);
-  *reinterpret_cast<uint16_t*>(hi + off) = (uint16_t)q.hi;
-  *reinterpret_cast<uint16_t*>(lo + off) = (uint16_t)q.lo;
-  if (l16 == 0) {
-    sc[aq_scale_off(row, K, blk, 0)] = (uint8_t)q.s_hi;
-    sc[aq_scale_off(row, K, blk, 1)] = (uint8_t)q.s_lo;
+  const bool valid = i < nrows;
+  const int src = valid ? (row_map ? row_map[row0 + i] : row0 + i) : 0;
+  uint8_t* tile = out + (long long)t * at_tile_bytes(K);
+  for (int b = 0; b < kChunkBlocks; ++b) {
+    const int k = c * kChunk + b * kGroup + 2 * l16;
+    float v0 = 0.f, v1 = 0.f;
+    if (valid && k < K) {
+      if (BF16) {
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + src * ldx + k);
+        v0 = bf16_lo(u);
+        v1 = bf16_hi(u);
+      } else {
+        const float2 f = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(x) + src * ldx + k);
+        v0 = f.x;
+        v1 = f.y;
+      }
+    }
+    const Quant2 q = quant2_block16(v0, v1);
+    *reinterpret_cast<uint16_t*>(tile + at_code_off(i, k, 0)) = (uint16_t)q.hi;
+    *reinterpret_cast<uint16_t*>(tile + at_code_off(i, k, 1)) = (uint16_t)q.lo;
+    if (l16 == 0) {
+      tile[at_scale_off(i, k, 0)] = (uint8_t)q.s_hi;
+      tile[at_scale_off(i, k, 1)] = (uint8_t)q.s_lo;
+    }
   }
 }
 
@@ -239,14 +255,16 @@ __global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, long long n_word
 
 }  // namespace
 
-hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, uint8_t* hi, uint8_t* lo,
-                             uint8_t* sc, hipStream_t s)
+hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
+                              const int* n_tiles, int max_tiles, const int* row_map, uint8_t* out, hipStream_t s)
 {
-  const long long groups = (long long)rows * (aq_kpad(K) / kGroup);
+  const long long groups = (long long)max_tiles * kFwdRowsPerTile * at_nchunks(K);
   if (groups == 0) return hipSuccess;
   dim3 grid((unsigned)((groups + 15) / 16)), block(256);
-  if (x_bf16) hipLaunchKernelGGL(quant_rows_kernel<true>, grid, block, 0, s, x, ldx, rows, K, hi, lo, sc);
-  else hipLaunchKernelGGL(quant_rows_kernel<false>, grid, block, 0, s, x, ldx, rows, K, hi, lo, sc);
+  if (x_bf16)
+    hipLaunchKernelGGL(quant_tiles_kernel<true>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, out);
+  else
+    hipLaunchKernelGGL(quant_tiles_kernel<false>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, out);
   return hipGetLastError();
 }
 

@@ -49,7 +49,8 @@ GEMM_SHAPES = [
     (1, 7168, 2048), (4, 7168, 2048), (16, 7168, 2048),             # config-2 gate/up, M sweep
     (64, 7168, 2048), (256, 7168, 2048), (16, 2048, 7168),          # ... and down
     (5, 96, 17), (33, 160, 100), (17, 640, 65),                     # ragged: K % 128 != 0, R % 64 != 0
-]
+    (20, 1024, 100), (7, 512, 200), (3, 1536, 300), (40, 4608, 72), # K % 512 == 0 with ragged R,
+]                                                                   # odd and > 8 super-chunk counts
 
 
 @pytest.mark.parametrize("M,K,R", GEMM_SHAPES)
