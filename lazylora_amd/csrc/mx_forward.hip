@@ -26,6 +26,8 @@
 #include "mx_device.h"
 #include "mx_kernels.h"
 
+#include <algorithm>
+
 namespace mx {
 
 namespace {
@@ -43,32 +45,38 @@ struct FwdLds {
 
 struct WorkItem {
   int tile, expert, row0, nrows, ct;
+  int ct0;      // first column tile of the work-group (its four waves take ct0 .. ct0 + 3)
   bool active;  // false: this wave's column tile is past the end; it only helps with the copies
 };
 
-// Work-groups are issued round-robin over the 8 XCDs (blockIdx % 8). Give each XCD one
-// contiguous run of work items so the tiles of one expert share that XCD's L2. Returns false
-// for the whole work-group at once.
+// The grid is persistent (about two work-groups per CU) and work-groups are issued round-robin
+// over the 8 XCDs (blockIdx % 8). Each XCD owns one contiguous run of work items, so the tiles
+// of one expert share that XCD's L2; its work-groups take the run's items in turn (iteration
+// `it` of slot s takes item s + it * slots). Returns false for the whole work-group at once.
 __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, int M, int n_ct, int wave,
-                                            WorkItem& w)
+                                            int it, WorkItem& w)
 {
-  const int ntiles = tiles ? *n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  // The tile list is written before this kernel and only read here: scalar loads through the
+  // constant address space, which do not wait for this work-group's outstanding stores.
+  typedef const __attribute__((address_space(4))) int* cint_ptr;
+  const int ntiles = tiles ? *(cint_ptr)n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
   const int n_cg = (n_ct + kWavesPerGroup - 1) / kWavesPerGroup;
   const int total = ntiles * n_cg;
   const int per_xcd = (total + 7) >> 3;
-  const int slot = (int)(blockIdx.x >> 3);
-  const int item = (int)(blockIdx.x & 7) * per_xcd + slot;
-  if (slot >= per_xcd || item >= total) return false;
+  const int k = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
+  const int item = (int)(blockIdx.x & 7) * per_xcd + k;
+  if (k >= per_xcd || item >= total) return false;
   const int t = item / n_cg;
   w.tile = t;
-  const int ct = (item - t * n_cg) * kWavesPerGroup + wave;
+  w.ct0 = (item - t * n_cg) * kWavesPerGroup;
+  const int ct = w.ct0 + wave;
   w.active = ct < n_ct;
   w.ct = w.active ? ct : n_ct - 1;
   if (tiles) {
-    const int4 tt = tiles[t];
-    w.expert = tt.x;
-    w.row0 = tt.y;
-    w.nrows = tt.z;
+    const cint_ptr tt = (cint_ptr)(tiles + t);
+    w.expert = tt[0];
+    w.row0 = tt[1];
+    w.nrows = tt[2];
   } else {
     w.expert = 0;
     w.row0 = t * kFwdRowsPerTile;
@@ -108,14 +116,103 @@ __device__ __forceinline__ i32x8 cat8(const i32x4& x, const i32x4& y)
   return i32x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
 }
 
-template <int MODE, bool FAST>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
-{
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps control flow scalar
-  WorkItem w;
-  if (!decode_work(a.tiles, a.n_tiles, a.M, a.n_ct, wave, w)) return;
+// Epilogue of the fast path. The four waves stage the work-group's outputs in the (now idle)
+// activation buffers of LDS, then write them with 16-byte stores that cover whole runs of
+// memory: scattered 1-byte and 4-byte stores of the same data cost the weight stream about a
+// tenth of its bandwidth. Lane (j, g) holds rows 4g+v (v = 0..3) of columns grp*16 + j.
+constexpr int kStagePitch = 260;  // floats per staged row: 256 + 4 keeps the row starts on distinct banks
 
+template <int MODE>
+__device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem& w, int wave, int lane,
+                                                const f32x4 (&acc)[4], const float (&tw)[4], FwdLds& lds)
+{
+  const int j = lane & 15, g = lane >> 4;
+  const int t = wave * 64 + lane;
+  if (MODE == kFwdGateUp) {
+    // act codes: [q = wave][plane][half][row 0..15][16 B] then scales [row][plane][q]; this is
+    // the AT byte order of the work-group's 128 features (super-chunk c, block group gl)
+    uint8_t* sq = lds.a[0];
+    float* ss = reinterpret_cast<float*>(lds.a[1]);  // [row][gate 128 | up 128] fp32
+    const int F = a.R;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int i = 4 * g + v;
+      const float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
+      Quant2 q = quant2_block16(glu_fwd(ga, ua, a.act_kind), glu_fwd(gb, ub, a.act_kind));
+      if (!w.active) q = Quant2{0, 0, 0, 0};  // features past F: the padding of the layout is zero
+      sq[((wave * 2 + 0) * 2 + 0) * 256 + i * 16 + j] = (uint8_t)q.hi;
+      sq[((wave * 2 + 0) * 2 + 1) * 256 + i * 16 + j] = (uint8_t)(q.hi >> 8);
+      sq[((wave * 2 + 1) * 2 + 0) * 256 + i * 16 + j] = (uint8_t)q.lo;
+      sq[((wave * 2 + 1) * 2 + 1) * 256 + i * 16 + j] = (uint8_t)(q.lo >> 8);
+      if (j == 0) {
+        sq[4096 + i * 8 + wave] = (uint8_t)q.s_hi;
+        sq[4096 + i * 8 + 4 + wave] = (uint8_t)q.s_lo;
+      }
+      if (a.save) {
+        float* r = ss + i * kStagePitch + wave * 32 + j;
+        r[0] = ga;
+        r[16] = gb;
+        r[128] = ua;
+        r[144] = ub;
+      }
+    }
+    __syncthreads();
+    const int f_wg = w.ct0 * 32;  // first feature of the work-group, a multiple of 128
+    const int c = f_wg >> 9, gl = (f_wg >> 7) & 3;
+    uint8_t* qbase = a.q_tiles + (long long)w.tile * at_tile_bytes(F) + (long long)c * kAtChunkBytes;
+    {
+      const int run = t >> 5, off = (t & 31) * 16;  // run = q * 2 + plane: 512 B each
+      *reinterpret_cast<i32x4*>(qbase + (run * 2 + (gl >> 1)) * 1024 + (gl & 1) * 512 + off) =
+          *reinterpret_cast<const i32x4*>(sq + run * 512 + off);
+      if (t < 8)
+        *reinterpret_cast<i32x4*>(qbase + kAtCodeBytes + gl * 128 + t * 16) =
+            *reinterpret_cast<const i32x4*>(sq + 4096 + t * 16);
+    }
+    if (a.save) {
+      const int part = lane >> 5, idx = (lane & 31) * 4, f = f_wg + idx;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int r = it * 4 + wave;
+        if (r < w.nrows && f < F)
+          *reinterpret_cast<f32x4*>(a.save + (long long)(w.row0 + r) * 2 * F + part * F + f) =
+              *reinterpret_cast<const f32x4*>(ss + r * kStagePitch + part * 128 + idx);
+      }
+    }
+    return;
+  }
+
+  // kFwdPlain / kFwdDown: [row][256 columns of the work-group] fp32
+  float* ss = reinterpret_cast<float*>(lds.a[0]);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const float wv = MODE == kFwdDown ? tw[v] : 1.0f;
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) ss[(4 * g + v) * kStagePitch + wave * 64 + grp * 16 + j] = acc[grp][v] * wv;
+  }
+  __syncthreads();
+  const int col = w.ct0 * kFwdColsPerTile + lane * 4;
+  const bool vec = ((a.ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int r = it * 4 + wave;
+    if (r >= w.nrows) continue;
+    const f32x4 val = *reinterpret_cast<const f32x4*>(ss + r * kStagePitch + lane * 4);
+    float* yr = a.y + (long long)(w.row0 + r) * a.ldy;
+    if (vec && col + 4 <= a.R) {
+      *reinterpret_cast<f32x4*>(yr + col) = val;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (col + e < a.R) yr[col + e] = val[e];
+    }
+  }
+}
+
+// One work item: the 16 x 64 tile (w.tile, w.ct) over all of K, then its epilogue.
+template <int MODE, bool FAST>
+__device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, int wave, int lane)
+{
+  __shared__ FwdLds lds;  // used by the fast path only
   const int j = lane & 15, g = lane >> 4;
   const int nb = a.K / kGroup;
   const int nsc = at_nchunks(a.K);
@@ -145,6 +242,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
   f32x4 acc[4];
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) acc[grp] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float tw[4];  // kFwdDown: combine weights of this lane's output rows, requested with the first loads
 
   auto load_b = [&](int c, i32x4 (&b)[4][4]) {
 #pragma unroll
@@ -154,7 +252,6 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
   };
 
   if constexpr (FAST) {
-    __shared__ FwdLds lds;
     uint8_t* const sw = lds.s[wave];
 
     // A(c) -> lds.a[buf]: wave w copies KiB units 4w..4w+3 of the codes; wave 0 also copies
@@ -170,13 +267,17 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
     };
     // scale window win -> sw: instruction i covers rows 8i..8i+7 of this wave's 64, lane l
     // copies 16 B (one super-chunk) of row 8i + l/8, chunk 8 win + l%8 (clamped to the row)
+    // (addresses are rebuilt at each call from uniform bases and 32-bit lane offsets rather
+    // than held in registers across the steps in between)
     auto issue_scales = [&](int win) {
-      const int cc = min(win * kScaleWin + (lane & 7), nsc - 1);
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int cc = min(win * kScaleWin + (ln & 7), nsc - 1);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int grp = i >> 1;
-        const int n = min(grp_row(grp) + 8 * (i & 1) + (lane >> 3), a.R - 1);
-        dma16(grp_ws(grp) + (long long)n * nb + cc * 16, sw + i * 1024);
+        const uint32_t off = (uint32_t)(min(grp_row(grp) + 8 * (i & 1) + (ln >> 3), a.R - 1) * nb + cc * 16);
+        dma16(grp_ws(grp) + off, sw + i * 1024);
       }
     };
     auto step = [&](int c, i32x4 (&cur)[4][4], i32x4 (&nxt)[4][4]) {
@@ -211,9 +312,12 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
     };
 
     i32x4 b0[4][4], b1[4][4];
+    load_b(0, b0);
     issue_a(0, 0);
     issue_scales(0);
-    load_b(0, b0);
+    if (MODE == kFwdDown)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tw[v] = a.row_w[w.row0 + min(4 * g + v, w.nrows - 1)];
     for (int c = 0;;) {
       step(c, b0, b1);
       if (++c >= nsc) break;
@@ -221,6 +325,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
       if (++c >= nsc) break;
     }
   } else {
+    if (MODE == kFwdDown)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tw[v] = a.row_w[w.row0 + min(4 * g + v, w.nrows - 1)];
     // any K (a multiple of 32): straight loads, blocks past the end of the row load nothing
     // and carry a zero operand with scale 2^0 (their activations are zero too)
     const uint8_t* bs[4];
@@ -264,6 +371,12 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
     }
   }
 
+  if constexpr (FAST) {
+    __syncthreads();  // every wave is done with the last chunk's LDS data
+    epilogue_staged<MODE>(a, w, wave, lane, acc, tw, lds);
+    return;
+  }
+
   if (!w.active) return;
 
   // epilogue, straight from the accumulators: lane (j, g) holds rows 4g+v (v = 0..3) of
@@ -305,14 +418,42 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
     const int i = 4 * g + v;
     if (i >= w.nrows) continue;
     const int row = w.row0 + i;
-    const float tw = MODE == kFwdDown ? a.row_w[row] : 1.0f;
+    const float wv = MODE == kFwdDown ? tw[v] : 1.0f;
     float* yr = a.y + (long long)row * a.ldy;
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       const int col = w.ct * kFwdColsPerTile + grp * 16 + j;
-      if (col < a.R) yr[col] = acc[grp][v] * tw;
+      if (col < a.R) yr[col] = acc[grp][v] * wv;
     }
   }
+}
+
+template <int MODE, bool FAST>
+__global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
+{
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps control flow scalar
+  WorkItem w;
+  for (int it = 0; decode_work(a.tiles, a.n_tiles, a.M, a.n_ct, wave, it, w); ++it) {
+    // the previous item's reads of LDS are complete before this item's copies land there;
+    // its output stores drain while this item's first loads are in flight
+    if (FAST && it > 0) __syncthreads();
+    // recompute lane-derived addresses per item instead of holding them across items
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    fwd_item<MODE, FAST>(a, w, wave, l);
+  }
+}
+
+// Work-groups that fit on the device at once (two per CU: the LDS and register budgets of
+// fwd_kernel), rounded down to a multiple of the 8 XCDs.
+int resident_groups()
+{
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return max(8, (2 * cus) / 8 * 8);
 }
 
 }  // namespace
@@ -322,7 +463,7 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   const long long n_cg = (a.n_ct + kWavesPerGroup - 1) / kWavesPerGroup;
   const long long total = (long long)max_tiles * n_cg;
   if (total <= 0) return hipSuccess;
-  const long long blocks = (total + 7) / 8 * 8;
+  const long long blocks = std::min<long long>((total + 7) / 8 * 8, resident_groups());
   const bool fast = (a.K % kChunk) == 0;
   dim3 grid((unsigned)blocks), block(64 * kWavesPerGroup);
 #define MX_LAUNCH(M, F) hipLaunchKernelGGL((fwd_kernel<M, F>), grid, block, 0, s, a)
