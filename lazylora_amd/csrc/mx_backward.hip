@@ -2,14 +2,20 @@
 //
 // The contraction runs over W's rows, the strided direction of the packed layout, and the
 // E8M0 scales group W along its columns, so the scaled MFMA cannot consume W directly here.
-// Each step a work-group (256 threads) cooperatively loads a 32-row x 256-column slab of W
-// (every thread one 16-byte MX block = 32 columns of one row), decodes it with
+// Each step a work-group (256 threads) cooperatively loads a 32-row x 512-column slab of W
+// (every thread two 16-byte MX blocks = 2 x 32 columns of one row), decodes it with
 // v_cvt_scalef32_pk_bf16_fp4 (bit-exact: e2m1 * 2^(s-127) is exact in bf16), and writes it
-// row-major (padded, see slab_off) into LDS. Each wave then owns 64 output columns and pulls its B operands with
-// ds_read_b64_tr_b16, which hands lane i of a 16-lane group column i of four consecutive
-// rows. A (activation gradients) is split into bf16 hi + lo terms, so the products carry
-// ~16 significant bits of the activation against the exact weights. The slab in LDS is
-// double-buffered: one barrier per step.
+// row-major (padded, see slab_off) into LDS. Each wave then owns 128 output columns and pulls
+// its B operands with ds_read_b64_tr_b16, which hands lane i of a 16-lane group column i of
+// four consecutive rows. A (activation gradients) is split into bf16 hi + lo terms, so the
+// products carry ~16 significant bits of the activation against the exact weights. One slab
+// buffer (42 KB, two work-groups per CU), two barriers per step: after the decode, and after
+// every wave has read its operands into registers, so the MFMAs of one step run while the
+// next step is decoded.
+//
+// 512 columns per work-group: the E8M0 scales of one W row sit in the same 128-byte lines
+// for all column tiles, and every work-group that reads a line only for its own 16 bytes
+// costs a fetch of the whole line; wider tiles cut those fetches in half.
 //
 // The whole contraction range (nseg * R rows) stays in one work-group, so every output
 // element has exactly one writer and the sum order is fixed: results are deterministic.
@@ -21,19 +27,20 @@ namespace mx {
 namespace {
 
 constexpr int kSlabRows = 32;
+constexpr int kSlabBlocks = kBwdColsPerTile / kGroup;  // 16 MX blocks per slab row
 // LDS slab layout (bytes): a 32-column block of a row takes 64 B + 16 B of padding, a row
-// 8 blocks + 32 B. With the 80 B block stride the 8 lanes of a ds_write_b128 phase (one row,
-// 8 blocks) land on 8 distinct bank groups; with the 672 B row pitch (168 dwords, = 8 banks
-// mod 32 and 40 mod 64) the 4 rows one 16-lane group reads with ds_read_b64_tr_b16 do too.
+// 16 blocks + 32 B. With the 80 B block stride the lanes of a ds_write_b128 phase (one row,
+// 8 blocks) land on distinct bank groups; with the 1312 B row pitch (328 dwords, = 8 mod 64)
+// the 4 rows one 16-lane group reads with ds_read_b64_tr_b16 do too.
 constexpr int kBlockBytes = 80;
-constexpr int kRowBytes = 8 * kBlockBytes + 32;
+constexpr int kRowBytes = kSlabBlocks * kBlockBytes + 32;
 constexpr int kSlabBytes = kSlabRows * kRowBytes;
 
 __device__ __forceinline__ int slab_off(int row, int col)  // col in bf16 elements
 {
   return row * kRowBytes + (col >> 5) * kBlockBytes + (col & 31) * 2;
 }
-constexpr int kPrefetch = 8;                      // weight slabs in flight per work-group (even)
+constexpr int kPrefetch = 8;  // weight steps in flight per work-group (even)
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
@@ -44,7 +51,9 @@ struct WorkItem {
 __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, int M, int n_ct,
                                             WorkItem& w)
 {
-  const int ntiles = tiles ? *n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  // the tile list is only read here: scalar loads through the constant address space
+  typedef const __attribute__((address_space(4))) int* cint_ptr;
+  const int ntiles = tiles ? *(cint_ptr)n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
   const int total = ntiles * n_ct;
   const int per_xcd = (total + 7) >> 3;
   const int slot = (int)(blockIdx.x >> 3);
@@ -53,10 +62,10 @@ __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tile
   const int t = item / n_ct;
   w.ct = item - t * n_ct;
   if (tiles) {
-    const int4 tt = tiles[t];
-    w.expert = tt.x;
-    w.row0 = tt.y;
-    w.nrows = tt.z;
+    const cint_ptr tt = (cint_ptr)(tiles + t);
+    w.expert = tt[0];
+    w.row0 = tt[1];
+    w.nrows = tt[2];
   } else {
     w.expert = 0;
     w.row0 = t * kFwdRowsPerTile;
@@ -81,10 +90,21 @@ __device__ __forceinline__ void decode_block_bf16(const i32x4& raw, uint32_t s, 
   }
 }
 
+__device__ __forceinline__ void store_block(uint8_t* slab, int row, int blk, const i32x4& raw, uint32_t s)
+{
+  uint32_t dec[16];
+  decode_block_bf16(raw, s, dec);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(slab + slab_off(row, blk * 32));
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<i32x4*>(dst + 4 * q) =
+        i32x4{(int)dec[4 * q], (int)dec[4 * q + 1], (int)dec[4 * q + 2], (int)dec[4 * q + 3]};
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
 {
-  __shared__ __attribute__((aligned(16))) uint8_t slab[2][kSlabBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t slab[kSlabBytes];
   __shared__ float dotred[4][16];
 
   WorkItem w;
@@ -99,29 +119,32 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
   // the ring below is unrolled kPrefetch-fold; padding steps load nothing useful (zero weights)
   const int nsteps_pad = (nsteps + kPrefetch - 1) / kPrefetch * kPrefetch;
 
-  // loader role: one 16-byte MX block per thread per step
-  const int lr = tid >> 3;         // slab row
-  const int lc = tid & 7;          // 32-column block inside the tile
-  const int lcol = c0 + lc * 32;
-  const int lcol_c = lcol < a.C ? lcol : 0;
+  // loader role: MX blocks lc and lc + 8 of slab row lr per step, so each load instruction
+  // of a wave reads whole 128-byte lines (8 rows x 8 blocks)
+  const int lr = tid >> 3;
+  const int lc = tid & 7;
   const int cbs = a.C / kGroup;    // scale bytes per W row
   const long long wpitch = a.C / 2;
-  const long long wbase = (long long)w.expert * a.wp_estride + lcol_c / 2;
-  const long long sbase = (long long)w.expert * a.ws_estride + lcol_c / kGroup;
+  const int colA = c0 + lc * 32, colB = c0 + (lc + 8) * 32;
+  const int colA_c = colA < a.C ? colA : 0, colB_c = colB < a.C ? colB : 0;
+  const long long wbase = (long long)w.expert * a.wp_estride;
+  const long long sbase = (long long)w.expert * a.ws_estride;
 
-  // Always issues the two loads, with row and column clamped into the matrix, so the wait
+  // Always issues the loads, with rows and columns clamped into the matrix, so the wait
   // counters stay exact and nothing touches the loaded data before its decode step. Clamped
   // blocks are harmless: columns >= C are never stored, and rows >= nseg*R meet zero
   // activations (zero padding of A, or the padding steps below). Rows >= R read the second
-  // segment (W3 after W1).
-  auto load_raw = [&](int step, i32x4& raw, uint8_t& sc) {
+  // segment (W3 after W1). Weight bytes are read exactly once: streaming loads.
+  auto load_raw = [&](int step, i32x4& r0, i32x4& r1, uint8_t& s0, uint8_t& s1) {
     const int r = min(step * kSlabRows + lr, rtot - 1);
     const bool seg = r >= a.R;
     const int rr = seg ? r - a.R : r;
-    const uint8_t* P = seg ? a.wp1 : a.wp0;
-    const uint8_t* S = seg ? a.ws1 : a.ws0;
-    raw = ldg16(P + wbase + (long long)rr * wpitch);
-    sc = S[sbase + (long long)rr * cbs];
+    const uint8_t* P = (seg ? a.wp1 : a.wp0) + wbase + (long long)rr * wpitch;
+    const uint8_t* S = (seg ? a.ws1 : a.ws0) + sbase + (long long)rr * cbs;
+    r0 = ldg16_nt(P + colA_c / 2);
+    r1 = ldg16_nt(P + colB_c / 2);
+    s0 = S[colA_c / kGroup];
+    s1 = S[colB_c / kGroup];
   };
 
   // A operand rows (rows past the tile end repeat the last row; never stored)
@@ -130,22 +153,22 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
   const uint16_t* pah = a.a_hi + (long long)arow * a.lda + 8 * g;
   const uint16_t* pal = a.a_lo + (long long)arow * a.lda + 8 * g;
 
-  f32x4 acc[4];
+  f32x4 acc[8];
 #pragma unroll
-  for (int cg = 0; cg < 4; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int cg = 0; cg < 8; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Pipeline: the raw blocks of the next kPrefetch steps are in flight in a register ring.
   // Within a step the next step's A loads are issued before the ring refill, so waiting for
   // A (vmcnt is an in-order counter) never waits for the far-ahead weight loads.
-  i32x4 ring[kPrefetch];
-  uint8_t rsc[kPrefetch];
+  i32x4 ring0[kPrefetch], ring1[kPrefetch];
+  uint8_t rs0[kPrefetch], rs1[kPrefetch];
   // Issue order is pinned (A first, then the ring slot by slot) so the loop head can wait
   // for slot 0 alone, whether it is entered from here or from the back edge.
   i32x4 ahv = ldg16(pah), alv = ldg16(pal);
 #pragma unroll
   for (int p = 0; p < kPrefetch; ++p) {
     __builtin_amdgcn_sched_barrier(0);
-    load_raw(p, ring[p], rsc[p]);
+    load_raw(p, ring0[p], ring1[p], rs0[p], rs1[p]);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -153,48 +176,45 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
 #pragma unroll
     for (int p = 0; p < kPrefetch; ++p) {
       const int s = s0 + p;
-      const int buf = p & 1;  // kPrefetch is even, so this is s & 1
       // keep later steps' use of the ring (and so their waits) below this point
       __builtin_amdgcn_sched_barrier(0);
-      {
-        uint32_t dec[16];
-        decode_block_bf16(ring[p], rsc[p], dec);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(&slab[buf][slab_off(lr, lc * 32)]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<i32x4*>(dst + 4 * q) =
-              i32x4{(int)dec[4 * q], (int)dec[4 * q + 1], (int)dec[4 * q + 2], (int)dec[4 * q + 3]};
-      }
+      // the slab is free: every wave has its B operands of the previous step in registers
+      store_block(slab, lr, lc, ring0[p], rs0[p]);
+      store_block(slab, lr, lc + 8, ring1[p], rs1[p]);
       __syncthreads();
       const int sn = min(s + 1, nsteps - 1);
       const i32x4 ahn = ldg16(pah + sn * kSlabRows);
       const i32x4 aln = ldg16(pal + sn * kSlabRows);
       __builtin_amdgcn_sched_barrier(0);
-      load_raw(s + kPrefetch, ring[p], rsc[p]);
+      load_raw(s + kPrefetch, ring0[p], ring1[p], rs0[p], rs1[p]);
       __builtin_amdgcn_sched_barrier(0);
 
       // padding steps (s >= nsteps) see clamped weights: zero their activations instead
       const bool real = s < nsteps;
       const bf16x8 ah = __builtin_bit_cast(bf16x8, real ? ahv : i32x4{0, 0, 0, 0});
       const bf16x8 al = __builtin_bit_cast(bf16x8, real ? alv : i32x4{0, 0, 0, 0});
+      // B operands of this wave's 8 column groups (rows 8g..8g+7 of column cg*16 + li), each
+      // read just before its two MFMAs
 #pragma unroll
-      for (int cg = 0; cg < 4; ++cg) {
-        const int col = wave * 64 + cg * 16 + 4 * (li & 3);
+      for (int cg = 0; cg < 8; ++cg) {
+        const int col = wave * 128 + cg * 16 + 4 * (li & 3);
         const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(&slab[buf][slab_off(8 * g + (li >> 2), col)]));
+            (lds_i16x4*)(&slab[slab_off(8 * g + (li >> 2), col)]));
         const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(&slab[buf][slab_off(8 * g + 4 + (li >> 2), col)]));
+            (lds_i16x4*)(&slab[slab_off(8 * g + 4 + (li >> 2), col)]));
         const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
         const bf16x8 b = __builtin_bit_cast(bf16x8, bs);
         acc[cg] = mfma_bf16(ah, b, acc[cg]);
         acc[cg] = mfma_bf16(al, b, acc[cg]);
       }
+      wait_lgkm0();
+      __syncthreads();  // every wave has read its operands: the slab may be overwritten
       ahv = ahn;
       alv = aln;
     }
   }
 
-  // epilogue: lane (li, g) holds rows 4g..4g+3 of column c0 + wave*64 + cg*16 + li
+  // epilogue: lane (li, g) holds rows 4g..4g+3 of column c0 + wave*128 + cg*16 + li
   if (MODE == kBwdDownT) {
     const int F = a.C;
     float dots[4] = {0.f, 0.f, 0.f, 0.f};
@@ -206,8 +226,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
       const float tw = a.row_w[p];
       const float* sv = a.saved + (long long)p * 2 * F;
 #pragma unroll
-      for (int cg = 0; cg < 4; ++cg) {
-        const int f = c0 + wave * 64 + cg * 16 + li;
+      for (int cg = 0; cg < 8; ++cg) {
+        const int f = c0 + wave * 128 + cg * 16 + li;
         if (f < F) {
           const float h = acc[cg][v];
           const float gt = sv[f], up = sv[F + f];
@@ -244,8 +264,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
     if (i >= w.nrows) continue;
     float* yr = a.y + (long long)(w.row0 + i) * a.ldy;
 #pragma unroll
-    for (int cg = 0; cg < 4; ++cg) {
-      const int col = c0 + wave * 64 + cg * 16 + li;
+    for (int cg = 0; cg < 8; ++cg) {
+      const int col = c0 + wave * 128 + cg * 16 + li;
       if (col < a.C) {
         if (a.accumulate) yr[col] += acc[cg][v];
         else yr[col] = acc[cg][v];

@@ -154,6 +154,11 @@ MX_DEV f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, f32x4 c)
 }
 
 MX_DEV i32x4 ldg16(const void* p) { return *reinterpret_cast<const i32x4*>(p); }
+// Streaming (non-temporal) load for data read exactly once, such as the expert weights: it
+// does not push reused lines (activations, scale rows shared by work-groups) out of L2. Only
+// for loads whose instruction consumes every byte of its cache lines: a line that a later
+// instruction reads again is fetched again.
+MX_DEV i32x4 ldg16_nt(const void* p) { return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p)); }
 
 // Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes from src land at
 // lds + 16 l. lds must be the same for the whole wave. Completion is counted by vmcnt.

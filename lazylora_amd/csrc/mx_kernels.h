@@ -61,7 +61,7 @@ struct BwdArgs {
   const int4* tiles;
   const int* n_tiles;
   int M;
-  int n_ct;  // column tiles of 256
+  int n_ct;  // column tiles of kBwdColsPerTile
   float* y;
   long long ldy;
   int accumulate;
@@ -76,7 +76,7 @@ struct BwdArgs {
 
 constexpr int kFwdRowsPerTile = 16;
 constexpr int kFwdColsPerTile = 64;  // kFwdPlain / kFwdDown; kFwdGateUp covers 32 features
-constexpr int kBwdColsPerTile = 256;
+constexpr int kBwdColsPerTile = 512;
 
 hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
