@@ -9,4 +9,4 @@ The arithmetic runs in hand-written gfx950 HIP kernels behind a C ABI
 (include/lazylora_mxfp4.h, built into lazylora_amd/liblazylora_mxfp4.so by lazylora_amd.build).
 """
 
-__all__ = ["native", "experts", "routed", "streaming"]
+__all__ = ["native", "experts", "routed"]
