@@ -8,10 +8,9 @@
 // row-major (padded, see slab_off) into LDS. Each wave then owns 128 output columns and pulls
 // its B operands with ds_read_b64_tr_b16, which hands lane i of a 16-lane group column i of
 // four consecutive rows. A (activation gradients) is split into bf16 hi + lo terms, so the
-// products carry ~16 significant bits of the activation against the exact weights. One slab
-// buffer (42 KB, two work-groups per CU), two barriers per step: after the decode, and after
-// every wave has read its operands into registers, so the MFMAs of one step run while the
-// next step is decoded.
+// products carry ~16 significant bits of the activation against the exact weights. The slab
+// is double-buffered (2 x 32 KiB, XOR-swizzled instead of padded, so two work-groups fit per
+// CU): one barrier per step.
 //
 // 512 columns per work-group: the E8M0 scales of one W row sit in the same 128-byte lines
 // for all column tiles, and every work-group that reads a line only for its own 16 bytes
@@ -27,18 +26,24 @@ namespace mx {
 namespace {
 
 constexpr int kSlabRows = 32;
-constexpr int kSlabBlocks = kBwdColsPerTile / kGroup;  // 16 MX blocks per slab row
-// LDS slab layout (bytes): a 32-column block of a row takes 64 B + 16 B of padding, a row
-// 16 blocks + 32 B. With the 80 B block stride the lanes of a ds_write_b128 phase (one row,
-// 8 blocks) land on distinct bank groups; with the 1312 B row pitch (328 dwords, = 8 mod 64)
-// the 4 rows one 16-lane group reads with ds_read_b64_tr_b16 do too.
-constexpr int kBlockBytes = 80;
-constexpr int kRowBytes = kSlabBlocks * kBlockBytes + 32;
-constexpr int kSlabBytes = kSlabRows * kRowBytes;
+constexpr int kRowBytes = kBwdColsPerTile * 2;     // 1 KiB of bf16 per slab row, no padding
+constexpr int kSlabBytes = kSlabRows * kRowBytes;  // 32 KiB; two of them per work-group
 
-__device__ __forceinline__ int slab_off(int row, int col)  // col in bf16 elements
+// LDS slab layout. LDS has 32 banks of 4 bytes; a ds_write_b128 is served 8 lanes per cycle
+// and a ds_read_b64_tr_b16 16 lanes per cycle (both measured on the hardware). A row is 128
+// "quads" of 4 bf16 (8 bytes); quad q of row r is stored at position
+//   q ^ (((q >> 4) & 3) << 1) ^ ((r & 3) << 2),
+// which only permutes bits 1-3 of q: aligned quad pairs stay together (16-byte writes stay
+// contiguous) and every quad stays in its aligned group of 16. The 8 lanes of a write phase
+// (one row, blocks lc = 0..7, same piece) then cover all 32 banks, and so do the 16 lanes of a
+// transposed-read phase (4 consecutive rows x 4 quads).
+__device__ __forceinline__ int quad_pos(int row, int q)
 {
-  return row * kRowBytes + (col >> 5) * kBlockBytes + (col & 31) * 2;
+  return q ^ (((q >> 4) & 3) << 1) ^ ((row & 3) << 2);
+}
+__device__ __forceinline__ int slab_off(int row, int q)  // byte offset of quad q of row
+{
+  return row * kRowBytes + quad_pos(row, q) * 8;
 }
 constexpr int kPrefetch = 8;  // weight steps in flight per work-group (even)
 
@@ -90,21 +95,21 @@ __device__ __forceinline__ void decode_block_bf16(const i32x4& raw, uint32_t s, 
   }
 }
 
+// Decoded block blk (32 columns = quads 8 blk .. 8 blk + 7) of a slab row: four 16-byte writes.
 __device__ __forceinline__ void store_block(uint8_t* slab, int row, int blk, const i32x4& raw, uint32_t s)
 {
   uint32_t dec[16];
   decode_block_bf16(raw, s, dec);
-  uint32_t* dst = reinterpret_cast<uint32_t*>(slab + slab_off(row, blk * 32));
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *reinterpret_cast<i32x4*>(dst + 4 * q) =
-        i32x4{(int)dec[4 * q], (int)dec[4 * q + 1], (int)dec[4 * q + 2], (int)dec[4 * q + 3]};
+  for (int j = 0; j < 4; ++j)
+    *reinterpret_cast<i32x4*>(slab + slab_off(row, blk * 8 + 2 * j)) =
+        i32x4{(int)dec[4 * j], (int)dec[4 * j + 1], (int)dec[4 * j + 2], (int)dec[4 * j + 3]};
 }
 
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
 {
-  __shared__ __attribute__((aligned(16))) uint8_t slab[kSlabBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t slab[2][kSlabBytes];
   __shared__ float dotred[4][16];
 
   WorkItem w;
@@ -176,11 +181,13 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
 #pragma unroll
     for (int p = 0; p < kPrefetch; ++p) {
       const int s = s0 + p;
+      uint8_t* const sl = slab[p & 1];  // kPrefetch is even, so this is slab[s & 1]
       // keep later steps' use of the ring (and so their waits) below this point
       __builtin_amdgcn_sched_barrier(0);
-      // the slab is free: every wave has its B operands of the previous step in registers
-      store_block(slab, lr, lc, ring0[p], rs0[p]);
-      store_block(slab, lr, lc + 8, ring1[p], rs1[p]);
+      // this buffer was last read two steps ago; the barrier of the previous step ordered
+      // those reads before these writes
+      store_block(sl, lr, lc, ring0[p], rs0[p]);
+      store_block(sl, lr, lc + 8, ring1[p], rs1[p]);
       __syncthreads();
       const int sn = min(s + 1, nsteps - 1);
       const i32x4 ahn = ldg16(pah + sn * kSlabRows);
@@ -197,18 +204,16 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
       // read just before its two MFMAs
 #pragma unroll
       for (int cg = 0; cg < 8; ++cg) {
-        const int col = wave * 128 + cg * 16 + 4 * (li & 3);
+        const int q = wave * 32 + cg * 4 + (li & 3);
         const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(&slab[slab_off(8 * g + (li >> 2), col)]));
+            (lds_i16x4*)(&sl[slab_off(8 * g + (li >> 2), q)]));
         const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(&slab[slab_off(8 * g + 4 + (li >> 2), col)]));
+            (lds_i16x4*)(&sl[slab_off(8 * g + 4 + (li >> 2), q)]));
         const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
         const bf16x8 b = __builtin_bit_cast(bf16x8, bs);
         acc[cg] = mfma_bf16(ah, b, acc[cg]);
         acc[cg] = mfma_bf16(al, b, acc[cg]);
       }
-      wait_lgkm0();
-      __syncthreads();  // every wave has read its operands: the slab may be overwritten
       ahv = ahn;
       alv = aln;
     }
