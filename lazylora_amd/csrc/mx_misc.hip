@@ -7,22 +7,22 @@ namespace mx {
 namespace {
 
 // ---------------------------------------------------------------- activation quantisation
-// One 16-lane group per (tile, row slot, super-chunk); it walks the 16 blocks of the chunk
-// and writes their two-term e4m3 codes and scales into the AT layout. Slots past the tile's
-// row count, and K positions past the row end, get zeros.
+// One work-group per (tile, super-chunk). Its 16 lane groups take the 16 row slots; each walks
+// the 16 blocks of the chunk, quantises them to two e4m3 terms and writes codes and scales into
+// an LDS copy of the chunk in the AT layout; the work-group then writes the chunk out with
+// contiguous 16-byte stores. Slots past the tile's row count, and K positions past the row
+// end, get zeros.
 template <bool BF16>
 __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long long ldx, int rows, int K,
                                                           const int4* tiles, const int* n_tiles, const int* row_map,
                                                           uint8_t* out)
 {
+  __shared__ __attribute__((aligned(16))) uint8_t chunk[kAtChunkBytes];
   const int nsc = at_nchunks(K);
-  const long long gid = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);  // (tile, slot, chunk)
-  const int l16 = threadIdx.x & 15;
+  const int t = (int)(blockIdx.x / nsc), c = (int)(blockIdx.x - (long long)t * nsc);
   const int ntiles = tiles ? *n_tiles : (rows + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
-  if (gid >= (long long)ntiles * kFwdRowsPerTile * nsc) return;  // whole 16-lane groups leave together
-  const int t = (int)(gid / (kFwdRowsPerTile * nsc));
-  const int rem = (int)(gid - (long long)t * kFwdRowsPerTile * nsc);
-  const int i = rem / nsc, c = rem - i * nsc;
+  if (t >= ntiles) return;  // the whole work-group
+  const int i = threadIdx.x >> 4, l16 = threadIdx.x & 15;
   int row0, nrows;
   if (tiles) {
     const int4 tt = tiles[t];
@@ -33,8 +33,8 @@ __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long lo
     nrows = min(kFwdRowsPerTile, rows - row0);
   }
   const bool valid = i < nrows;
-  const int src = valid ? (row_map ? row_map[row0 + i] : row0 + i) : 0;
-  uint8_t* tile = out + (long long)t * at_tile_bytes(K);
+  const long long src = valid ? (row_map ? row_map[row0 + i] : row0 + i) : 0;
+  const long long cbase = (long long)c * kAtChunkBytes;  // at_*_off are tile-relative
   for (int b = 0; b < kChunkBlocks; ++b) {
     const int k = c * kChunk + b * kGroup + 2 * l16;
     float v0 = 0.f, v1 = 0.f;
@@ -50,13 +50,17 @@ __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long lo
       }
     }
     const Quant2 q = quant2_block16(v0, v1);
-    *reinterpret_cast<uint16_t*>(tile + at_code_off(i, k, 0)) = (uint16_t)q.hi;
-    *reinterpret_cast<uint16_t*>(tile + at_code_off(i, k, 1)) = (uint16_t)q.lo;
+    *reinterpret_cast<uint16_t*>(chunk + (at_code_off(i, k, 0) - cbase)) = (uint16_t)q.hi;
+    *reinterpret_cast<uint16_t*>(chunk + (at_code_off(i, k, 1) - cbase)) = (uint16_t)q.lo;
     if (l16 == 0) {
-      tile[at_scale_off(i, k, 0)] = (uint8_t)q.s_hi;
-      tile[at_scale_off(i, k, 1)] = (uint8_t)q.s_lo;
+      chunk[at_scale_off(i, k, 0) - cbase] = (uint8_t)q.s_hi;
+      chunk[at_scale_off(i, k, 1) - cbase] = (uint8_t)q.s_lo;
     }
   }
+  __syncthreads();
+  uint8_t* dst = out + (long long)t * at_tile_bytes(K) + cbase;
+  for (int o = threadIdx.x * 16; o < kAtChunkBytes; o += 256 * 16)
+    *reinterpret_cast<i32x4*>(dst + o) = *reinterpret_cast<const i32x4*>(chunk + o);
 }
 
 // ---------------------------------------------------------------- fp32 -> bf16 hi + lo
@@ -258,9 +262,9 @@ __global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, long long n_word
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
                               const int* n_tiles, int max_tiles, const int* row_map, uint8_t* out, hipStream_t s)
 {
-  const long long groups = (long long)max_tiles * kFwdRowsPerTile * at_nchunks(K);
+  const long long groups = (long long)max_tiles * at_nchunks(K);  // (tile, super-chunk) work-groups
   if (groups == 0) return hipSuccess;
-  dim3 grid((unsigned)((groups + 15) / 16)), block(256);
+  dim3 grid((unsigned)groups), block(256);
   if (x_bf16)
     hipLaunchKernelGGL(quant_tiles_kernel<true>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, out);
   else
