@@ -111,6 +111,30 @@ int mxfp4_moe_backward(float *grad_h, float *grad_w, const float *grad_out, cons
  * synchronising `stream`: bit 0 set = some topk_idx entry was outside [0, E). */
 int mxfp4_moe_route_status(const void *workspace, int *host_flags, hipStream_t stream);
 
+/* Expert selection of KimiK3MoERouter.forward after the gate product
+ * (lazy_lora/core/moe_router.py:81-99, the torch branch; :102-123 is the same in NumPy):
+ *   scores = sigmoid(logits); choice = scores + bias (bias may be NULL: no bias);
+ *   topk_idx[t, :] = the top_k experts by choice, in descending order (torch.topk(sorted=True);
+ *   equal choices go to the lower expert id first);
+ *   topk_w[t, j] = scores[t, topk_idx[t, j]], divided by (sum over j + 1e-20) when
+ *   renormalize != 0 and top_k > 1, then multiplied by routed_scaling_factor.
+ * logits [N, E] fp32 (the caller's x . W_gate^T, fp32 as in the reference), bias [E] fp32;
+ * topk_idx [N, top_k] int64 and topk_w [N, top_k] fp32, the dtypes the routed-layer entry
+ * points take. 1 <= top_k <= min(E, 64), E <= 4096. */
+int mxfp4_router_topk(int64_t *topk_idx, float *topk_w, const float *logits, const float *bias, int N,
+                      int E, int top_k, float routed_scaling_factor, int renormalize,
+                      hipStream_t stream);
+
+/* Gradient of mxfp4_router_topk's weights with respect to its logits: the autograd of the
+ * torch branch (lazy_lora/core/moe_router.py:86-98) that carries dL/dtopk_w back into the
+ * router's input (lazy_lora/trainer/lazy_trainer.py:842-844). grad_logits [N, E] fp32 is fully
+ * written: sigmoid'(logit) times the derivative of the renormalised, scaled weights for the
+ * chosen experts, 0 elsewhere. topk_idx [N, top_k] int64 as produced by mxfp4_router_topk;
+ * grad_w [N, top_k] fp32. Same limits as mxfp4_router_topk. */
+int mxfp4_router_topk_backward(float *grad_logits, const int64_t *topk_idx, const float *grad_w,
+                               const float *logits, int N, int E, int top_k,
+                               float routed_scaling_factor, int renormalize, hipStream_t stream);
+
 /* Phase timing of the routed-layer calls made on the calling thread, the counterpart of the
  * reference's LAZYLORA_PROFILE timings (lazy_lora/trainer/lazy_trainer.py:192-194). While
  * enabled, every mxfp4_moe_forward/backward call records HIP events on its stream around

@@ -388,6 +388,34 @@ int mxfp4_moe_phase_times(int call, float* ms, const char** names, int max_phase
   return n;
 }
 
+int mxfp4_router_topk(int64_t* topk_idx, float* topk_w, const float* logits, const float* bias, int N, int E,
+                      int top_k, float routed_scaling_factor, int renormalize, hipStream_t stream)
+{
+  if (N < 0 || E <= 0 || E > 4096) return fail(MXFP4_EINVAL, "router_topk: need 0 < E <= 4096 and N >= 0%s");
+  if (top_k < 1 || top_k > E || top_k > 64) return fail(MXFP4_EINVAL, "router_topk: need 1 <= top_k <= min(E, 64)%s");
+  if (N == 0) return MXFP4_OK;
+  if (!topk_idx || !topk_w || !logits) return fail(MXFP4_EINVAL, "router_topk: null pointer%s");
+  MX_TRY(mx::launch_router_topk(reinterpret_cast<long long*>(topk_idx), topk_w, logits, bias, N, E, top_k,
+                                routed_scaling_factor, renormalize, stream),
+         "router_topk");
+  return MXFP4_OK;
+}
+
+int mxfp4_router_topk_backward(float* grad_logits, const int64_t* topk_idx, const float* grad_w, const float* logits,
+                               int N, int E, int top_k, float routed_scaling_factor, int renormalize,
+                               hipStream_t stream)
+{
+  if (N < 0 || E <= 0 || E > 4096) return fail(MXFP4_EINVAL, "router_topk_backward: need 0 < E <= 4096 and N >= 0%s");
+  if (top_k < 1 || top_k > E || top_k > 64)
+    return fail(MXFP4_EINVAL, "router_topk_backward: need 1 <= top_k <= min(E, 64)%s");
+  if (N == 0) return MXFP4_OK;
+  if (!grad_logits || !topk_idx || !grad_w || !logits) return fail(MXFP4_EINVAL, "router_topk_backward: null pointer%s");
+  MX_TRY(mx::launch_router_topk_bwd(grad_logits, reinterpret_cast<const long long*>(topk_idx), grad_w, logits, N, E,
+                                    top_k, routed_scaling_factor, renormalize, stream),
+         "router_topk_backward");
+  return MXFP4_OK;
+}
+
 int mxfp4_moe_route_status(const void* workspace, int* host_flags, hipStream_t stream)
 {
   if (!workspace || !host_flags) return fail(MXFP4_EINVAL, "route_status: null pointer%s");

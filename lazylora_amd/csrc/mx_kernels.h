@@ -102,5 +102,12 @@ hipError_t launch_combine_bwd(float* grad_h, float* grad_w, const float* dxpair,
                               const float* gw_part, int n_ct, const int* pair_of, int N, int k, int D,
                               hipStream_t s);
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+// Router selection (sigmoid, bias, top-k, renormalise, scale), one wave per token.
+hipError_t launch_router_topk(long long* topk_idx, float* topk_w, const float* logits, const float* bias, int N,
+                              int E, int top_k, float scale, int renormalize, hipStream_t s);
+hipError_t launch_router_topk_bwd(float* grad_logits, const long long* topk_idx, const float* grad_w,
+                                  const float* logits, int N, int E, int top_k, float scale, int renormalize,
+                                  hipStream_t s);
+
 
 }  // namespace mx

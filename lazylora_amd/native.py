@@ -70,6 +70,10 @@ def _load_library() -> ctypes.CDLL:
                                        ci, ci, ci, ci, ci, vp, sz, vp]
     lib.mxfp4_moe_route_status.restype = ci
     lib.mxfp4_moe_route_status.argtypes = [vp, vp, vp]
+    lib.mxfp4_router_topk.restype = ci
+    lib.mxfp4_router_topk.argtypes = [vp, vp, vp, vp, ci, ci, ci, ctypes.c_float, ci, vp]
+    lib.mxfp4_router_topk_backward.restype = ci
+    lib.mxfp4_router_topk_backward.argtypes = [vp, vp, vp, vp, ci, ci, ci, ctypes.c_float, ci, vp]
     lib.mxfp4_moe_timing.restype = ci
     lib.mxfp4_moe_timing.argtypes = [ci]
     lib.mxfp4_moe_timed_calls.restype = ci
@@ -211,6 +215,59 @@ class MXFP4Kernel:
             experts.E, call.D, call.F, call.act, MOE_REUSE_FORWARD if reuse_forward else 0,
             call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
         return grad_h, grad_w
+
+    # -- router ----------------------------------------------------------------------------
+    def router_topk(self, logits: torch.Tensor, bias: Optional[torch.Tensor], top_k: int,
+                    routed_scaling_factor: float = 1.0,
+                    renormalize: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(topk_idx [N, k] int64, topk_w [N, k] fp32) from gate logits [N, E] on the GPU: the
+        selection of KimiK3MoERouter.forward (lazy_lora/core/moe_router.py:86-99)."""
+        lg, N, E = self._logits(logits)
+        self._router_limits(E, top_k)
+        b = None
+        if bias is not None:
+            if tuple(bias.shape) != (E,):
+                raise ValueError(f"bias must be [{E}], got {tuple(bias.shape)}")
+            b = bias.to(lg.device, non_blocking=True).contiguous().float()
+        idx = torch.empty((N, top_k), dtype=torch.int64, device=lg.device)
+        w = torch.empty((N, top_k), dtype=torch.float32, device=lg.device)
+        _check(self.lib.mxfp4_router_topk(idx.data_ptr(), w.data_ptr(), lg.data_ptr(),
+                                          b.data_ptr() if b is not None else None, N, E, top_k,
+                                          float(routed_scaling_factor), 1 if renormalize else 0,
+                                          _stream(lg.device)), self.lib)
+        return idx, w
+
+    def router_topk_backward(self, logits: torch.Tensor, topk_idx: torch.Tensor, grad_w: torch.Tensor,
+                             routed_scaling_factor: float = 1.0, renormalize: bool = True) -> torch.Tensor:
+        """dL/dlogits [N, E] fp32 for dL/dtopk_w [N, k] (the autograd of moe_router.py:86-98)."""
+        lg, N, E = self._logits(logits)
+        if topk_idx.dim() != 2 or topk_idx.shape[0] != N:
+            raise ValueError(f"topk_idx must be [{N}, k], got {tuple(topk_idx.shape)}")
+        top_k = topk_idx.shape[1]
+        self._router_limits(E, top_k)
+        if tuple(grad_w.shape) != tuple(topk_idx.shape):
+            raise ValueError("grad_w and topk_idx must have the same shape")
+        idx = topk_idx.to(lg.device, non_blocking=True).contiguous().long()
+        g = grad_w.to(lg.device, non_blocking=True).contiguous().float()
+        out = torch.empty((N, E), dtype=torch.float32, device=lg.device)
+        _check(self.lib.mxfp4_router_topk_backward(out.data_ptr(), idx.data_ptr(), g.data_ptr(), lg.data_ptr(),
+                                                   N, E, top_k, float(routed_scaling_factor),
+                                                   1 if renormalize else 0, _stream(lg.device)), self.lib)
+        return out
+
+    @staticmethod
+    def _logits(logits: torch.Tensor):
+        if logits.dim() != 2:
+            raise ValueError(f"logits must be [N, E], got {tuple(logits.shape)}")
+        dev = _device_for(logits)
+        return logits.to(dev, non_blocking=True).contiguous().float(), logits.shape[0], logits.shape[1]
+
+    @staticmethod
+    def _router_limits(E: int, top_k: int) -> None:
+        if not 0 < E <= 4096:
+            raise ValueError(f"the router kernel takes 1..4096 experts, got {E}")
+        if not 1 <= top_k <= min(E, 64):
+            raise ValueError(f"top_k must lie in [1, min(E, 64)] = [1, {min(E, 64)}], got {top_k}")
 
     def moe_workspace_bytes(self, N: int, k: int, E: int, D: int, F: int) -> int:
         return int(self.lib.mxfp4_moe_workspace_size(N, k, E, D, F))

@@ -111,18 +111,46 @@ def glu_backward(grad, gate, up, act: str):
 
 
 # ------------------------------------------------------------------------------------ router
-def router_forward(x, gate_weight, bias=None, top_k=2, routed_scaling_factor=1.0, renormalize=True):
-    """KimiK3MoERouter.forward, NumPy branch (lazy_lora/core/moe_router.py:102-123): sigmoid
-    scores, bias added for selection only, top-k, gather unbiased scores, renormalise (+1e-20),
-    scale. Returns (indices [N, k] int64, weights [N, k] float64)."""
-    x = np.asarray(x, np.float64).reshape(-1, gate_weight.shape[1])
-    scores = _sigmoid(x @ np.asarray(gate_weight, np.float64).T)
+def router_select(logits, bias=None, top_k=2, routed_scaling_factor=1.0, renormalize=True):
+    """The selection half of KimiK3MoERouter.forward on given logits [N, E]
+    (lazy_lora/core/moe_router.py:106-123): sigmoid scores, bias added for selection only,
+    top-k (stable: equal choices go to the lower expert id), gather unbiased scores,
+    renormalise (+1e-20) when top_k > 1, scale. Returns (indices [N, k] int64, weights float64)."""
+    scores = _sigmoid(np.asarray(logits, np.float64))
     choice = scores + np.asarray(bias, np.float64) if bias is not None else scores
     idx = np.argsort(-choice, axis=-1, kind="stable")[:, :top_k]
     w = np.take_along_axis(scores, idx, axis=-1)
     if top_k > 1 and renormalize:
         w = w / (w.sum(-1, keepdims=True) + 1e-20)
     return idx.astype(np.int64), w * routed_scaling_factor
+
+
+def router_forward(x, gate_weight, bias=None, top_k=2, routed_scaling_factor=1.0, renormalize=True):
+    """KimiK3MoERouter.forward, NumPy branch (lazy_lora/core/moe_router.py:102-123): logits =
+    x . W^T, then router_select. Returns (indices [N, k] int64, weights [N, k] float64)."""
+    x = np.asarray(x, np.float64).reshape(-1, gate_weight.shape[1])
+    logits = x @ np.asarray(gate_weight, np.float64).T
+    return router_select(logits, bias, top_k, routed_scaling_factor, renormalize)
+
+
+def router_select_backward(logits, idx, grad_w, routed_scaling_factor=1.0, renormalize=True):
+    """dL/dlogits [N, E] for upstream dL/dweights grad_w [N, k], the closed-form derivative of
+    router_select at fixed indices (what torch autograd computes through moe_router.py:86-98):
+    with s the chosen scores, S = sum s + 1e-20 and c the scale, dL/ds_i = c (g_i / S -
+    sum_j g_j s_j / S^2) when renormalising (top_k > 1), else c g_i; dL/dlogit_i = dL/ds_i s_i
+    (1 - s_i); unchosen experts get 0."""
+    logits = np.asarray(logits, np.float64)
+    idx = np.asarray(idx, np.int64)
+    g = np.asarray(grad_w, np.float64)
+    s = _sigmoid(np.take_along_axis(logits, idx, axis=-1))
+    if idx.shape[1] > 1 and renormalize:
+        den = s.sum(-1, keepdims=True) + 1e-20
+        ds = routed_scaling_factor * (g / den - (g * s).sum(-1, keepdims=True) / den ** 2)
+    else:
+        ds = routed_scaling_factor * g
+    out = np.zeros_like(logits)
+    np.put_along_axis(out, idx, ds * s * (1.0 - s), axis=-1)
+    return out
 
 
 def rms_norm(x, weight, eps=1e-5):

@@ -55,6 +55,13 @@ def test_host_side_argument_errors(lib):
     assert lib.mxfp4_moe_forward(*bad, 0, 0, dummy, 1 << 40, None) == -1    # D % 32 != 0
     unaligned = [dummy, dummy, 0, dummy, 3, dummy, 4, 2, vp(257)] + [dummy] * 5 + [8, 64, 32]
     assert lib.mxfp4_moe_forward(*unaligned, 0, 0, dummy, 1 << 40, None) == -1
+    assert lib.mxfp4_router_topk(dummy, dummy, dummy, None, 4, 100, 65, 1.0, 1, None) == -1  # top_k > 64
+    assert b"top_k" in lib.mxfp4_last_error()
+    assert lib.mxfp4_router_topk(dummy, dummy, dummy, None, 4, 100, 0, 1.0, 1, None) == -1
+    assert lib.mxfp4_router_topk(dummy, dummy, dummy, None, 4, 4097, 8, 1.0, 1, None) == -1  # E > 4096
+    assert lib.mxfp4_router_topk(None, dummy, dummy, None, 4, 100, 8, 1.0, 1, None) == -1    # null output
+    assert lib.mxfp4_router_topk(None, None, None, None, 0, 100, 8, 1.0, 1, None) == 0       # N = 0: no-op
+    assert lib.mxfp4_router_topk_backward(dummy, dummy, dummy, dummy, 4, 8, 9, 1.0, 1, None) == -1
 
 
 def test_python_api_validation():

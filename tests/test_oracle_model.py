@@ -72,6 +72,45 @@ def test_router_fixture():
     assert changed == fx["rows_where_bias_changed_selection"]
 
 
+@pytest.mark.parametrize("top_k,renorm,scale", [(4, True, 1.0), (4, True, 2.5), (4, False, 1.0), (1, True, 1.0)])
+def test_router_select_backward_central_differences(top_k, renorm, scale):
+    """The closed-form router gradient against central differences of router_select with the
+    selection held fixed (every finite-difference step keeps the same top-k)."""
+    rng = np.random.default_rng(5)
+    N, E = 3, 12
+    logits = rng.standard_normal((N, E))
+    bias = 0.1 * rng.standard_normal(E)
+    idx, _ = oracle.router_select(logits, bias, top_k, scale, renorm)
+    g = rng.standard_normal((N, top_k))
+    got = oracle.router_select_backward(logits, idx, g, scale, renorm)
+    eps = 1e-6
+    fd = np.zeros_like(logits)
+    for n in range(N):
+        for e in range(E):
+            lp, lm = logits.copy(), logits.copy()
+            lp[n, e] += eps
+            lm[n, e] -= eps
+            ip, wp = oracle.router_select(lp, bias, top_k, scale, renorm)
+            im, wm = oracle.router_select(lm, bias, top_k, scale, renorm)
+            assert (ip == idx).all() and (im == idx).all()
+            fd[n, e] = ((wp - wm) * g).sum() / (2 * eps)
+    assert np.allclose(got, fd, rtol=1e-6, atol=1e-9)
+    unchosen = np.ones_like(logits, bool)
+    np.put_along_axis(unchosen, idx, False, axis=-1)
+    assert (got[unchosen] == 0).all()
+
+
+def test_router_select_ties_and_bias_only_in_selection():
+    """Equal choices go to the lower expert id (a stable descending sort), and the weights are
+    the unbiased scores: a huge bias on one expert selects it without changing its weight."""
+    logits = np.zeros((1, 6))
+    idx, w = oracle.router_select(logits, None, 3, 1.0, False)
+    assert idx.tolist() == [[0, 1, 2]] and np.allclose(w, 0.5)
+    bias = np.array([0, 0, 0, 0, 0, 100.0])
+    idx, w = oracle.router_select(logits, bias, 2, 1.0, False)
+    assert idx.tolist() == [[5, 0]] and np.allclose(w, 0.5)
+
+
 def test_moe_block_fixture():
     """The latent MoE block of moe.json through the oracle's routed composition with the
     fixture's dense expert weights (they are not MXFP4-representable)."""
