@@ -107,6 +107,36 @@ int mxfp4_moe_backward(float *grad_h, float *grad_w, const float *grad_out, cons
                        int F, int act_kind, int flags, void *workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
+/* The routed layer with the layer's LoRA adapters, which all its experts share
+ * (lazy_lora/trainer/lazy_trainer.py:130-134), applied as the reference applies them per expert
+ * (_expert_forward, lazy_trainer.py:762-791; LazyLoRALinear.forward_lora_only,
+ * lazy_lora/core/lora_layer.py:104-139; dropout off, as the reference's config sets it):
+ *   gate = x W1^T + s_g (x A_g^T) B_g^T, up likewise with A_u, B_u, act = GLU(gate, up),
+ *   down = act W2^T + s_d (act A_d^T) B_d^T.
+ * lora: host array of 6 DEVICE pointers, fp32 row-major: A_gate [r, D], B_gate [F, r],
+ * A_up [r, D], B_up [F, r], A_down [r, F], B_down [D, r]; NULL = LoRA off (then these calls are
+ * mxfp4_moe_forward / mxfp4_moe_backward). lora_scaling: host array {s_g, s_u, s_d}
+ * (lora_alpha / r). 1 <= lora_rank <= 32.
+ * The backward also writes the adapter gradients (lora_layer.py:178-226 summed over the
+ * experts, the sum the reference accumulates with accumulate_grad, lazy_trainer.py:866-876)
+ * into lora_grads: host array of 6 device pointers shaped like `lora`, overwritten.
+ * MXFP4_MOE_REUSE_FORWARD needs a forward made with MXFP4_MOE_SAVE and the same adapters. */
+int mxfp4_moe_forward_lora(float *out, const void *h, int h_dtype, const void *topk_idx,
+                           int idx_dtype, const float *topk_w, int N, int k, const uint8_t *w1p,
+                           const uint8_t *w1s, const uint8_t *w3p, const uint8_t *w3s,
+                           const uint8_t *w2p, const uint8_t *w2s, int E, int D, int F,
+                           int act_kind, const float *const *lora, const float *lora_scaling,
+                           int lora_rank, int flags, void *workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+int mxfp4_moe_backward_lora(float *grad_h, float *grad_w, const float *grad_out, const void *h,
+                            int h_dtype, const void *topk_idx, int idx_dtype,
+                            const float *topk_w, int N, int k, const uint8_t *w1p,
+                            const uint8_t *w1s, const uint8_t *w3p, const uint8_t *w3s,
+                            const uint8_t *w2p, const uint8_t *w2s, int E, int D, int F,
+                            int act_kind, const float *const *lora, const float *lora_scaling,
+                            int lora_rank, float *const *lora_grads, int flags, void *workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
 /* Copies the routing status word of a routed-layer workspace to *host_flags after
  * synchronising `stream`: bit 0 set = some topk_idx entry was outside [0, E). */
 int mxfp4_moe_route_status(const void *workspace, int *host_flags, hipStream_t stream);

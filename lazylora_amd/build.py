@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblazylora_mxfp4.so")
-SOURCES = ["capi.hip", "mx_forward.hip", "mx_backward.hip", "mx_misc.hip", "mx_router.hip"]
+SOURCES = ["capi.hip", "mx_forward.hip", "mx_backward.hip", "mx_misc.hip", "mx_router.hip", "mx_lora.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

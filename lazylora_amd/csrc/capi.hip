@@ -3,6 +3,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "../../include/lazylora_mxfp4.h"
 #include "mx_device.h"
 #include "mx_kernels.h"
@@ -36,7 +38,7 @@ int hip_fail(hipError_t e, const char* where)
 // are read, so timing can stay on inside a timed loop.
 struct PhaseTimer {
   static constexpr int kRing = 128;
-  static constexpr int kMaxPhases = 12;
+  static constexpr int kMaxPhases = 16;
   bool on = false;
   int calls = 0;  // calls recorded since enabled
   int cur = -1;   // ring slot of the call in progress
@@ -95,7 +97,9 @@ long long pad32(long long v) { return (v + 31) / 32 * 32; }
 struct MoeLayout {
   size_t meta, counts, offsets, cursor, tiles, pair_token, pair_w, pair_of;
   size_t at_x, at_act;
-  size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part, end;
+  size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part;
+  size_t l_u, l_delta, l_v, l_vsum, l_q, l_rq, l_dh, l_dsum, l_part;  // LoRA (rank <= kLoraMaxRank)
+  size_t end;
   int max_tiles, n_ct_bwd;
 };
 
@@ -123,6 +127,19 @@ MoeLayout moe_layout(int N, int k, int E, int D, int F)
   L.d_hi = o; o = align_up(o + 2 * (size_t)(P * 2 * F));
   L.d_lo = o; o = align_up(o + 2 * (size_t)(P * 2 * F));
   L.gw_part = o; o = align_up(o + sizeof(float) * (size_t)(P * L.n_ct_bwd));
+  const size_t R = mx::kLoraMaxRank;
+  L.l_u = o; o = align_up(o + sizeof(float) * (size_t)N * 2 * R);
+  L.l_delta = o; o = align_up(o + sizeof(float) * (size_t)N * 2 * F);
+  L.l_v = o; o = align_up(o + sizeof(float) * (size_t)P * R);
+  L.l_vsum = o; o = align_up(o + sizeof(float) * (size_t)N * R);
+  L.l_q = o; o = align_up(o + sizeof(float) * (size_t)N * R);
+  L.l_rq = o; o = align_up(o + sizeof(float) * (size_t)N * F);
+  L.l_dh = o; o = align_up(o + sizeof(float) * (size_t)P * 2 * R);
+  L.l_dsum = o; o = align_up(o + sizeof(float) * (size_t)N * 2 * R);
+  size_t part = mx::lora_outer_partial_floats(N, 2 * (int)R, D);
+  part = std::max(part, mx::lora_outer_partial_floats((int)P, (int)R, F));
+  part = std::max(part, mx::lora_outer_partial_floats((int)P, (int)R, 2 * F));
+  L.l_part = o; o = align_up(o + sizeof(float) * part);
   L.end = o;
   return L;
 }
@@ -147,10 +164,39 @@ int check_moe_args(const void* h, int h_dtype, const void* idx, int idx_dtype, c
   return MXFP4_OK;
 }
 
-// Routing + quantised x + gate/up (+GLU) into the workspace.
+// The layer's LoRA adapters, shared by all its experts (lazy_trainer.py:130-134).
+struct Lora {
+  const float* m[6] = {};  // A_gate [r, D], B_gate [F, r], A_up [r, D], B_up [F, r], A_down [r, F], B_down [D, r]
+  float sg = 0.f, su = 0.f, sd = 0.f;  // alpha / r of gate, up, down
+  int r = 0;                           // 0: LoRA off
+};
+
+int check_lora(const float* const* lora, const float* scaling, int rank, Lora& lo)
+{
+  lo = Lora{};
+  if (!lora) return MXFP4_OK;
+  if (rank < 1 || rank > mx::kLoraMaxRank) return fail(MXFP4_EINVAL, "moe: LoRA rank must lie in [1, 32]%s");
+  if (!scaling) return fail(MXFP4_EINVAL, "moe: null LoRA scaling%s");
+  for (int i = 0; i < 6; ++i) {
+    if (!lora[i]) return fail(MXFP4_EINVAL, "moe: null LoRA factor%s");
+    lo.m[i] = lora[i];
+  }
+  lo.sg = scaling[0]; lo.su = scaling[1]; lo.sd = scaling[2];
+  lo.r = rank;
+  return MXFP4_OK;
+}
+
+mx::LoraMat mat_f32(const void* p, long long ld) { return mx::LoraMat{mx::kLoraF32, p, nullptr, ld, 0, 0}; }
+mx::LoraFactor jmajor(const float* m, long long ld, float scale) { return mx::LoraFactor{m, ld, 0, scale}; }
+mx::LoraFactor kmajor(const float* m, long long ld, float scale) { return mx::LoraFactor{m, ld, 1, scale}; }
+
+// Routing + quantised x + gate/up (+GLU) into the workspace. With LoRA also the per-token
+// adapter inputs U = [A_gate x | A_up x], their gate/up deltas (added in the product's
+// epilogue), v = A_down act per pair and V = sum over a token's slots of w * v; gate|up are
+// then always saved, since v and the backward read them.
 int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const float* w, int N, int k,
-              const uint8_t* const* wts, int E, int D, int F, int act_kind, bool save, void* ws, const MoeLayout& L,
-              hipStream_t s)
+              const uint8_t* const* wts, int E, int D, int F, int act_kind, bool save, const Lora& lo, void* ws,
+              const MoeLayout& L, hipStream_t s)
 {
   const long long P = (long long)N * k;
   MX_TRY(mx::launch_route(idx, idx_dtype == MXFP4_I64, w, N, k, E, at<int>(ws, L.counts), at<int>(ws, L.offsets),
@@ -174,11 +220,35 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   a.tiles = at<int4>(ws, L.tiles); a.n_tiles = at<int>(ws, L.meta);
   a.n_ct = F / 32;
   a.q_tiles = at<uint8_t>(ws, L.at_act);
-  a.save = save ? at<float>(ws, L.saved) : nullptr;
+  a.save = (save || lo.r) ? at<float>(ws, L.saved) : nullptr;
   a.act_kind = act_kind;
-  (void)P;
+  const int r = lo.r;
+  if (r) {
+    const mx::LoraMat x{h_dtype == MXFP4_BF16 ? mx::kLoraBF16 : mx::kLoraF32, h, nullptr, D, 0, 0};
+    const mx::LoraFactor fa[2] = {jmajor(lo.m[0], D, 1.f), jmajor(lo.m[2], D, 1.f)};
+    const int koff[2] = {0, 0};
+    MX_TRY(mx::launch_lora_rowdot(x, N, nullptr, D, r, 2, fa, koff, at<float>(ws, L.l_u), s), "LoRA: A x");
+    const mx::LoraFactor fb[2] = {kmajor(lo.m[1], r, lo.sg), kmajor(lo.m[3], r, lo.su)};
+    const int coff[2] = {0, r}, col0[2] = {0, F}, ncol[2] = {F, F};
+    MX_TRY(mx::launch_lora_expand(at<float>(ws, L.l_u), 2 * r, N, r, 2, fb, coff, col0, ncol,
+                                  at<float>(ws, L.l_delta), 2LL * F, 2 * F, 0, s),
+           "LoRA: gate/up deltas");
+    a.row_token = at<int>(ws, L.pair_token);
+    a.lora_delta = at<float>(ws, L.l_delta);
+    MX_PHASE("lora_in", s);
+  }
   MX_TRY(mx::launch_fwd(a, mx::kFwdGateUp, L.max_tiles, s), "gate/up product");
   MX_PHASE("fwd_gateup", s);
+  if (r) {
+    const mx::LoraMat act{mx::kLoraGLU, at<float>(ws, L.saved), nullptr, 2LL * F, F, act_kind};
+    const mx::LoraFactor fd = jmajor(lo.m[4], F, 1.f);
+    const int koff = 0;
+    MX_TRY(mx::launch_lora_rowdot(act, (int)P, at<int>(ws, L.offsets) + E, F, r, 1, &fd, &koff, at<float>(ws, L.l_v), s),
+           "LoRA: A_down act");
+    MX_TRY(mx::launch_lora_slot_sum(at<float>(ws, L.l_v), r, at<int>(ws, L.pair_of), w, N, k, at<float>(ws, L.l_vsum), s),
+           "LoRA: slot sum");
+    MX_PHASE("lora_mid", s);
+  }
   return MXFP4_OK;
 }
 
@@ -272,13 +342,17 @@ size_t mxfp4_moe_workspace_size(int N, int k, int E, int D, int F)
   return moe_layout(N, k, E, D, F).end;
 }
 
-int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
-                      const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p,
-                      const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, int E, int D, int F, int act_kind,
-                      int flags, void* workspace, size_t workspace_bytes, hipStream_t stream)
+int mxfp4_moe_forward_lora(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
+                           const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s,
+                           const uint8_t* w3p, const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, int E,
+                           int D, int F, int act_kind, const float* const* lora, const float* lora_scaling,
+                           int lora_rank, int flags, void* workspace, size_t workspace_bytes, hipStream_t stream)
 {
   const uint8_t* wts[6] = {w1p, w1s, w3p, w3s, w2p, w2s};
   int rc = check_moe_args(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind);
+  if (rc) return rc;
+  Lora lo;
+  rc = check_lora(lora, lora_scaling, lora_rank, lo);
   if (rc) return rc;
   if (N > 0 && !out) return fail(MXFP4_EINVAL, "moe_forward: null output%s");
   const MoeLayout L = moe_layout(N, k, E, D, F);
@@ -286,7 +360,7 @@ int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_i
   if (N == 0) return MXFP4_OK;
   MX_TRY(g_timer.begin(stream), "phase timer");
   rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, (flags & MXFP4_MOE_SAVE) != 0,
-                 workspace, L, stream);
+                 lo, workspace, L, stream);
   if (rc) return rc;
   mx::FwdArgs a = {};
   a.wp0 = w2p; a.ws0 = w2s;
@@ -303,25 +377,60 @@ int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_i
   MX_TRY(mx::launch_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D, stream),
          "moe_forward: combine");
   MX_PHASE("fwd_combine", stream);
+  if (lo.r) {  // out += s_down B_down V, V = sum over the token's slots of w A_down act
+    const mx::LoraFactor fb = kmajor(lo.m[5], lo.r, lo.sd);
+    const int coff = 0, col0 = 0, ncol = D;
+    MX_TRY(mx::launch_lora_expand(at<float>(workspace, L.l_vsum), lo.r, N, lo.r, 1, &fb, &coff, &col0, &ncol, out, D,
+                                  D, 1, stream),
+           "moe_forward: LoRA down");
+    MX_PHASE("lora_out", stream);
+  }
   return MXFP4_OK;
 }
 
-int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, const void* h, int h_dtype,
-                       const void* topk_idx, int idx_dtype, const float* topk_w, int N, int k, const uint8_t* w1p,
-                       const uint8_t* w1s, const uint8_t* w3p, const uint8_t* w3s, const uint8_t* w2p,
-                       const uint8_t* w2s, int E, int D, int F, int act_kind, int flags, void* workspace,
-                       size_t workspace_bytes, hipStream_t stream)
+int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
+                      const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p,
+                      const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, int E, int D, int F, int act_kind,
+                      int flags, void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+  return mxfp4_moe_forward_lora(out, h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, w1p, w1s, w3p, w3s, w2p, w2s, E,
+                                D, F, act_kind, nullptr, nullptr, 0, flags, workspace, workspace_bytes, stream);
+}
+
+int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out, const void* h, int h_dtype,
+                            const void* topk_idx, int idx_dtype, const float* topk_w, int N, int k,
+                            const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p, const uint8_t* w3s,
+                            const uint8_t* w2p, const uint8_t* w2s, int E, int D, int F, int act_kind,
+                            const float* const* lora, const float* lora_scaling, int lora_rank,
+                            float* const* lora_grads, int flags, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream)
 {
   const uint8_t* wts[6] = {w1p, w1s, w3p, w3s, w2p, w2s};
   int rc = check_moe_args(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind);
   if (rc) return rc;
+  Lora lo;
+  rc = check_lora(lora, lora_scaling, lora_rank, lo);
+  if (rc) return rc;
+  if (lo.r) {
+    if (!lora_grads) return fail(MXFP4_EINVAL, "moe_backward: null LoRA gradient array%s");
+    for (int i = 0; i < 6; ++i)
+      if (!lora_grads[i]) return fail(MXFP4_EINVAL, "moe_backward: null LoRA gradient%s");
+  }
   if (N > 0 && (!grad_h || !grad_w || !grad_out)) return fail(MXFP4_EINVAL, "moe_backward: null pointer%s");
   const MoeLayout L = moe_layout(N, k, E, D, F);
   if (!workspace || workspace_bytes < L.end) return fail(MXFP4_EWORKSPACE, "moe_backward: workspace too small%s");
-  if (N == 0) return MXFP4_OK;
+  if (N == 0) {
+    if (lo.r) {  // no tokens: the adapter gradients are zero
+      const size_t n[6] = {(size_t)lo.r * D, (size_t)F * lo.r, (size_t)lo.r * D, (size_t)F * lo.r, (size_t)lo.r * F,
+                           (size_t)D * lo.r};
+      for (int i = 0; i < 6; ++i) MX_TRY(mx::launch_zero(lora_grads[i], n[i] * sizeof(float), stream), "zero grads");
+    }
+    return MXFP4_OK;
+  }
   MX_TRY(g_timer.begin(stream), "phase timer");
   if (!(flags & MXFP4_MOE_REUSE_FORWARD)) {
-    rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, true, workspace, L, stream);
+    rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, true, lo, workspace, L,
+                   stream);
     if (rc) return rc;
   }
   // grad_out -> bf16 hi + lo, the A operand of the W2 transposed product
@@ -329,6 +438,20 @@ int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, cons
                                stream),
          "moe_backward: split grad_out");
   MX_PHASE("split_grad", stream);
+  const int r = lo.r;
+  if (r) {  // q = s_down B_down^T g per token, and its expansion A_down^T q for the W2 epilogue
+    const mx::LoraFactor fb = kmajor(lo.m[5], r, lo.sd);
+    const int koff = 0;
+    MX_TRY(mx::launch_lora_rowdot(mat_f32(grad_out, D), N, nullptr, D, r, 1, &fb, &koff, at<float>(workspace, L.l_q),
+                                  stream),
+           "moe_backward: LoRA B_down^T g");
+    const mx::LoraFactor fa = jmajor(lo.m[4], F, 1.f);
+    const int coff = 0, col0 = 0, ncol = F;
+    MX_TRY(mx::launch_lora_expand(at<float>(workspace, L.l_q), r, N, r, 1, &fa, &coff, &col0, &ncol,
+                                  at<float>(workspace, L.l_rq), F, F, 0, stream),
+           "moe_backward: LoRA A_down^T q");
+    MX_PHASE("lora_q", stream);
+  }
   mx::BwdArgs b = {};
   b.wp0 = w2p; b.ws0 = w2s;
   b.wp_estride = (long long)F * D / 2;
@@ -343,6 +466,7 @@ int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, cons
   b.act_kind = act_kind;
   b.d_hi = at<uint16_t>(workspace, L.d_hi); b.d_lo = at<uint16_t>(workspace, L.d_lo);
   b.gw_part = at<float>(workspace, L.gw_part);
+  b.lora_rq = r ? at<float>(workspace, L.l_rq) : nullptr;
   MX_TRY(mx::launch_bwd(b, mx::kBwdDownT, L.max_tiles, stream), "moe_backward: W2 transposed product");
   MX_PHASE("bwd_down_t", stream);
 
@@ -361,7 +485,72 @@ int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, cons
                                 L.n_ct_bwd, at<int>(workspace, L.pair_of), N, k, D, stream),
          "moe_backward: combine");
   MX_PHASE("bwd_combine", stream);
+  if (r) {
+    float* ws_f = at<float>(workspace, L.l_part);
+    const long long P = (long long)N * k;
+    const int* n_valid = at<int>(workspace, L.offsets) + E;
+    // dh = [s_gate B_gate^T d_gate | s_up B_up^T d_up] per pair, summed over each token's slots
+    const mx::LoraMat dmat{mx::kLoraHiLo, at<uint16_t>(workspace, L.d_hi), at<uint16_t>(workspace, L.d_lo), 2LL * F, 0,
+                           0};
+    const mx::LoraFactor fb[2] = {kmajor(lo.m[1], r, lo.sg), kmajor(lo.m[3], r, lo.su)};
+    const int koff[2] = {0, F};
+    MX_TRY(mx::launch_lora_rowdot(dmat, (int)P, n_valid, F, r, 2, fb, koff, at<float>(workspace, L.l_dh), stream),
+           "moe_backward: LoRA B^T d");
+    MX_TRY(mx::launch_lora_slot_sum(at<float>(workspace, L.l_dh), 2 * r, at<int>(workspace, L.pair_of), nullptr, N, k,
+                                    at<float>(workspace, L.l_dsum), stream),
+           "moe_backward: LoRA slot sum");
+    // grad_h += A_gate^T Dg + A_up^T Du
+    const mx::LoraFactor fa[2] = {jmajor(lo.m[0], D, 1.f), jmajor(lo.m[2], D, 1.f)};
+    const int coff[2] = {0, r}, col0[2] = {0, 0}, ncol[2] = {D, D};
+    MX_TRY(mx::launch_lora_expand(at<float>(workspace, L.l_dsum), 2 * r, N, r, 2, fa, coff, col0, ncol, grad_h, D, D,
+                                  1, stream),
+           "moe_backward: LoRA grad_h");
+    MX_PHASE("lora_dx", stream);
+    // adapter gradients (lora_layer.py:178-226, summed over the experts)
+    const mx::LoraMat x{h_dtype == MXFP4_BF16 ? mx::kLoraBF16 : mx::kLoraF32, h, nullptr, D, 0, 0};
+    const mx::LoraMat act{mx::kLoraGLU, at<float>(workspace, L.saved), nullptr, 2LL * F, F, act_kind};
+    mx::LoraOuterDst d = {};
+    // A_gate / A_up: sum over tokens of [Dg | Du] (x) x
+    d.p[0] = lora_grads[0]; d.ld[0] = D; d.kmajor[0] = 0; d.scale[0] = 1.f;
+    d.p[1] = lora_grads[2]; d.ld[1] = D; d.kmajor[1] = 0; d.scale[1] = 1.f;
+    d.split_j = r;
+    MX_TRY(mx::launch_lora_outer(x, N, nullptr, k, nullptr, at<float>(workspace, L.l_dsum), 2 * r, 2 * r, 0, 0, D, ws_f,
+                                 d, stream),
+           "moe_backward: LoRA grad A_gate/A_up");
+    // B_gate / B_up: s * sum over pairs of [d_gate | d_up] (x) U of the pair's token
+    d = {};
+    d.p[0] = lora_grads[1]; d.ld[0] = r; d.kmajor[0] = 1; d.scale[0] = lo.sg;
+    d.p[1] = lora_grads[3]; d.ld[1] = r; d.kmajor[1] = 1; d.scale[1] = lo.su;
+    d.split_c = F;
+    MX_TRY(mx::launch_lora_outer(dmat, (int)P, at<int>(workspace, L.pair_of), k, nullptr, at<float>(workspace, L.l_u),
+                                 2 * r, r, F, r, 2 * F, ws_f, d, stream),
+           "moe_backward: LoRA grad B_gate/B_up");
+    // A_down: sum over pairs of w q(token) (x) act
+    d = {};
+    d.p[0] = lora_grads[4]; d.ld[0] = F; d.kmajor[0] = 0; d.scale[0] = 1.f;
+    MX_TRY(mx::launch_lora_outer(act, (int)P, at<int>(workspace, L.pair_of), k, topk_w, at<float>(workspace, L.l_q), r,
+                                 r, 0, 0, F, ws_f, d, stream),
+           "moe_backward: LoRA grad A_down");
+    // B_down: s * sum over tokens of g (x) V
+    d = {};
+    d.p[0] = lora_grads[5]; d.ld[0] = r; d.kmajor[0] = 1; d.scale[0] = lo.sd;
+    MX_TRY(mx::launch_lora_outer(mat_f32(grad_out, D), N, nullptr, k, nullptr, at<float>(workspace, L.l_vsum), r, r, 0,
+                                 0, D, ws_f, d, stream),
+           "moe_backward: LoRA grad B_down");
+    MX_PHASE("lora_grads", stream);
+  }
   return MXFP4_OK;
+}
+
+int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, const void* h, int h_dtype,
+                       const void* topk_idx, int idx_dtype, const float* topk_w, int N, int k, const uint8_t* w1p,
+                       const uint8_t* w1s, const uint8_t* w3p, const uint8_t* w3s, const uint8_t* w2p,
+                       const uint8_t* w2s, int E, int D, int F, int act_kind, int flags, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream)
+{
+  return mxfp4_moe_backward_lora(grad_h, grad_w, grad_out, h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, w1p, w1s,
+                                 w3p, w3s, w2p, w2s, E, D, F, act_kind, nullptr, nullptr, 0, nullptr, flags, workspace,
+                                 workspace_bytes, stream);
 }
 
 int mxfp4_moe_timing(int enable)

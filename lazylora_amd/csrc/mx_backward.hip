@@ -230,11 +230,13 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
       const int p = w.row0 + (row_ok ? i : 0);
       const float tw = a.row_w[p];
       const float* sv = a.saved + (long long)p * 2 * F;
+      // LoRA: the down adapter's A_d^T q of the row's token joins g . W2
+      const float* rq = a.lora_rq ? a.lora_rq + (long long)a.a_row_map[p] * F : nullptr;
 #pragma unroll
       for (int cg = 0; cg < 8; ++cg) {
         const int f = c0 + wave * 128 + cg * 16 + li;
         if (f < F) {
-          const float h = acc[cg][v];
+          const float h = rq ? acc[cg][v] + rq[f] : acc[cg][v];
           const float gt = sv[f], up = sv[F + f];
           dots[v] += glu_fwd(gt, up, a.act_kind) * h;
           float dg, du;

@@ -137,7 +137,14 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int i = 4 * g + v;
-      const float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
+      float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
+      if (a.lora_delta && w.active && i < w.nrows) {  // LoRA gate/up delta of the row's token
+        const float* dl = a.lora_delta + (long long)a.row_token[w.row0 + i] * 2 * F + w.ct * 32 + j;
+        ga += dl[0];
+        gb += dl[16];
+        ua += dl[F];
+        ub += dl[F + 16];
+      }
       Quant2 q = quant2_block16(glu_fwd(ga, ua, a.act_kind), glu_fwd(gb, ub, a.act_kind));
       if (!w.active) q = Quant2{0, 0, 0, 0};  // features past F: the padding of the layout is zero
       sq[((wave * 2 + 0) * 2 + 0) * 256 + i * 16 + j] = (uint8_t)q.hi;
@@ -389,7 +396,14 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int i = 4 * g + v;
-      const float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
+      float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
+      if (a.lora_delta && i < w.nrows) {  // LoRA gate/up delta of the row's token
+        const float* dl = a.lora_delta + (long long)a.row_token[w.row0 + i] * 2 * F + f0 + j;
+        ga += dl[0];
+        gb += dl[16];
+        ua += dl[F];
+        ub += dl[F + 16];
+      }
       const float a0 = glu_fwd(ga, ua, a.act_kind), a1 = glu_fwd(gb, ub, a.act_kind);
       if (a.save && i < w.nrows) {
         float* sv = a.save + (long long)(w.row0 + i) * 2 * F;

@@ -36,6 +36,9 @@ struct FwdArgs {
   uint8_t* q_tiles;      // kFwdGateUp: act in the AT layout with K = R (= F), same tiles
   float* save;           // kFwdGateUp: [rows, 2R] gate | up in fp32, or null
   int act_kind;
+  // kFwdGateUp with LoRA: gate|up of row p gain lora_delta[row_token[p], 0:2R) before the GLU
+  const int* row_token;
+  const float* lora_delta;  // [tokens, 2R] fp32, or null
 };
 
 // ---------------------------------------------------------------- transposed products
@@ -72,6 +75,9 @@ struct BwdArgs {
   uint16_t* d_hi;      // [rows, 2C]
   uint16_t* d_lo;
   float* gw_part;      // [rows, n_ct]
+  // kBwdDownT with LoRA: h = g . W2 of row p gains lora_rq[a_row_map[p], 0:C) (the down
+  // adapter's A^T q of the row's token), so both the GLU backward and grad_w see it
+  const float* lora_rq;  // [tokens, C] fp32, or null
 };
 
 constexpr int kFwdRowsPerTile = 16;
@@ -102,6 +108,63 @@ hipError_t launch_combine_bwd(float* grad_h, float* grad_w, const float* dxpair,
                               const float* gw_part, int n_ct, const int* pair_of, int N, int k, int D,
                               hipStream_t s);
 hipError_t launch_zero(void* p, size_t bytes, hipStream_t s);
+// ---------------------------------------------------------------- LoRA coupling
+// Encodings of the row-major matrices the LoRA kernels read.
+enum LoraSrc : int {
+  kLoraF32 = 0,   // p0: fp32 [rows, ld]
+  kLoraBF16 = 1,  // p0: bf16 [rows, ld]
+  kLoraGLU = 2,   // p0: saved fp32 gate | up [rows, 2F]; element (row, c) = GLU(gate[c], up[c])
+  kLoraHiLo = 3,  // p0 / p1: bf16 hi and lo [rows, ld]; element = hi + lo
+};
+struct LoraMat {
+  int kind;
+  const void* p0;
+  const void* p1;
+  long long ld;
+  int F, act_kind;  // kLoraGLU
+};
+// Small dense factor M of a LoRA adapter, addressed as M(j, k) (j < rank): j-major means
+// M[j * ld + k] (lora_A [r, in]), k-major means M[k * ld + j] (lora_B [out, r]).
+struct LoraFactor {
+  const float* m;
+  long long ld;
+  int kmajor;
+  float scale;
+};
+
+constexpr int kLoraMaxRank = 32;
+
+// out[row, s*r + j] = f_s.scale * sum_{k < K} src(row, koff_s + k) * f_s(j, k), segments s < nseg,
+// rows < rows (and < *rows_dev when given).
+hipError_t launch_lora_rowdot(const LoraMat& src, int rows, const int* rows_dev, int K, int r, int nseg,
+                              const LoraFactor* f, const int* koff, float* out, hipStream_t s);
+// out[t, :] (+)= sum over segments s of f_s.scale * sum_{j < r} coef[t, coff_s + j] * f_s(j, c - col0_s)
+// for the columns c in [col0_s, col0_s + ncol_s); Cout columns in all.
+hipError_t launch_lora_expand(const float* coef, int ldc, int rows, int r, int nseg, const LoraFactor* f,
+                              const int* coff, const int* col0, const int* ncol, float* out, long long ldo, int Cout,
+                              int accumulate, hipStream_t s);
+// out[t, j] = sum over the token's slots in slot order of (topk_w[t, s] if weighted) * src[pair_of[t, s], j]
+hipError_t launch_lora_slot_sum(const float* src, int m, const int* pair_of, const float* topk_w, int N, int k,
+                                float* out, hipStream_t s);
+// Column-wise outer-product reduction: G[j, c] = sum over rows q of coef(q, j) * src(row(q), c), j < m,
+// c < C, then written through `dst`. Rows q are tokens (pair_of == null: row = q, coef row q) or the
+// (token, slot) pairs in token order (row = pair_of[q], skipped when negative; coef row = q / k,
+// times topk_w[q] when weighted). With coef_split > 0 the columns c >= coef_split read coef
+// columns shifted by coef_shift. The sums run over fixed row chunks and are added in chunk order,
+// so the result does not depend on scheduling.
+struct LoraOuterDst {
+  float* p[2];
+  long long ld[2];
+  int kmajor[2];
+  float scale[2];
+  int split_c;  // columns >= split_c go to p[1] (column index minus split_c), or 0
+  int split_j;  // coefficients j >= split_j go to p[1] (index minus split_j), or 0
+};
+size_t lora_outer_partial_floats(int Q, int m, int C);
+hipError_t launch_lora_outer(const LoraMat& src, int Q, const int* pair_of, int k, const float* topk_w,
+                             const float* coef, int ldc, int m, int coef_split, int coef_shift, int C, float* partial,
+                             const LoraOuterDst& dst, hipStream_t s);
+
 // Router selection (sigmoid, bias, top-k, renormalise, scale), one wave per token.
 hipError_t launch_router_topk(long long* topk_idx, float* topk_w, const float* logits, const float* bias, int N,
                               int E, int top_k, float scale, int renormalize, hipStream_t s);

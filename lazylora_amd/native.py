@@ -68,6 +68,12 @@ def _load_library() -> ctypes.CDLL:
     lib.mxfp4_moe_backward.restype = ci
     lib.mxfp4_moe_backward.argtypes = [vp, vp, vp, vp, ci, vp, ci, vp, ci, ci, vp, vp, vp, vp, vp, vp,
                                        ci, ci, ci, ci, ci, vp, sz, vp]
+    lib.mxfp4_moe_forward_lora.restype = ci
+    lib.mxfp4_moe_forward_lora.argtypes = [vp, vp, ci, vp, ci, vp, ci, ci, vp, vp, vp, vp, vp, vp,
+                                           ci, ci, ci, ci, vp, vp, ci, ci, vp, sz, vp]
+    lib.mxfp4_moe_backward_lora.restype = ci
+    lib.mxfp4_moe_backward_lora.argtypes = [vp, vp, vp, vp, ci, vp, ci, vp, ci, ci, vp, vp, vp, vp, vp, vp,
+                                            ci, ci, ci, ci, vp, vp, ci, vp, ci, vp, sz, vp]
     lib.mxfp4_moe_route_status.restype = ci
     lib.mxfp4_moe_route_status.argtypes = [vp, vp, vp]
     lib.mxfp4_router_topk.restype = ci
@@ -180,40 +186,52 @@ class MXFP4Kernel:
     # -- routed layer ------------------------------------------------------------------------
     def routed_forward(self, h: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                        experts, act="swiglu", save_for_backward: bool = False,
-                       workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       workspace: Optional[torch.Tensor] = None, lora=None) -> torch.Tensor:
         """sum_e w_e(token) * expert_e(h) for one routed-expert layer; fp32 [N, D].
 
-        Mirrors LazyLoRATrainer._routed_experts_forward (lazy_lora/trainer/lazy_trainer.py:806-834)
-        with LoRA off. `experts` is an ExpertLayer (stacked packed weights in HBM).
+        Mirrors LazyLoRATrainer._routed_experts_forward (lazy_lora/trainer/lazy_trainer.py:806-834).
+        `experts` is an ExpertLayer (stacked packed weights in HBM). `lora` is the layer's
+        adapters: an object with gate_lora / up_lora / down_lora (the reference's LayerLoRABundle)
+        or a (gate, up, down) sequence, each with lora_A [r, in], lora_B [out, r] and scaling
+        (LazyLoRALinear, lazy_lora/core/lora_layer.py:53-97); None = LoRA off.
         """
         call = _RoutedCall(self.lib, h, topk_indices, topk_weights, experts, act, workspace)
+        lo = _LoraCall(lora, call.dev, call.D, call.F)
         out = torch.empty((call.N, call.D), dtype=torch.float32, device=call.dev)
-        _check(self.lib.mxfp4_moe_forward(
+        _check(self.lib.mxfp4_moe_forward_lora(
             out.data_ptr(), call.h.data_ptr(), call.h_dtype, call.idx.data_ptr(), call.idx_dtype,
             call.w.data_ptr(), call.N, call.k, *experts.pointers(), experts.E, call.D, call.F, call.act,
-            MOE_SAVE if save_for_backward else 0, call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
+            lo.ptrs, lo.scaling, lo.r, MOE_SAVE if save_for_backward else 0, call.ws.data_ptr(), call.nws,
+            _stream(call.dev)), self.lib)
         return out
 
     def routed_backward(self, h: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                         experts, grad_out: torch.Tensor, act="swiglu", reuse_forward: bool = False,
-                        workspace: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
-        """(dL/dh [N, D] fp32, dL/dtopk_weights [N, k] fp32) for upstream grad_out [N, D].
+                        workspace: Optional[torch.Tensor] = None, lora=None):
+        """(dL/dh [N, D] fp32, dL/dtopk_weights [N, k] fp32) for upstream grad_out [N, D]; with
+        `lora`, also the adapter gradients (gate_A, gate_B, up_A, up_B, down_A, down_B), fp32,
+        summed over the experts (what the reference accumulates, lazy_trainer.py:866-876).
 
-        Mirrors _routed_experts_backward (lazy_trainer.py:836-880) with LoRA off. With
-        reuse_forward=True the workspace must come from a routed_forward(save_for_backward=True)
-        call on the same inputs; the routing and gate/up products are then not recomputed.
+        Mirrors _routed_experts_backward (lazy_trainer.py:836-880). With reuse_forward=True the
+        workspace must come from a routed_forward(save_for_backward=True) call on the same inputs
+        and adapters; the routing and gate/up products are then not recomputed.
         """
         call = _RoutedCall(self.lib, h, topk_indices, topk_weights, experts, act, workspace)
+        lo = _LoraCall(lora, call.dev, call.D, call.F)
         if grad_out.shape != (call.N, call.D):
             raise ValueError(f"grad_out must be [{call.N}, {call.D}], got {tuple(grad_out.shape)}")
         g = grad_out.to(call.dev, non_blocking=True).contiguous().float()
         grad_h = torch.empty((call.N, call.D), dtype=torch.float32, device=call.dev)
         grad_w = torch.empty((call.N, call.k), dtype=torch.float32, device=call.dev)
-        _check(self.lib.mxfp4_moe_backward(
+        grads = [torch.empty_like(t) for t in lo.tensors]
+        gptrs = (ctypes.c_void_p * 6)(*[t.data_ptr() for t in grads]) if lo.r else None
+        _check(self.lib.mxfp4_moe_backward_lora(
             grad_h.data_ptr(), grad_w.data_ptr(), g.data_ptr(), call.h.data_ptr(), call.h_dtype,
             call.idx.data_ptr(), call.idx_dtype, call.w.data_ptr(), call.N, call.k, *experts.pointers(),
-            experts.E, call.D, call.F, call.act, MOE_REUSE_FORWARD if reuse_forward else 0,
-            call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
+            experts.E, call.D, call.F, call.act, lo.ptrs, lo.scaling, lo.r, gptrs,
+            MOE_REUSE_FORWARD if reuse_forward else 0, call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
+        if lo.r:
+            return grad_h, grad_w, tuple(grads)
         return grad_h, grad_w
 
     # -- router ----------------------------------------------------------------------------
@@ -351,6 +369,42 @@ class _RoutedCall:
         elif workspace.numel() < self.nws or workspace.dtype != torch.uint8:
             raise ValueError(f"workspace must be uint8 with at least {self.nws} bytes")
         self.ws = workspace
+
+
+class _LoraCall:
+    """Validated fp32 device copies of a layer's three adapters and their ctypes arrays."""
+
+    def __init__(self, lora, dev, D: int, F: int):
+        self.tensors, self.ptrs, self.scaling, self.r = [], None, None, 0
+        if lora is None:
+            return
+        mods = (lora.gate_lora, lora.up_lora, lora.down_lora) if hasattr(lora, "gate_lora") else tuple(lora)
+        if len(mods) != 3:
+            raise ValueError("lora must hold three adapters: gate, up, down")
+        ins, outs = (D, D, F), (F, F, D)
+        r = None
+        for mod, n_in, n_out, name in zip(mods, ins, outs, ("gate", "up", "down")):
+            A, B = getattr(mod, "lora_A", None), getattr(mod, "lora_B", None)
+            if A is None or B is None:
+                raise ValueError(f"{name} adapter has no lora_A / lora_B (rank 0 adapters are not supported)")
+            if float(getattr(mod, "dropout_rate", 0.0) or 0.0) != 0.0:
+                raise ValueError("LoRA dropout is not supported: the backward recomputes the layer, so the "
+                                 "reference runs with lora_dropout = 0")
+            ra = A.shape[0]
+            if tuple(A.shape) != (ra, n_in) or tuple(B.shape) != (n_out, ra):
+                raise ValueError(f"{name} adapter must be A [r, {n_in}], B [{n_out}, r]; got "
+                                 f"{tuple(A.shape)}, {tuple(B.shape)}")
+            if r is None:
+                r = ra
+            elif ra != r:
+                raise ValueError("the three adapters must share one rank")
+            self.tensors += [torch.as_tensor(A).detach().to(dev, torch.float32).contiguous(),
+                             torch.as_tensor(B).detach().to(dev, torch.float32).contiguous()]
+        if not 1 <= r <= 32:
+            raise ValueError(f"LoRA rank must lie in [1, 32], got {r}")
+        self.r = r
+        self.ptrs = (ctypes.c_void_p * 6)(*[t.data_ptr() for t in self.tensors])
+        self.scaling = (ctypes.c_float * 3)(*[float(m.scaling) for m in mods])
 
 
 def kernel() -> Optional[MXFP4Kernel]:

@@ -2,7 +2,7 @@
 The routed-expert map of one MoE layer as a single autograd node, on MI355X.
 
 Mirrors RoutedExpertsFunction and the two expert sweeps of the reference trainer
-(lazy_lora/trainer/lazy_trainer.py:45-77, :806-880) with LoRA off: forward returns the fp32
+(lazy_lora/trainer/lazy_trainer.py:45-77, :806-880): forward returns the fp32
 routed sum, backward returns (dL/dh_latent cast to h's dtype, dL/dtopk_weights). The expert
 loops run on the GPU in a few launches each (routing histogram/scan/placement, fused
 gate/up/GLU, down product with the combine weight, deterministic combine; and the three
@@ -12,6 +12,9 @@ As in the reference, a `cached` routed sum short-circuits the forward (the backw
 lazy_trainer.py:60-66); here the backward can additionally reuse the forward's gate/up
 activations when the same workspace is kept (save_for_backward=True), which removes the
 recompute of the gate/up products that the reference performs (:859).
+
+The layer's LoRA adapters (gate, up, down; shared by its experts, lazy_trainer.py:130-134) are
+optional: their terms are added on the device and their gradients accumulated into them.
 """
 from typing import Optional
 
@@ -30,26 +33,54 @@ def _native():
 
 def routed_experts_forward(h_latent: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                            layer: ExpertLayer, act: str = "swiglu", save_for_backward: bool = False,
-                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """sum_e w_e(token) * expert_e(h_latent) in fp32 (lazy_trainer.py:806-834)."""
+                           workspace: Optional[torch.Tensor] = None, lora=None) -> torch.Tensor:
+    """sum_e w_e(token) * expert_e(h_latent) in fp32 (lazy_trainer.py:806-834); `lora` = the
+    layer's (gate, up, down) adapters or None."""
     return _native().routed_forward(h_latent, topk_indices, topk_weights, layer, act=act,
-                                    save_for_backward=save_for_backward, workspace=workspace)
+                                    save_for_backward=save_for_backward, workspace=workspace, lora=lora)
 
 
 def routed_experts_backward(h_latent: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                             layer: ExpertLayer, grad_out: torch.Tensor, act: str = "swiglu",
-                            reuse_forward: bool = False, workspace: Optional[torch.Tensor] = None):
-    """(dL/dh_latent, dL/dtopk_weights) (lazy_trainer.py:836-880); grad_h in h's dtype."""
-    gh, gw = _native().routed_backward(h_latent, topk_indices, topk_weights, layer, grad_out, act=act,
-                                       reuse_forward=reuse_forward, workspace=workspace)
-    return gh.to(h_latent.dtype), gw.to(topk_weights.dtype)
+                            reuse_forward: bool = False, workspace: Optional[torch.Tensor] = None, lora=None):
+    """(dL/dh_latent, dL/dtopk_weights) (lazy_trainer.py:836-880); grad_h in h's dtype. With
+    `lora` the adapters' gradients are accumulated into them as the reference does
+    (accumulate_grad, lazy_trainer.py:866-876)."""
+    res = _native().routed_backward(h_latent, topk_indices, topk_weights, layer, grad_out, act=act,
+                                    reuse_forward=reuse_forward, workspace=workspace, lora=lora)
+    if lora is not None:
+        accumulate_lora_grads(lora, res[2])
+    return res[0].to(h_latent.dtype), res[1].to(topk_weights.dtype)
+
+
+def _adapters(lora):
+    return (lora.gate_lora, lora.up_lora, lora.down_lora) if hasattr(lora, "gate_lora") else tuple(lora)
+
+
+def accumulate_lora_grads(lora, grads) -> None:
+    """Adds (gate_A, gate_B, up_A, up_B, down_A, down_B) gradients to the adapters: through their
+    accumulate_grad when they have one (LazyLoRALinear, lora_layer.py:228-266), else into
+    lora_A.grad / lora_B.grad."""
+    for n, mod in enumerate(_adapters(lora)):
+        gA, gB = grads[2 * n], grads[2 * n + 1]
+        if hasattr(mod, "accumulate_grad"):
+            mod.accumulate_grad(gA, gB)
+            continue
+        for p, gp in ((mod.lora_A, gA), (mod.lora_B, gB)):
+            gp = gp.to(p.device, p.dtype)
+            if p.grad is None:
+                p.grad = gp.clone()
+            else:
+                p.grad.add_(gp)
 
 
 class RoutedExpertsFunction(torch.autograd.Function):
-    """autograd node: (h_latent, topk_weights, topk_indices, layer, act, cached) -> routed sum."""
+    """autograd node: (h_latent, topk_weights, topk_indices, layer, act, cached, lora) -> routed
+    sum. The LoRA adapters are not inputs of the node; their gradients are accumulated into them
+    in backward, as the reference's node does (lazy_trainer.py:45-77, :866-876)."""
 
     @staticmethod
-    def forward(ctx, h_latent, topk_weights, topk_indices, layer, act="swiglu", cached=None):
+    def forward(ctx, h_latent, topk_weights, topk_indices, layer, act="swiglu", cached=None, lora=None):
         k = _native()
         ws = torch.empty(max(k.moe_workspace_bytes(h_latent.shape[0], topk_indices.shape[1], layer.E,
                                                    layer.D, layer.F), 1),
@@ -59,10 +90,10 @@ class RoutedExpertsFunction(torch.autograd.Function):
             reuse = False
         else:
             out = k.routed_forward(h_latent, topk_indices, topk_weights, layer, act=act,
-                                   save_for_backward=True, workspace=ws)
+                                   save_for_backward=True, workspace=ws, lora=lora)
             reuse = True
         ctx.save_for_backward(h_latent, topk_weights, topk_indices)
-        ctx.layer, ctx.act, ctx.ws, ctx.reuse = layer, act, ws, reuse
+        ctx.layer, ctx.act, ctx.ws, ctx.reuse, ctx.lora = layer, act, ws, reuse, lora
         return out
 
     @staticmethod
@@ -70,6 +101,6 @@ class RoutedExpertsFunction(torch.autograd.Function):
         h_latent, topk_weights, topk_indices = ctx.saved_tensors
         grad_h, grad_w = routed_experts_backward(h_latent, topk_indices, topk_weights, ctx.layer,
                                                  grad_out, act=ctx.act, reuse_forward=ctx.reuse,
-                                                 workspace=ctx.ws)
+                                                 workspace=ctx.ws, lora=ctx.lora)
         ctx.ws = None
-        return grad_h, grad_w, None, None, None, None
+        return grad_h, grad_w, None, None, None, None, None

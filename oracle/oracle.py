@@ -198,43 +198,127 @@ def _expert_rows(e, topk_idx, topk_w):
     return rows, tw, mask[rows]
 
 
-def routed_forward(h, topk_idx, topk_w, experts, act: str = "swiglu", dense=None) -> np.ndarray:
-    """sum_e w_e(token) * expert_e(h) in float64 (lazy_trainer.py:806-834, LoRA off).
-    `dense(e) -> (W1, W3, W2)` overrides the weights (used for the dense moe.json fixture)."""
+@dataclass
+class LoRA:
+    """The layer's LoRA adapters, shared by all its experts (lazy_trainer.py:130-134): A [r, in],
+    B [out, r], scaling = alpha / r (lora_layer.py:53-97). Gate/up map D -> F, down F -> D."""
+    gate_A: np.ndarray
+    gate_B: np.ndarray
+    up_A: np.ndarray
+    up_B: np.ndarray
+    down_A: np.ndarray
+    down_B: np.ndarray
+    gate_s: float = 2.0
+    up_s: float = 2.0
+    down_s: float = 2.0
+
+    def adapters(self):
+        return ((self.gate_A, self.gate_B, self.gate_s), (self.up_A, self.up_B, self.up_s),
+                (self.down_A, self.down_B, self.down_s))
+
+
+def lora_delta(x, A, B, s):
+    """forward_lora_only, dropout off (lora_layer.py:104-139): s (x A^T) B^T."""
+    return s * (np.asarray(x, np.float64) @ np.asarray(A, np.float64).T) @ np.asarray(B, np.float64).T
+
+
+def lora_gradients(dy, x, A, B, s):
+    """compute_lora_gradients (lora_layer.py:178-226) without the base term: (grad_A, grad_B,
+    dx_lora) with h = x A^T, grad_B = s dy^T h, dh = s dy B, grad_A = dh^T x, dx_lora = dh A."""
+    A, B = np.asarray(A, np.float64), np.asarray(B, np.float64)
+    h = x @ A.T
+    dh = s * dy @ B
+    return dh.T @ x, s * dy.T @ h, dh @ A
+
+
+def routed_forward(h, topk_idx, topk_w, experts, act: str = "swiglu", dense=None, lora=None) -> np.ndarray:
+    """sum_e w_e(token) * expert_e(h) in float64 (lazy_trainer.py:806-834, and _expert_forward
+    :762-791 for the LoRA terms). `dense(e) -> (W1, W3, W2)` overrides the weights (used for
+    the dense moe.json fixture); `lora` is a LoRA or None."""
     h = np.asarray(h, np.float64)
     topk_idx = np.asarray(topk_idx)
     out = np.zeros(h.shape, np.float64)
     get = dense if dense is not None else experts.dense
     for e in np.unique(topk_idx):
         rows, tw, _ = _expert_rows(e, topk_idx, topk_w)
+        if rows.size == 0:
+            continue
         W1, W3, W2 = get(int(e))
         x = h[rows]
-        down = glu_forward(x @ W1.T, x @ W3.T, act) @ W2.T
+        gate, up = x @ W1.T, x @ W3.T
+        if lora is not None:
+            (ag, bg, sg), (au, bu, su), _ = lora.adapters()
+            gate = gate + lora_delta(x, ag, bg, sg)
+            up = up + lora_delta(x, au, bu, su)
+        a = glu_forward(gate, up, act)
+        down = a @ W2.T
+        if lora is not None:
+            down = down + lora_delta(a, lora.down_A, lora.down_B, lora.down_s)
         out[rows] += down * tw[:, None]
     return out
 
 
-def routed_backward(h, topk_idx, topk_w, experts, grad_out, act: str = "swiglu", dense=None):
-    """(dL/dh [N, D], dL/dtopk_w [N, k]) in float64 (lazy_trainer.py:836-880, LoRA off):
-    grad_w[t, slot] = <g_t, down_e(t)> for the slot that chose e; d_down = g * tw; then
-    d_act = d_down . W2, the GLU derivative, and d_h = d_gate . W1 + d_up . W3."""
+def routed_backward(h, topk_idx, topk_w, experts, grad_out, act: str = "swiglu", dense=None, lora=None):
+    """(dL/dh [N, D], dL/dtopk_w [N, k]) in float64 (lazy_trainer.py:836-880): grad_w[t, slot] =
+    <g_t, down_e(t)> for the slot that chose e; d_down = g * tw; then d_act = d_down . W2, the
+    GLU derivative, and d_h = d_gate . W1 + d_up . W3. With `lora` the adapters' terms join
+    each step as in compute_lora_gradients, and a third result holds the adapter gradients summed
+    over the experts: (gate_A, gate_B, up_A, up_B, down_A, down_B)."""
     h = np.asarray(h, np.float64)
     g_all = np.asarray(grad_out, np.float64)
     topk_idx = np.asarray(topk_idx)
     grad_h = np.zeros(h.shape, np.float64)
     grad_w = np.zeros(topk_idx.shape, np.float64)
     get = dense if dense is not None else experts.dense
+    lg = None
+    if lora is not None:
+        lg = [np.zeros(np.shape(m), np.float64) for m in (lora.gate_A, lora.gate_B, lora.up_A, lora.up_B,
+                                                         lora.down_A, lora.down_B)]
     for e in np.unique(topk_idx):
         rows, tw, m = _expert_rows(e, topk_idx, topk_w)
+        if rows.size == 0:
+            continue
         W1, W3, W2 = get(int(e))
         x, g = h[rows], g_all[rows]
         gate, up = x @ W1.T, x @ W3.T
-        down = glu_forward(gate, up, act) @ W2.T
+        if lora is not None:
+            gate = gate + lora_delta(x, lora.gate_A, lora.gate_B, lora.gate_s)
+            up = up + lora_delta(x, lora.up_A, lora.up_B, lora.up_s)
+        a = glu_forward(gate, up, act)
+        down = a @ W2.T
+        if lora is not None:
+            down = down + lora_delta(a, lora.down_A, lora.down_B, lora.down_s)
         grad_w[rows] += (g * down).sum(-1, keepdims=True) * m
-        d_act = (g * tw[:, None]) @ W2
+        d_down = g * tw[:, None]
+        d_act = d_down @ W2
+        if lora is not None:
+            gA, gB, dx = lora_gradients(d_down, a, lora.down_A, lora.down_B, lora.down_s)
+            lg[4] += gA
+            lg[5] += gB
+            d_act = d_act + dx
         d_gate, d_up = glu_backward(d_act, gate, up, act)
-        grad_h[rows] += d_gate @ W1 + d_up @ W3
+        d_in = d_gate @ W1 + d_up @ W3
+        if lora is not None:
+            gA, gB, dx = lora_gradients(d_gate, x, lora.gate_A, lora.gate_B, lora.gate_s)
+            lg[0] += gA
+            lg[1] += gB
+            d_in = d_in + dx
+            gA, gB, dx = lora_gradients(d_up, x, lora.up_A, lora.up_B, lora.up_s)
+            lg[2] += gA
+            lg[3] += gB
+            d_in = d_in + dx
+        grad_h[rows] += d_in
+    if lora is not None:
+        return grad_h, grad_w, tuple(lg)
     return grad_h, grad_w
+
+
+def random_lora(rng: np.random.Generator, D: int, F: int, r: int, scale: float = 0.05, alpha: float = 32.0) -> LoRA:
+    """Adapters with nonzero A and B (the reference initialises B to zero, which would hide every
+    LoRA term), scaling alpha / r."""
+    s = alpha / r
+    mk = lambda *shape: (scale * rng.standard_normal(shape)).astype(np.float32)
+    return LoRA(mk(r, D), mk(F, r), mk(r, D), mk(F, r), mk(r, F), mk(D, r), s, s, s)
 
 
 # ------------------------------------------------------------------------------------ C restatement

@@ -186,3 +186,71 @@ def test_routed_invariants(clib):
     gh, gw = clib.moe_backward(h, idx, w, ex, g)
     gh64, gw64 = oracle.routed_backward(h, idx, w, ex, g)
     assert oracle.rel_l2(gh, gh64) < 1e-6 and oracle.rel_l2(gw, gw64) < 1e-6
+
+
+# ------------------------------------------------------------------------------------ LoRA terms
+def _lora_case(seed=9, E=4, D=64, F=32, N=6, k=2, r=3):
+    rng = np.random.default_rng(seed)
+    ex = oracle.random_experts(rng, E, D, F, 124, 128)
+    h = rng.standard_normal((N, D))
+    idx, w = oracle.softmax_topk(rng.standard_normal((N, E)), k)
+    g = rng.standard_normal((N, D))
+    lora = oracle.random_lora(rng, D, F, r, scale=0.2)
+    return ex, h, idx, w.astype(np.float64), g, lora
+
+
+@pytest.mark.parametrize("act", ["swiglu", "situ"])
+def test_lora_with_zero_B_changes_nothing(act):
+    """The reference initialises B to zero (lora_layer.py:82-84): the layer then equals the
+    LoRA-off layer, A gets no gradient and B does."""
+    ex, h, idx, w, g, lora = _lora_case()
+    for name in ("gate_B", "up_B", "down_B"):
+        setattr(lora, name, np.zeros_like(getattr(lora, name)))
+    assert np.allclose(oracle.routed_forward(h, idx, w, ex, act, lora=lora), oracle.routed_forward(h, idx, w, ex, act))
+    gh, gw, lg = oracle.routed_backward(h, idx, w, ex, g, act, lora=lora)
+    gh0, gw0 = oracle.routed_backward(h, idx, w, ex, g, act)
+    assert np.allclose(gh, gh0) and np.allclose(gw, gw0)
+    assert all(not lg[i].any() for i in (0, 2, 4))
+    assert all(np.abs(lg[i]).max() > 0 for i in (1, 3, 5))
+
+
+@pytest.mark.parametrize("act", ["swiglu", "situ"])
+def test_lora_equals_merged_weights(act):
+    """x W^T + s (x A^T) B^T = x (W + s B A)^T: the adapters must act exactly like merged dense
+    weights, in the forward and in dL/dh and dL/dw."""
+    ex, h, idx, w, g, lora = _lora_case()
+
+    def merged(e):
+        W1, W3, W2 = ex.dense(e)
+        return (W1 + lora.gate_s * lora.gate_B.astype(np.float64) @ lora.gate_A,
+                W3 + lora.up_s * lora.up_B.astype(np.float64) @ lora.up_A,
+                W2 + lora.down_s * lora.down_B.astype(np.float64) @ lora.down_A)
+
+    got = oracle.routed_forward(h, idx, w, ex, act, lora=lora)
+    assert np.allclose(got, oracle.routed_forward(h, idx, w, None, act, dense=merged), rtol=1e-10, atol=1e-12)
+    assert not np.allclose(got, oracle.routed_forward(h, idx, w, ex, act))
+    gh, gw, _ = oracle.routed_backward(h, idx, w, ex, g, act, lora=lora)
+    mh, mw = oracle.routed_backward(h, idx, w, None, g, act, dense=merged)
+    assert np.allclose(gh, mh, rtol=1e-10, atol=1e-12) and np.allclose(gw, mw, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("act", ["swiglu", "situ"])
+def test_lora_gradients_central_differences(act):
+    ex, h, idx, w, g, lora = _lora_case()
+    _, _, lg = oracle.routed_backward(h, idx, w, ex, g, act, lora=lora)
+    names = ("gate_A", "gate_B", "up_A", "up_B", "down_A", "down_B")
+    eps = 1e-6
+    rng = np.random.default_rng(0)
+    for n, name in enumerate(names):
+        base = getattr(lora, name).astype(np.float64)
+        for _ in range(6):
+            pos = tuple(int(rng.integers(0, s)) for s in base.shape)
+            vals = []
+            for sign in (1, -1):
+                pert = base.copy()
+                pert[pos] += sign * eps
+                setattr(lora, name, pert)
+                vals.append(float((oracle.routed_forward(h, idx, w, ex, act, lora=lora) * g).sum()))
+            setattr(lora, name, base)
+            fd = (vals[0] - vals[1]) / (2 * eps)
+            assert abs(lg[n][pos] - fd) <= 1e-6 + 1e-5 * abs(fd), (name, pos, lg[n][pos], fd)
