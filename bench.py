@@ -132,6 +132,21 @@ def cpu_baseline(layer, H, I, W, G, n_active, budget_s: float):
             "sample": f"C restatement (oracle/mxfp4_oracle.c, -O3 -mavx2 -mfma -fopenmp) fwd+bwd of {what}"}
 
 
+def make_lora(r: int):
+    """Rank-r gate/up/down adapters of the layer (lora_alpha 32, as lazy_lora/core/config.py:69),
+    with nonzero A and B so every LoRA term is computed on real values."""
+    import types
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+
+    def adapter(n_in, n_out):
+        A = 0.02 * torch.randn((r, n_in), device="cuda", generator=gen)
+        B = 0.02 * torch.randn((n_out, r), device="cuda", generator=gen)
+        return types.SimpleNamespace(lora_A=A, lora_B=B, scaling=32.0 / r, dropout_rate=0.0)
+
+    return (adapter(D, F), adapter(D, F), adapter(F, D))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,6 +156,8 @@ def main():
     ap.add_argument("--act", choices=["swiglu", "situ"], default="swiglu")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--lora-rank", type=int, default=0,
+                    help="rank of the layer's gate/up/down LoRA adapters (0: off, the BASELINE configs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (reference kernel for rocprof byte counters)")
     args = ap.parse_args()
@@ -164,9 +181,11 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] layer {layer.nbytes / 1e9:.2f} GB in HBM, {n_active} active experts, setup {time.time() - t_setup:.1f}s")
 
+    lora = make_lora(args.lora_rank) if args.lora_rank else None
+
     def step():
-        k.routed_forward(H, I, W, layer, act=args.act, save_for_backward=True, workspace=ws)
-        return k.routed_backward(H, I, W, layer, G, act=args.act, reuse_forward=True, workspace=ws)
+        k.routed_forward(H, I, W, layer, act=args.act, save_for_backward=True, workspace=ws, lora=lora)
+        return k.routed_backward(H, I, W, layer, G, act=args.act, reuse_forward=True, workspace=ws, lora=lora)
 
     for _ in range(args.warmup):
         step()
@@ -235,7 +254,7 @@ def main():
         "config": {
             "workload": "config 4: routed-expert MoE layer fwd+bwd, 896 experts (w1/w3 2048x7168, w2 7168x2048 "
                         "MXFP4), 1024 tokens x 7168, top-8",
-            "routing": args.routing, "act": args.act, "active_experts": n_active,
+            "routing": args.routing, "act": args.act, "active_experts": n_active, "lora_rank": args.lora_rank,
             "arithmetic": "MXFP4 weights x two-term e4m3 activations (fwd, fp4-native scaled MFMA) / exact bf16 "
                           "decode x two-term bf16 gradients (bwd, bf16 MFMA), fp32 accumulate",
             "weight_bytes_per_step": step_bytes,

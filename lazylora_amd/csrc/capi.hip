@@ -138,7 +138,10 @@ MoeLayout moe_layout(int N, int k, int E, int D, int F)
   L.l_dsum = o; o = align_up(o + sizeof(float) * (size_t)N * 2 * R);
   size_t part = mx::lora_outer_partial_floats(N, 2 * (int)R, D);
   part = std::max(part, mx::lora_outer_partial_floats((int)P, (int)R, F));
-  part = std::max(part, mx::lora_outer_partial_floats((int)P, (int)R, 2 * F));
+  for (int nseg = 1; nseg <= 2; ++nseg) {
+    part = std::max(part, mx::lora_rowdot_partial_floats(N, D, nseg, (int)R));
+    part = std::max(part, mx::lora_rowdot_partial_floats((int)P, F, nseg, (int)R));
+  }
   L.l_part = o; o = align_up(o + sizeof(float) * part);
   L.end = o;
   return L;
@@ -179,6 +182,7 @@ int check_lora(const float* const* lora, const float* scaling, int rank, Lora& l
   if (!scaling) return fail(MXFP4_EINVAL, "moe: null LoRA scaling%s");
   for (int i = 0; i < 6; ++i) {
     if (!lora[i]) return fail(MXFP4_EINVAL, "moe: null LoRA factor%s");
+    if (!aligned16(lora[i])) return fail(MXFP4_EINVAL, "moe: LoRA factors must be 16-byte aligned%s");
     lo.m[i] = lora[i];
   }
   lo.sg = scaling[0]; lo.su = scaling[1]; lo.sd = scaling[2];
@@ -227,7 +231,8 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
     const mx::LoraMat x{h_dtype == MXFP4_BF16 ? mx::kLoraBF16 : mx::kLoraF32, h, nullptr, D, 0, 0};
     const mx::LoraFactor fa[2] = {jmajor(lo.m[0], D, 1.f), jmajor(lo.m[2], D, 1.f)};
     const int koff[2] = {0, 0};
-    MX_TRY(mx::launch_lora_rowdot(x, N, nullptr, D, r, 2, fa, koff, at<float>(ws, L.l_u), s), "LoRA: A x");
+    MX_TRY(mx::launch_lora_rowdot(x, N, nullptr, D, r, 2, fa, koff, at<float>(ws, L.l_part), at<float>(ws, L.l_u), s),
+           "LoRA: A x");
     const mx::LoraFactor fb[2] = {kmajor(lo.m[1], r, lo.sg), kmajor(lo.m[3], r, lo.su)};
     const int coff[2] = {0, r}, col0[2] = {0, F}, ncol[2] = {F, F};
     MX_TRY(mx::launch_lora_expand(at<float>(ws, L.l_u), 2 * r, N, r, 2, fb, coff, col0, ncol,
@@ -243,7 +248,8 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
     const mx::LoraMat act{mx::kLoraGLU, at<float>(ws, L.saved), nullptr, 2LL * F, F, act_kind};
     const mx::LoraFactor fd = jmajor(lo.m[4], F, 1.f);
     const int koff = 0;
-    MX_TRY(mx::launch_lora_rowdot(act, (int)P, at<int>(ws, L.offsets) + E, F, r, 1, &fd, &koff, at<float>(ws, L.l_v), s),
+    MX_TRY(mx::launch_lora_rowdot(act, (int)P, at<int>(ws, L.offsets) + E, F, r, 1, &fd, &koff, at<float>(ws, L.l_part),
+                                  at<float>(ws, L.l_v), s),
            "LoRA: A_down act");
     MX_TRY(mx::launch_lora_slot_sum(at<float>(ws, L.l_v), r, at<int>(ws, L.pair_of), w, N, k, at<float>(ws, L.l_vsum), s),
            "LoRA: slot sum");
@@ -354,6 +360,7 @@ int mxfp4_moe_forward_lora(float* out, const void* h, int h_dtype, const void* t
   Lora lo;
   rc = check_lora(lora, lora_scaling, lora_rank, lo);
   if (rc) return rc;
+  if (lo.r && !aligned16(h)) return fail(MXFP4_EINVAL, "moe_forward: h must be 16-byte aligned with LoRA%s");
   if (N > 0 && !out) return fail(MXFP4_EINVAL, "moe_forward: null output%s");
   const MoeLayout L = moe_layout(N, k, E, D, F);
   if (!workspace || workspace_bytes < L.end) return fail(MXFP4_EWORKSPACE, "moe_forward: workspace too small%s");
@@ -412,6 +419,8 @@ int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out,
   rc = check_lora(lora, lora_scaling, lora_rank, lo);
   if (rc) return rc;
   if (lo.r) {
+    if (!aligned16(h) || !aligned16(grad_out))
+      return fail(MXFP4_EINVAL, "moe_backward: h and grad_out must be 16-byte aligned with LoRA%s");
     if (!lora_grads) return fail(MXFP4_EINVAL, "moe_backward: null LoRA gradient array%s");
     for (int i = 0; i < 6; ++i)
       if (!lora_grads[i]) return fail(MXFP4_EINVAL, "moe_backward: null LoRA gradient%s");
@@ -442,8 +451,8 @@ int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out,
   if (r) {  // q = s_down B_down^T g per token, and its expansion A_down^T q for the W2 epilogue
     const mx::LoraFactor fb = kmajor(lo.m[5], r, lo.sd);
     const int koff = 0;
-    MX_TRY(mx::launch_lora_rowdot(mat_f32(grad_out, D), N, nullptr, D, r, 1, &fb, &koff, at<float>(workspace, L.l_q),
-                                  stream),
+    MX_TRY(mx::launch_lora_rowdot(mat_f32(grad_out, D), N, nullptr, D, r, 1, &fb, &koff,
+                                  at<float>(workspace, L.l_part), at<float>(workspace, L.l_q), stream),
            "moe_backward: LoRA B_down^T g");
     const mx::LoraFactor fa = jmajor(lo.m[4], F, 1.f);
     const int coff = 0, col0 = 0, ncol = F;
@@ -494,7 +503,7 @@ int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out,
                            0};
     const mx::LoraFactor fb[2] = {kmajor(lo.m[1], r, lo.sg), kmajor(lo.m[3], r, lo.su)};
     const int koff[2] = {0, F};
-    MX_TRY(mx::launch_lora_rowdot(dmat, (int)P, n_valid, F, r, 2, fb, koff, at<float>(workspace, L.l_dh), stream),
+    MX_TRY(mx::launch_lora_rowdot(dmat, (int)P, n_valid, F, r, 2, fb, koff, ws_f, at<float>(workspace, L.l_dh), stream),
            "moe_backward: LoRA B^T d");
     MX_TRY(mx::launch_lora_slot_sum(at<float>(workspace, L.l_dh), 2 * r, at<int>(workspace, L.pair_of), nullptr, N, k,
                                     at<float>(workspace, L.l_dsum), stream),
@@ -514,28 +523,28 @@ int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out,
     d.p[0] = lora_grads[0]; d.ld[0] = D; d.kmajor[0] = 0; d.scale[0] = 1.f;
     d.p[1] = lora_grads[2]; d.ld[1] = D; d.kmajor[1] = 0; d.scale[1] = 1.f;
     d.split_j = r;
-    MX_TRY(mx::launch_lora_outer(x, N, nullptr, k, nullptr, at<float>(workspace, L.l_dsum), 2 * r, 2 * r, 0, 0, D, ws_f,
+    MX_TRY(mx::launch_lora_outer(x, 0, N, nullptr, k, nullptr, at<float>(workspace, L.l_dsum), 2 * r, 0, 2 * r, D, ws_f,
                                  d, stream),
            "moe_backward: LoRA grad A_gate/A_up");
-    // B_gate / B_up: s * sum over pairs of [d_gate | d_up] (x) U of the pair's token
-    d = {};
-    d.p[0] = lora_grads[1]; d.ld[0] = r; d.kmajor[0] = 1; d.scale[0] = lo.sg;
-    d.p[1] = lora_grads[3]; d.ld[1] = r; d.kmajor[1] = 1; d.scale[1] = lo.su;
-    d.split_c = F;
-    MX_TRY(mx::launch_lora_outer(dmat, (int)P, at<int>(workspace, L.pair_of), k, nullptr, at<float>(workspace, L.l_u),
-                                 2 * r, r, F, r, 2 * F, ws_f, d, stream),
-           "moe_backward: LoRA grad B_gate/B_up");
+    // B_gate, B_up: s * sum over pairs of d_gate (d_up) (x) A_gate x (A_up x) of the pair's token
+    for (int u = 0; u < 2; ++u) {
+      d = {};
+      d.p[0] = lora_grads[1 + 2 * u]; d.ld[0] = r; d.kmajor[0] = 1; d.scale[0] = u ? lo.su : lo.sg;
+      MX_TRY(mx::launch_lora_outer(dmat, u * F, (int)P, at<int>(workspace, L.pair_of), k, nullptr,
+                                   at<float>(workspace, L.l_u), 2 * r, u * r, r, F, ws_f, d, stream),
+             "moe_backward: LoRA grad B_gate/B_up");
+    }
     // A_down: sum over pairs of w q(token) (x) act
     d = {};
     d.p[0] = lora_grads[4]; d.ld[0] = F; d.kmajor[0] = 0; d.scale[0] = 1.f;
-    MX_TRY(mx::launch_lora_outer(act, (int)P, at<int>(workspace, L.pair_of), k, topk_w, at<float>(workspace, L.l_q), r,
-                                 r, 0, 0, F, ws_f, d, stream),
+    MX_TRY(mx::launch_lora_outer(act, 0, (int)P, at<int>(workspace, L.pair_of), k, topk_w, at<float>(workspace, L.l_q),
+                                 r, 0, r, F, ws_f, d, stream),
            "moe_backward: LoRA grad A_down");
     // B_down: s * sum over tokens of g (x) V
     d = {};
     d.p[0] = lora_grads[5]; d.ld[0] = r; d.kmajor[0] = 1; d.scale[0] = lo.sd;
-    MX_TRY(mx::launch_lora_outer(mat_f32(grad_out, D), N, nullptr, k, nullptr, at<float>(workspace, L.l_vsum), r, r, 0,
-                                 0, D, ws_f, d, stream),
+    MX_TRY(mx::launch_lora_outer(mat_f32(grad_out, D), 0, N, nullptr, k, nullptr, at<float>(workspace, L.l_vsum), r, 0,
+                                 r, D, ws_f, d, stream),
            "moe_backward: LoRA grad B_down");
     MX_PHASE("lora_grads", stream);
   }

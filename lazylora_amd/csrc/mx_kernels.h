@@ -134,10 +134,12 @@ struct LoraFactor {
 
 constexpr int kLoraMaxRank = 32;
 
-// out[row, s*r + j] = f_s.scale * sum_{k < K} src(row, koff_s + k) * f_s(j, k), segments s < nseg,
-// rows < rows (and < *rows_dev when given).
+// out[row, s*r + j] = f_s.scale * sum_{k < K} src(row, koff_s + k) * f_s(j, k), segments s < nseg
+// (nseg <= 2), rows < rows; rows at or past *rows_dev (when given) get 0. K is a multiple of 16.
+// `partial` holds lora_rowdot_partial_floats(rows, K, nseg, r) floats of scratch.
+size_t lora_rowdot_partial_floats(int rows, int K, int nseg, int r);
 hipError_t launch_lora_rowdot(const LoraMat& src, int rows, const int* rows_dev, int K, int r, int nseg,
-                              const LoraFactor* f, const int* koff, float* out, hipStream_t s);
+                              const LoraFactor* f, const int* koff, float* partial, float* out, hipStream_t s);
 // out[t, :] (+)= sum over segments s of f_s.scale * sum_{j < r} coef[t, coff_s + j] * f_s(j, c - col0_s)
 // for the columns c in [col0_s, col0_s + ncol_s); Cout columns in all.
 hipError_t launch_lora_expand(const float* coef, int ldc, int rows, int r, int nseg, const LoraFactor* f,
@@ -146,23 +148,22 @@ hipError_t launch_lora_expand(const float* coef, int ldc, int rows, int r, int n
 // out[t, j] = sum over the token's slots in slot order of (topk_w[t, s] if weighted) * src[pair_of[t, s], j]
 hipError_t launch_lora_slot_sum(const float* src, int m, const int* pair_of, const float* topk_w, int N, int k,
                                 float* out, hipStream_t s);
-// Column-wise outer-product reduction: G[j, c] = sum over rows q of coef(q, j) * src(row(q), c), j < m,
-// c < C, then written through `dst`. Rows q are tokens (pair_of == null: row = q, coef row q) or the
-// (token, slot) pairs in token order (row = pair_of[q], skipped when negative; coef row = q / k,
-// times topk_w[q] when weighted). With coef_split > 0 the columns c >= coef_split read coef
-// columns shifted by coef_shift. The sums run over fixed row chunks and are added in chunk order,
-// so the result does not depend on scheduling.
+// Column-wise outer-product reduction: G[j, c] = sum over rows q of coef(q, j) * src(row(q), c_off + c),
+// j < m (<= 64), c < C (a multiple of 4), then written through `dst`. Rows q are tokens
+// (pair_of == null: row = q, coef row q) or the (token, slot) pairs in token order (row =
+// pair_of[q], skipped when negative; coef row = q / k, times topk_w[q] when weighted); coef
+// columns start at coff. The sums run over fixed row chunks added in chunk order, so the result
+// does not depend on scheduling. `partial` holds lora_outer_partial_floats(Q, m, C) floats.
 struct LoraOuterDst {
   float* p[2];
   long long ld[2];
   int kmajor[2];
   float scale[2];
-  int split_c;  // columns >= split_c go to p[1] (column index minus split_c), or 0
   int split_j;  // coefficients j >= split_j go to p[1] (index minus split_j), or 0
 };
 size_t lora_outer_partial_floats(int Q, int m, int C);
-hipError_t launch_lora_outer(const LoraMat& src, int Q, const int* pair_of, int k, const float* topk_w,
-                             const float* coef, int ldc, int m, int coef_split, int coef_shift, int C, float* partial,
+hipError_t launch_lora_outer(const LoraMat& src, int c_off, int Q, const int* pair_of, int k, const float* topk_w,
+                             const float* coef, int ldc, int coff, int m, int C, float* partial,
                              const LoraOuterDst& dst, hipStream_t s);
 
 // Router selection (sigmoid, bias, top-k, renormalise, scale), one wave per token.

@@ -18,18 +18,29 @@ namespace mx {
 namespace {
 
 MX_DEV float bf16f(uint16_t v) { return __builtin_bit_cast(float, (uint32_t)v << 16); }
+MX_DEV float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
+MX_DEV float bf16_hi(uint32_t v) { return __builtin_bit_cast(float, v & 0xffff0000u); }
 
+// Elements (row, c .. c+3) of a source matrix as fp32; c is a multiple of 4.
 template <int KIND>
-MX_DEV float src_at(const LoraMat& a, long long row, int c)
+MX_DEV f32x4 src4(const LoraMat& a, long long row, int c)
 {
-  if (KIND == kLoraF32) return static_cast<const float*>(a.p0)[row * a.ld + c];
-  if (KIND == kLoraBF16) return bf16f(static_cast<const uint16_t*>(a.p0)[row * a.ld + c]);
+  if (KIND == kLoraF32) return *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.p0) + row * a.ld + c);
+  if (KIND == kLoraBF16) {
+    const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.p0) + row * a.ld + c);
+    return f32x4{bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y)};
+  }
   if (KIND == kLoraGLU) {
     const float* r = static_cast<const float*>(a.p0) + row * a.ld;
-    return glu_fwd(r[c], r[a.F + c], a.act_kind);
+    const f32x4 g = *reinterpret_cast<const f32x4*>(r + c), u = *reinterpret_cast<const f32x4*>(r + a.F + c);
+    return f32x4{glu_fwd(g[0], u[0], a.act_kind), glu_fwd(g[1], u[1], a.act_kind), glu_fwd(g[2], u[2], a.act_kind),
+                 glu_fwd(g[3], u[3], a.act_kind)};
   }
   const long long o = row * a.ld + c;
-  return bf16f(static_cast<const uint16_t*>(a.p0)[o]) + bf16f(static_cast<const uint16_t*>(a.p1)[o]);
+  const uint2 h = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.p0) + o);
+  const uint2 l = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.p1) + o);
+  return f32x4{bf16_lo(h.x) + bf16_lo(l.x), bf16_hi(h.x) + bf16_hi(l.x), bf16_lo(h.y) + bf16_lo(l.y),
+               bf16_hi(h.y) + bf16_hi(l.y)};
 }
 
 MX_DEV float factor_at(const LoraFactor& f, int j, int k)
@@ -37,64 +48,111 @@ MX_DEV float factor_at(const LoraFactor& f, int j, int k)
   return f.kmajor ? f.m[(long long)k * f.ld + j] : f.m[(long long)j * f.ld + k];
 }
 
+// f(j, k .. k+3), zero for j >= r; k is a multiple of 4.
+MX_DEV f32x4 factor4(const LoraFactor& f, int j, int k, int r)
+{
+  if (j >= r) return f32x4{0.f, 0.f, 0.f, 0.f};
+  if (!f.kmajor) return *reinterpret_cast<const f32x4*>(f.m + (long long)j * f.ld + k);
+  const float* p = f.m + (long long)k * f.ld + j;
+  return f32x4{p[0], p[f.ld], p[2 * f.ld], p[3 * f.ld]};
+}
+
+// fp32 matrix-core step: D[16 x 16] += A[16 x 4] B[4 x 16]. Lane l = (i = l % 16, q = l / 16)
+// supplies A[i][q] and B[q][i] and holds D[4q + v][i] in element v.
+MX_DEV f32x4 mfma4(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
 // ---------------------------------------------------------------- row dots
+// Each wave takes one (16-row tile, segment, k-slice) and accumulates its 16 x r block of
+// partial sums on the matrix cores: per 16 k, lane (i, q) loads row i's k .. k+3 (k = 16 kb + 4q)
+// and the same four k of coefficient i (and 16 + i), then four MFMAs take one k each. The
+// k-slices are added in order by lora_rowdot_reduce_kernel.
 struct RowDotArgs {
   LoraMat src;
   int rows;
   const int* rows_dev;
-  int K, r, nseg;
+  int K, r, nseg, S, kb_per;
   LoraFactor f[2];
   int koff[2];
-  float* out;
+  float* partial;  // [S][rows][nseg * r]
 };
 
-// Two rows per wave; lane l takes k = l, l + 64, ... and keeps 64 partial sums (2 rows x 32
-// coefficients). The wave then reduces them by recursive halving: at offset o each lane keeps
-// the half of its values selected by lane bit o and adds its partner's copy of that half, so
-// after six steps lane l holds the full sum of value l (row l / 32, coefficient l % 32).
 template <int KIND>
 __global__ __launch_bounds__(256) void lora_rowdot_kernel(RowDotArgs a)
 {
-  const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+  const int tiles = (a.rows + 15) / 16;
+  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task >= (long long)tiles * a.nseg * a.S) return;  // whole waves leave together
+  const int ks = (int)(task % a.S);
+  const int sg = (int)((task / a.S) % a.nseg);
+  const int tile = (int)(task / ((long long)a.S * a.nseg));
   int nrows = a.rows;
   if (a.rows_dev) nrows = min(nrows, *a.rows_dev);
-  if (row0 >= nrows) return;  // whole waves leave together
-  const bool two = row0 + 1 < nrows;
-  for (int sg = 0; sg < a.nseg; ++sg) {
-    const LoraFactor f = a.f[sg];
-    const int koff = a.koff[sg];
-    float v[64];
+  const int row = tile * 16 + i;
+  const bool rok = row < nrows;
+  const LoraFactor f = a.f[sg];
+  const int koff = a.koff[sg];
+  const bool two = a.r > 16;
+  const int nkb = a.K / 16;
+  const int kb0 = ks * a.kb_per, kb1 = min(kb0 + a.kb_per, nkb);
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  // four blocks of 16 k per iteration, loads first
+  for (int kb = kb0; kb < kb1; kb += 4) {
+    f32x4 x[4], m0[4], m1[4];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) v[i] = 0.f;
-    for (int k = lane; k < a.K; k += 64) {
-      const float x0 = src_at<KIND>(a.src, row0, koff + k);
-      const float x1 = two ? src_at<KIND>(a.src, row0 + 1, koff + k) : 0.f;
-#pragma unroll
-      for (int j = 0; j < kLoraMaxRank; ++j) {
-        if (j < a.r) {
-          const float m = factor_at(f, j, k);
-          v[j] += x0 * m;
-          v[32 + j] += x1 * m;
-        }
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int k = (kb + u) * 16 + 4 * q;
+      const bool in = kb + u < kb1;
+      x[u] = (rok && in) ? src4<KIND>(a.src, row, koff + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+      m0[u] = in ? factor4(f, i, k, a.r) : f32x4{0.f, 0.f, 0.f, 0.f};
+      m1[u] = (in && two) ? factor4(f, 16 + i, k, a.r) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const bool up = (lane & o) != 0;
+    for (int u = 0; u < 4; ++u) {
 #pragma unroll
-      for (int i = 0; i < o; ++i) {
-        const float keep = up ? v[o + i] : v[i];
-        const float give = up ? v[i] : v[o + i];
-        v[i] = keep + __shfl_xor(give, o, 64);
+      for (int c = 0; c < 4; ++c) acc0 = mfma4(x[u][c], m0[u][c], acc0);
+      if (two) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc1 = mfma4(x[u][c], m1[u][c], acc1);
       }
     }
-    const int rr = lane >> 5, j = lane & 31;
-    if (j < a.r && (rr == 0 || two)) a.out[(long long)(row0 + rr) * (a.nseg * a.r) + sg * a.r + j] = f.scale * v[0];
+  }
+  const int m = a.nseg * a.r;
+  float* out = a.partial + (long long)ks * a.rows * m + sg * a.r;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int ro = tile * 16 + 4 * q + v;
+    if (ro >= a.rows) continue;
+    if (i < a.r) out[(long long)ro * m + i] = acc0[v];
+    if (two && 16 + i < a.r) out[(long long)ro * m + 16 + i] = acc1[v];
   }
 }
 
+__global__ __launch_bounds__(256) void lora_rowdot_reduce_kernel(const float* partial, int S, int rows, int r,
+                                                                 int nseg, float scale0, float scale1, float* out)
+{
+  const int m = nseg * r;
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long long)rows * m) return;
+  float s = 0.f;
+  for (int ks = 0; ks < S; ++ks) s += partial[(long long)ks * rows * m + idx];
+  out[idx] = ((int)(idx % m) < r ? scale0 : scale1) * s;
+}
+
+// k-slices of a row dot: about 4096 waves in all, at least 8 blocks of 16 k each.
+void rowdot_slices(int rows, int K, int nseg, int& S, int& kb_per)
+{
+  const int tiles = (rows + 15) / 16, nkb = K / 16;
+  S = 4096 / max(1, tiles * nseg);
+  S = max(1, min(S, nkb / 8));
+  kb_per = (nkb + S - 1) / S;
+  S = max(1, (nkb + kb_per - 1) / kb_per);
+}
+
 // ---------------------------------------------------------------- expansions
+// One column per thread and 16 rows per work-group: the thread keeps its column of the factor
+// in registers and forms the rank-r dot with each row's coefficients (uniform across the
+// work-group, so they come through the scalar cache).
 struct ExpandArgs {
   const float* coef;
   int ldc, rows, r, nseg;
@@ -105,25 +163,40 @@ struct ExpandArgs {
   int Cout, accumulate;
 };
 
+constexpr int kExpandRows = 16;
+
 __global__ __launch_bounds__(256) void lora_expand_kernel(ExpandArgs a)
 {
-  const int t = blockIdx.y;
   const int c = blockIdx.x * 256 + threadIdx.x;
-  if (t >= a.rows || c >= a.Cout) return;
-  const float* cr = a.coef + (long long)t * a.ldc;
-  float* o = a.out + (long long)t * a.ldo + c;
-  float acc = a.accumulate ? *o : 0.f;
+  const int t0 = blockIdx.y * kExpandRows;
+  if (c >= a.Cout) return;
+  const int nr = min(kExpandRows, a.rows - t0);
+  float acc[kExpandRows];
+#pragma unroll
+  for (int u = 0; u < kExpandRows; ++u)
+    acc[u] = (a.accumulate && u < nr) ? a.out[(long long)(t0 + u) * a.ldo + c] : 0.f;
   for (int sg = 0; sg < a.nseg; ++sg) {
     const int cc = c - a.col0[sg];
     if (cc < 0 || cc >= a.ncol[sg]) continue;
     const LoraFactor f = a.f[sg];
-    float s = 0.f;
+    float mc[kLoraMaxRank];
 #pragma unroll
-    for (int j = 0; j < kLoraMaxRank; ++j)
-      if (j < a.r) s += cr[a.coff[sg] + j] * factor_at(f, j, cc);
-    acc += f.scale * s;
+    for (int j = 0; j < kLoraMaxRank; ++j) mc[j] = j < a.r ? factor_at(f, j, cc) : 0.f;
+#pragma unroll
+    for (int u = 0; u < kExpandRows; ++u) {
+      if (u < nr) {
+        const float* cr = a.coef + (long long)(t0 + u) * a.ldc + a.coff[sg];
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < kLoraMaxRank; ++j)
+          if (j < a.r) s += cr[j] * mc[j];
+        acc[u] += f.scale * s;
+      }
+    }
   }
-  *o = acc;
+#pragma unroll
+  for (int u = 0; u < kExpandRows; ++u)
+    if (u < nr) a.out[(long long)(t0 + u) * a.ldo + c] = acc[u];
 }
 
 __global__ __launch_bounds__(256) void lora_slot_sum_kernel(const float* src, int m, const int* pair_of,
@@ -143,67 +216,90 @@ __global__ __launch_bounds__(256) void lora_slot_sum_kernel(const float* src, in
 }
 
 // ---------------------------------------------------------------- outer-product reductions
+// Each wave takes 64 columns and one chunk of rows; per 4 rows, lane (i, q) loads row q's
+// columns 4i .. 4i+3 and that row's coefficient 16 jt + i, and four MFMAs (one per column
+// phase t) accumulate G[16 jt + .., 4 i' + t]. Chunks are added in order by the reduce kernel.
+constexpr int kOuterBlocks = 4;
+
 struct OuterArgs {
   LoraMat src;
-  int Q;
+  int c_off, Q;
   const int* pair_of;
   int k;
   const float* topk_w;
   const float* coef;
-  int ldc, m, coef_split, coef_shift, C, chunk;
-  float* partial;
+  int ldc, coff, m, C, chunk, RS;
+  float* partial;  // [RS][m][C]
 };
 
-constexpr int kOuterUnroll = 8;
-
-// One column per thread, one row chunk per blockIdx.y; rows are taken eight at a time so
-// their loads are in flight together.
-template <int KIND>
+template <int KIND, int JT>
 __global__ __launch_bounds__(256) void lora_outer_kernel(OuterArgs a)
 {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  const int rs = blockIdx.y;
-  const int q0 = rs * a.chunk, q1 = min(q0 + a.chunk, a.Q);
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+  const int ncb = (a.C + 63) / 64;
+  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task >= (long long)ncb * a.RS) return;
+  const int cb = (int)(task % ncb), rs = (int)(task / ncb);
+  const int c = cb * 64 + 4 * i;
   const bool cok = c < a.C;
-  const int cs = cok ? c : 0;
-  const int shift = (a.coef_split > 0 && cs >= a.coef_split) ? a.coef_shift : 0;
-  float acc[64];
+  const int q0 = rs * a.chunk, q1 = min(q0 + a.chunk, a.Q);
+  f32x4 acc[JT][4];
 #pragma unroll
-  for (int j = 0; j < 64; ++j) acc[j] = 0.f;
-  for (int q = q0; q < q1; q += kOuterUnroll) {
-    float x[kOuterUnroll];
-    int crow[kOuterUnroll];
-    bool ok[kOuterUnroll];
+  for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
-    for (int u = 0; u < kOuterUnroll; ++u) {
-      const int qq = q + u;
+    for (int t = 0; t < 4; ++t) acc[jt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // four blocks of 4 rows per iteration: every load of the 16 rows is issued before the MFMAs
+  for (int qb = q0; qb < q1; qb += 4 * kOuterBlocks) {
+    bool ok[kOuterBlocks];
+    long long row[kOuterBlocks], crow[kOuterBlocks];
+    float wq[kOuterBlocks];
+#pragma unroll
+    for (int u = 0; u < kOuterBlocks; ++u) {
+      const int qq = qb + 4 * u + q;
       ok[u] = qq < q1;
-      long long row = qq;
+      row[u] = qq;
       crow[u] = qq;
-      float wq = 1.0f;
+      wq[u] = 1.0f;
       if (a.pair_of && ok[u]) {
         const int p = a.pair_of[qq];
         ok[u] = p >= 0;
-        row = p;
+        row[u] = p;
         crow[u] = qq / a.k;
-        if (a.topk_w) wq = a.topk_w[qq];
+        if (a.topk_w) wq[u] = a.topk_w[qq];
       }
-      x[u] = ok[u] ? wq * src_at<KIND>(a.src, row, cs) : 0.f;
+    }
+    f32x4 x[kOuterBlocks];
+#pragma unroll
+    for (int u = 0; u < kOuterBlocks; ++u)
+      x[u] = (ok[u] && cok) ? src4<KIND>(a.src, row[u], a.c_off + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    float cf[kOuterBlocks][JT];
+#pragma unroll
+    for (int u = 0; u < kOuterBlocks; ++u) {
+      const float* cr = a.coef + crow[u] * a.ldc + a.coff;
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        const int j = jt * 16 + i;
+        cf[u][jt] = (ok[u] && j < a.m) ? wq[u] * cr[j] : 0.f;
+      }
     }
 #pragma unroll
-    for (int u = 0; u < kOuterUnroll; ++u) {
-      if (!ok[u]) continue;
-      const float* cr = a.coef + (long long)crow[u] * a.ldc + shift;
+    for (int u = 0; u < kOuterBlocks; ++u)
 #pragma unroll
-      for (int j = 0; j < 64; ++j)
-        if (j < a.m) acc[j] += cr[j] * x[u];
-    }
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[jt][t] = mfma4(cf[u][jt], x[u][t], acc[jt][t]);
   }
-  if (!cok) return;
   float* out = a.partial + (long long)rs * a.m * a.C;
 #pragma unroll
-  for (int j = 0; j < 64; ++j)
-    if (j < a.m) out[(long long)j * a.C + c] = acc[j];
+  for (int jt = 0; jt < JT; ++jt) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int j = jt * 16 + 4 * q + v;
+      if (j < a.m && cok)
+        *reinterpret_cast<f32x4*>(out + (long long)j * a.C + c) =
+            f32x4{acc[jt][0][v], acc[jt][1][v], acc[jt][2][v], acc[jt][3][v]};
+    }
+  }
 }
 
 __global__ __launch_bounds__(256) void lora_outer_reduce_kernel(const float* partial, int RS, int m, int C,
@@ -214,44 +310,68 @@ __global__ __launch_bounds__(256) void lora_outer_reduce_kernel(const float* par
   const int j = (int)(idx / C), c = (int)(idx % C);
   float s = 0.f;
   for (int rs = 0; rs < RS; ++rs) s += partial[((long long)rs * m + j) * C + c];
-  const bool seg = (d.split_c > 0 && c >= d.split_c) || (d.split_j > 0 && j >= d.split_j);
-  const int sg = seg ? 1 : 0;
-  const int cc = (seg && d.split_c > 0) ? c - d.split_c : c;
-  const int jj = (seg && d.split_j > 0) ? j - d.split_j : j;
-  const long long o = d.kmajor[sg] ? (long long)cc * d.ld[sg] + jj : (long long)jj * d.ld[sg] + cc;
+  const int sg = (d.split_j > 0 && j >= d.split_j) ? 1 : 0;
+  const int jj = sg ? j - d.split_j : j;
+  const long long o = d.kmajor[sg] ? (long long)c * d.ld[sg] + jj : (long long)jj * d.ld[sg] + c;
   d.p[sg][o] = d.scale[sg] * s;
 }
 
-// Row chunking of the outer reductions: about 1024 work-groups in all, at least 32 rows each.
+template <int JT>
+void outer_launch(int kind, dim3 grid, dim3 block, const OuterArgs& a, hipStream_t s)
+{
+  switch (kind) {
+    case kLoraF32: hipLaunchKernelGGL((lora_outer_kernel<kLoraF32, JT>), grid, block, 0, s, a); break;
+    case kLoraBF16: hipLaunchKernelGGL((lora_outer_kernel<kLoraBF16, JT>), grid, block, 0, s, a); break;
+    case kLoraGLU: hipLaunchKernelGGL((lora_outer_kernel<kLoraGLU, JT>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((lora_outer_kernel<kLoraHiLo, JT>), grid, block, 0, s, a); break;
+  }
+}
+
+// Row chunking of the outer reductions: about 4096 waves in all, at least 16 rows each.
 void outer_chunks(int Q, int C, int& RS, int& chunk)
 {
-  const int colblocks = (C + 255) / 256;
-  int want = (1024 + colblocks - 1) / colblocks;
-  want = max(1, min(want, (Q + 31) / 32));
+  const int ncb = (C + 63) / 64;
+  int want = 4096 / max(1, ncb);
+  want = max(1, min(want, (Q + 15) / 16));
   chunk = (Q + want - 1) / want;
-  chunk = (chunk + kOuterUnroll - 1) / kOuterUnroll * kOuterUnroll;
+  chunk = (chunk + 4 * kOuterBlocks - 1) / (4 * kOuterBlocks) * (4 * kOuterBlocks);
   RS = chunk > 0 ? (Q + chunk - 1) / chunk : 0;
 }
 
 }  // namespace
 
+size_t lora_rowdot_partial_floats(int rows, int K, int nseg, int r)
+{
+  int S, kb_per;
+  rowdot_slices(rows, K, nseg, S, kb_per);
+  return (size_t)S * (size_t)rows * (size_t)(nseg * r);
+}
+
 hipError_t launch_lora_rowdot(const LoraMat& src, int rows, const int* rows_dev, int K, int r, int nseg,
-                              const LoraFactor* f, const int* koff, float* out, hipStream_t s)
+                              const LoraFactor* f, const int* koff, float* partial, float* out, hipStream_t s)
 {
   if (rows <= 0) return hipSuccess;
+  if (r > kLoraMaxRank || nseg < 1 || nseg > 2 || K % 16) return hipErrorInvalidValue;
   RowDotArgs a = {};
-  a.src = src; a.rows = rows; a.rows_dev = rows_dev; a.K = K; a.r = r; a.nseg = nseg; a.out = out;
+  a.src = src; a.rows = rows; a.rows_dev = rows_dev; a.K = K; a.r = r; a.nseg = nseg; a.partial = partial;
+  rowdot_slices(rows, K, nseg, a.S, a.kb_per);
   for (int i = 0; i < nseg; ++i) {
     a.f[i] = f[i];
     a.koff[i] = koff[i];
   }
-  dim3 grid((unsigned)((rows + 7) / 8)), block(256);
+  const long long waves = (long long)((rows + 15) / 16) * nseg * a.S;
+  dim3 grid((unsigned)((waves + 3) / 4)), block(256);
   switch (src.kind) {
     case kLoraF32: hipLaunchKernelGGL(lora_rowdot_kernel<kLoraF32>, grid, block, 0, s, a); break;
     case kLoraBF16: hipLaunchKernelGGL(lora_rowdot_kernel<kLoraBF16>, grid, block, 0, s, a); break;
     case kLoraGLU: hipLaunchKernelGGL(lora_rowdot_kernel<kLoraGLU>, grid, block, 0, s, a); break;
     default: hipLaunchKernelGGL(lora_rowdot_kernel<kLoraHiLo>, grid, block, 0, s, a); break;
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const long long n = (long long)rows * nseg * r;
+  hipLaunchKernelGGL(lora_rowdot_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, a.S,
+                     rows, r, nseg, f[0].scale, nseg > 1 ? f[1].scale : f[0].scale, out);
   return hipGetLastError();
 }
 
@@ -269,7 +389,7 @@ hipError_t launch_lora_expand(const float* coef, int ldc, int rows, int r, int n
     a.ncol[i] = ncol[i];
   }
   a.out = out; a.ldo = ldo; a.Cout = Cout; a.accumulate = accumulate;
-  dim3 grid((unsigned)((Cout + 255) / 256), (unsigned)rows), block(256);
+  dim3 grid((unsigned)((Cout + 255) / 256), (unsigned)((rows + kExpandRows - 1) / kExpandRows)), block(256);
   hipLaunchKernelGGL(lora_expand_kernel, grid, block, 0, s, a);
   return hipGetLastError();
 }
@@ -291,31 +411,28 @@ size_t lora_outer_partial_floats(int Q, int m, int C)
   return (size_t)RS * (size_t)m * (size_t)C;
 }
 
-hipError_t launch_lora_outer(const LoraMat& src, int Q, const int* pair_of, int k, const float* topk_w,
-                             const float* coef, int ldc, int m, int coef_split, int coef_shift, int C, float* partial,
+hipError_t launch_lora_outer(const LoraMat& src, int c_off, int Q, const int* pair_of, int k, const float* topk_w,
+                             const float* coef, int ldc, int coff, int m, int C, float* partial,
                              const LoraOuterDst& dst, hipStream_t s)
 {
   if (C <= 0 || m <= 0) return hipSuccess;
-  int RS, chunk;
-  outer_chunks(Q, C, RS, chunk);
-  if (RS > 0) {
-    OuterArgs a = {};
-    a.src = src; a.Q = Q; a.pair_of = pair_of; a.k = k; a.topk_w = topk_w;
-    a.coef = coef; a.ldc = ldc; a.m = m; a.coef_split = coef_split; a.coef_shift = coef_shift;
-    a.C = C; a.chunk = chunk; a.partial = partial;
-    dim3 grid((unsigned)((C + 255) / 256), (unsigned)RS), block(256);
-    switch (src.kind) {
-      case kLoraF32: hipLaunchKernelGGL(lora_outer_kernel<kLoraF32>, grid, block, 0, s, a); break;
-      case kLoraBF16: hipLaunchKernelGGL(lora_outer_kernel<kLoraBF16>, grid, block, 0, s, a); break;
-      case kLoraGLU: hipLaunchKernelGGL(lora_outer_kernel<kLoraGLU>, grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL(lora_outer_kernel<kLoraHiLo>, grid, block, 0, s, a); break;
-    }
+  if (m > 64 || C % 4) return hipErrorInvalidValue;
+  OuterArgs a = {};
+  outer_chunks(Q, C, a.RS, a.chunk);
+  if (a.RS > 0) {
+    a.src = src; a.c_off = c_off; a.Q = Q; a.pair_of = pair_of; a.k = k; a.topk_w = topk_w;
+    a.coef = coef; a.ldc = ldc; a.coff = coff; a.m = m; a.C = C; a.partial = partial;
+    const long long waves = (long long)((C + 63) / 64) * a.RS;
+    dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    if (m <= 16) outer_launch<1>(src.kind, grid, block, a, s);
+    else if (m <= 32) outer_launch<2>(src.kind, grid, block, a, s);
+    else outer_launch<4>(src.kind, grid, block, a, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   const long long n = (long long)m * C;
-  hipLaunchKernelGGL(lora_outer_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, RS, m, C,
-                     dst);
+  hipLaunchKernelGGL(lora_outer_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, a.RS, m,
+                     C, dst);
   return hipGetLastError();
 }
 

@@ -220,7 +220,7 @@ class MXFP4Kernel:
         lo = _LoraCall(lora, call.dev, call.D, call.F)
         if grad_out.shape != (call.N, call.D):
             raise ValueError(f"grad_out must be [{call.N}, {call.D}], got {tuple(grad_out.shape)}")
-        g = grad_out.to(call.dev, non_blocking=True).contiguous().float()
+        g = _aligned(grad_out.to(call.dev, non_blocking=True).contiguous().float())
         grad_h = torch.empty((call.N, call.D), dtype=torch.float32, device=call.dev)
         grad_w = torch.empty((call.N, call.k), dtype=torch.float32, device=call.dev)
         grads = [torch.empty_like(t) for t in lo.tensors]
@@ -350,7 +350,7 @@ class _RoutedCall:
             self.h_dtype = F32
         else:
             raise ValueError(f"h must be float32 or bfloat16, got {h.dtype}")
-        self.h = h.to(self.dev, non_blocking=True).contiguous()
+        self.h = _aligned(h.to(self.dev, non_blocking=True).contiguous())
         if topk_indices.dtype == torch.int64:
             self.idx_dtype = I64
         elif topk_indices.dtype == torch.int32:
@@ -369,6 +369,11 @@ class _RoutedCall:
         elif workspace.numel() < self.nws or workspace.dtype != torch.uint8:
             raise ValueError(f"workspace must be uint8 with at least {self.nws} bytes")
         self.ws = workspace
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its data starts on a 16-byte boundary, else an aligned copy."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 class _LoraCall:
@@ -398,8 +403,8 @@ class _LoraCall:
                 r = ra
             elif ra != r:
                 raise ValueError("the three adapters must share one rank")
-            self.tensors += [torch.as_tensor(A).detach().to(dev, torch.float32).contiguous(),
-                             torch.as_tensor(B).detach().to(dev, torch.float32).contiguous()]
+            self.tensors += [_aligned(torch.as_tensor(A).detach().to(dev, torch.float32).contiguous()),
+                             _aligned(torch.as_tensor(B).detach().to(dev, torch.float32).contiguous())]
         if not 1 <= r <= 32:
             raise ValueError(f"LoRA rank must lie in [1, 32], got {r}")
         self.r = r
