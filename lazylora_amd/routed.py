@@ -59,7 +59,7 @@ def _adapters(lora):
 
 def accumulate_lora_grads(lora, grads) -> None:
     """Adds (gate_A, gate_B, up_A, up_B, down_A, down_B) gradients to the adapters: through their
-    accumulate_grad when they have one (LazyLoRALinear, lora_layer.py:228-266), else into
+    accumulate_grad when they have one (LazyLoRALinear, lora_layer.py:258-308), else into
     lora_A.grad / lora_B.grad."""
     for n, mod in enumerate(_adapters(lora)):
         gA, gB = grads[2 * n], grads[2 * n + 1]
