@@ -147,6 +147,76 @@ def make_lora(r: int):
     return (adapter(D, F), adapter(D, F), adapter(F, D))
 
 
+def stream_main(args, k):
+    """Config 5: an out-of-core sweep of `layers` routed-expert layers of the config-3 shape, each
+    copied from pinned host memory (a ring of `ring` distinct layers, as 93 x 20.96 GB cannot be
+    pinned) into one of two HBM slots on a copy stream while the compute stream runs the layer
+    forward for 1024 tokens on the previous slot."""
+    from lazylora_amd.streaming import LayerStreamer, host_layer_from
+    t_setup = time.time()
+    hosts = []
+    for r in range(args.ring):
+        layer = make_layer(r)
+        hosts.append(host_layer_from(layer, pin=True))
+        del layer
+        torch.cuda.empty_cache()
+    H, I, W, _ = make_inputs(1, args.routing)
+    ws = torch.empty(k.moe_workspace_bytes(N, TOPK, E, D, F), dtype=torch.uint8, device="cuda")
+    streamer = LayerStreamer(E, D, F, slots=2, timing=True)
+    log(f"[bench] stream: {args.ring} pinned host layers of {hosts[0].nbytes / 1e9:.2f} GB, setup "
+        f"{time.time() - t_setup:.1f}s")
+    # one warm sweep of a few layers (first-touch of the slots and the workspace)
+    for _, layer in streamer.stream(hosts[i % args.ring] for i in range(min(3, args.layers))):
+        k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
+    torch.cuda.synchronize()
+    streamer.copy_events.clear()
+    comp = []
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i, layer in streamer.stream(hosts[i % args.ring] for i in range(args.layers)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
+        b.record(stream)
+        comp.append((a, b))
+        if (i + 1) % 16 == 0:
+            log(f"[bench] stream: {i + 1} layers issued")
+    end.record(stream)
+    torch.cuda.synchronize()
+    t_total = start.elapsed_time(end) / 1e3
+    t_comp = sum(a.elapsed_time(b) for a, b in comp) / 1e3
+    copy_ms, copy_bytes = streamer.copy_stats()
+    t_copy = copy_ms / 1e3
+    hidden = max(0.0, min(1.0, (t_copy + t_comp - t_total) / t_comp)) if t_comp > 0 else 0.0
+    h2d = copy_bytes / t_copy / 1e9
+    line = {
+        "metric": "config 5 out-of-core sweep: tokens/s through all layers (H2D-bound)",
+        "value": N / t_total,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.layers,
+        "warmup": 3,
+        "ms_per_step": t_total * 1e3 / args.layers,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4",
+        "data": "synthetic",
+        "config": {"workload": f"config 5: {args.layers} routed-expert layers (config-3 shape, 20.96 GB each) "
+                               f"streamed from a ring of {args.ring} pinned host layers into 2 HBM slots, layer "
+                               f"forward for {N} tokens x {D}, top-{TOPK}",
+                   "routing": args.routing, "act": args.act},
+        "h2d_GBps": h2d,
+        "h2d_bytes_per_layer": copy_bytes / args.layers,
+        "copy_s": t_copy,
+        "compute_s": t_comp,
+        "total_s": t_total,
+        "hidden_compute_fraction": hidden,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,6 +226,10 @@ def main():
     ap.add_argument("--act", choices=["swiglu", "situ"], default="swiglu")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--workload", choices=["layer", "stream"], default="layer",
+                    help="layer: config 4 (the metric); stream: config 5, layers streamed from pinned host memory")
+    ap.add_argument("--layers", type=int, default=93, help="stream: layers per sweep (Kimi K3 has 93 MoE layers)")
+    ap.add_argument("--ring", type=int, default=2, help="stream: distinct pinned host layers cycled through")
     ap.add_argument("--lora-rank", type=int, default=0,
                     help="rank of the layer's gate/up/down LoRA adapters (0: off, the BASELINE configs)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -173,6 +247,9 @@ def main():
     from lazylora_amd.native import kernel
     k = kernel()
     torch.cuda.set_device(0)
+    if args.workload == "stream":
+        stream_main(args, k)
+        return
     t_setup = time.time()
     layer = make_layer(0)
     H, I, W, G = make_inputs(1, args.routing)

@@ -44,6 +44,14 @@ class ExpertLayer:
             t.to(self.device, non_blocking=True).contiguous() for t in tensors]
 
     @classmethod
+    def empty(cls, E: int, D: int, F: int, device=None) -> "ExpertLayer":
+        """An uninitialised layer in HBM (a destination for streamed or loaded experts)."""
+        if device is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        shapes = ((E, F, D // 2), (E, F, D // 32), (E, F, D // 2), (E, F, D // 32), (E, D, F // 2), (E, D, F // 32))
+        return cls(*[torch.empty(s, dtype=torch.uint8, device=device) for s in shapes], device=device)
+
+    @classmethod
     def from_bundles(cls, bundles: Sequence, device=None) -> "ExpertLayer":
         """Stack per-expert bundles with gate/up/down_packed and _scale attributes."""
         def stack(attr):

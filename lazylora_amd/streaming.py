@@ -1,0 +1,100 @@
+"""
+Out-of-core layer streaming: host-resident routed-expert layers through a ring of HBM slots.
+
+The reference streams experts from disk one at a time, reading ahead on a background thread
+so the drive keeps moving while the CPU multiplies (DynamicExpertStreamer.stream_experts,
+lazy_lora/streaming/expert_streamer.py:316-369, depth 2). On MI355X a whole layer of packed
+experts fits in HBM many times over, so the unit of streaming is the layer: `LayerStreamer`
+keeps `slots` HBM copies of the layer geometry and, on its own copy stream (default priority),
+copies layer i + slots - 1 from (pinned) host memory while the compute stream runs layer i.
+Ordering is by events only: a slot is refilled after the compute stream has recorded that it
+finished reading it, and the compute stream waits for the slot's copy before using it; the
+host never blocks except to throttle when all slots are in flight.
+"""
+from collections import deque
+from typing import Iterable, Iterator, List, Optional, Sequence, Tuple
+
+import torch
+
+from lazylora_amd.experts import ExpertLayer
+from lazylora_amd.loader import HostLayer, upload
+
+
+class LayerStreamer:
+    def __init__(self, E: int, D: int, F: int, slots: int = 2, device=None, timing: bool = False):
+        if slots < 2:
+            raise ValueError("streaming needs at least two HBM slots")
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.layers = [ExpertLayer.empty(E, D, F, self.device) for _ in range(slots)]
+        self.copy_stream = torch.cuda.Stream(device=self.device)
+        self.ready = [torch.cuda.Event() for _ in range(slots)]
+        self.free = [torch.cuda.Event() for _ in range(slots)]
+        self.timing = timing
+        self.copy_events: List[Tuple[torch.cuda.Event, torch.cuda.Event, int]] = []
+        self.bytes_copied = 0
+
+    @property
+    def slots(self) -> int:
+        return len(self.layers)
+
+    def _fill(self, slot: int, host: HostLayer, expert_ids: Optional[Sequence[int]]) -> None:
+        cs = self.copy_stream
+        cs.wait_event(self.free[slot])  # the compute stream has finished with the slot's last layer
+        t0 = t1 = None
+        if self.timing:
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record(cs)
+        n = upload(host, self.layers[slot], expert_ids, stream=cs)
+        if self.timing:
+            t1.record(cs)
+            self.copy_events.append((t0, t1, n))
+        self.ready[slot].record(cs)
+        self.bytes_copied += n
+
+    def stream(self, hosts: Iterable, expert_ids: Optional[Iterable] = None) -> Iterator[Tuple[int, ExpertLayer]]:
+        """Yields (i, layer in HBM) for each host layer in turn. The caller enqueues its work on
+        the current stream before asking for the next layer; the slot is then handed back. With
+        `expert_ids` (one id list per layer, or None per layer) only those experts are copied."""
+        hosts = iter(hosts)
+        ids = iter(expert_ids) if expert_ids is not None else None
+        compute = torch.cuda.current_stream(self.device)
+        for ev in self.free:
+            ev.record(compute)
+        pending = deque()
+        i = 0
+
+        def issue():
+            nonlocal i
+            try:
+                host = next(hosts)
+            except StopIteration:
+                return False
+            slot = i % self.slots
+            self._fill(slot, host, next(ids) if ids is not None else None)
+            pending.append((i, slot))
+            i += 1
+            return True
+
+        for _ in range(self.slots):
+            if not issue():
+                break
+        while pending:
+            j, slot = pending.popleft()
+            compute.wait_event(self.ready[slot])
+            yield j, self.layers[slot]
+            self.free[slot].record(compute)
+            issue()
+
+    def copy_stats(self) -> Tuple[float, int]:
+        """(total ms spent in the copies recorded with timing=True, bytes). Synchronises."""
+        torch.cuda.synchronize(self.device)
+        ms = sum(a.elapsed_time(b) for a, b, _ in self.copy_events)
+        return ms, sum(n for _, _, n in self.copy_events)
+
+
+def host_layer_from(layer: ExpertLayer, pin: Optional[bool] = None) -> HostLayer:
+    """A host copy of an HBM layer (test and benchmark helper)."""
+    h = HostLayer(layer.E, layer.D, layer.F, pin=pin)
+    for src, dst in zip(layer.tensors(), h.tensors):
+        dst.copy_(src)
+    return h
