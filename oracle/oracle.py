@@ -61,6 +61,26 @@ def dequant(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     return (E2M1[codes].reshape(R, K // 32, 32) * mult[:, :, None]).reshape(R, K)
 
 
+def quantize_mxfp4(w: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """(packed [R, K/2], scales [R, K/32]): the nearest MXFP4 encoding of W [R, K] (K % 32 == 0),
+    a test-input generator. Per 32-block the scale is the smallest power of two 2^e with
+    amax / 2^e <= 6 (no element saturates); each element takes the nearest E2M1 magnitude."""
+    w = np.asarray(w, np.float64)
+    R, K = w.shape
+    blocks = w.reshape(R, K // 32, 32)
+    amax = np.abs(blocks).max(-1)
+    e = np.where(amax > 0, np.ceil(np.log2(np.where(amax > 0, amax, 6.0) / 6.0)), -127)
+    sbyte = np.clip(e + 127, 0, MAX_SAFE_E8M0 - 1).astype(np.uint8)
+    scale = _E8M0[sbyte].astype(np.float64)
+    mags = np.abs(E2M1[:8]).astype(np.float64)
+    v = np.abs(blocks) / np.where(scale > 0, scale, 1.0)[..., None]
+    code = np.abs(v[..., None] - mags).argmin(-1).astype(np.uint8)
+    code |= (blocks < 0).astype(np.uint8) << 3
+    code = code.reshape(R, K)
+    packed = (code[:, 0::2] | (code[:, 1::2] << 4)).astype(np.uint8)
+    return packed, sbyte
+
+
 # ------------------------------------------------------------------------------------ products
 def gemm(x: np.ndarray, packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     """y[M, R] = x[M, K] . W^T in float64 (the semantics of mxfp4_gemm.c:64-94)."""
@@ -311,6 +331,24 @@ def routed_backward(h, topk_idx, topk_w, experts, grad_out, act: str = "swiglu",
     if lora is not None:
         return grad_h, grad_w, tuple(lg)
     return grad_h, grad_w
+
+
+def latent_moe_forward(x, p, experts=None, dense=None, lora=None, act: str = "situ"):
+    """Kimi-K3 latent MoE block (lazy_trainer.py:697-737) in float64, with moe.json's parameter
+    names: the shared expert at full width (shared_w1/w3/w2), the router on x (gate_weight,
+    e_score_correction_bias, top_k, routed_scale), the routed experts in the latent space
+    (down_weight, routed sum, RMSNorm with norm_weight when latent_norm, up_weight)."""
+    x = np.asarray(x, np.float64)
+    flat = x.reshape(-1, int(p["hidden"]))
+    a = lambda k: np.asarray(p[k], np.float64)
+    shared = glu_forward(flat @ a("shared_w1_weight").T, flat @ a("shared_w3_weight").T, act) @ a("shared_w2_weight").T
+    idx, w = router_forward(flat, a("gate_weight"), a("e_score_correction_bias"), top_k=int(p["top_k"]),
+                            routed_scaling_factor=float(p["routed_scale"]), renormalize=bool(p.get("renorm", 1)))
+    h_lat = flat @ a("down_weight").T
+    routed = routed_forward(h_lat, idx, w, experts, act, dense=dense, lora=lora)
+    if p.get("latent_norm", 1):
+        routed = rms_norm(routed, a("norm_weight"), eps=float(p.get("rms_eps", 1e-5)))
+    return (shared + routed @ a("up_weight").T).reshape(x.shape), idx, w
 
 
 def random_lora(rng: np.random.Generator, D: int, F: int, r: int, scale: float = 0.05, alpha: float = 32.0) -> LoRA:

@@ -111,27 +111,37 @@ def test_router_select_ties_and_bias_only_in_selection():
     assert idx.tolist() == [[5, 0]] and np.allclose(w, 0.5)
 
 
+def moe_params(fx):
+    return {k: (arr(v) if isinstance(v, dict) else v) for k, v in fx.items()}
+
+
 def test_moe_block_fixture():
-    """The latent MoE block of moe.json through the oracle's routed composition with the
-    fixture's dense expert weights (they are not MXFP4-representable)."""
+    """The latent MoE block of moe.json through the oracle's composition with the fixture's
+    dense expert weights (they are not MXFP4-representable)."""
     fx = load("moe")
-    x = arr(fx["in"])
-    hidden = fx["hidden"]
-    s_act = oracle.glu_forward(x @ arr(fx["shared_w1_weight"]).T, x @ arr(fx["shared_w3_weight"]).T, "situ")
-    shared = s_act @ arr(fx["shared_w2_weight"]).T
-    idx, w = oracle.router_forward(x, arr(fx["gate_weight"]), arr(fx["e_score_correction_bias"]),
-                                   top_k=fx["top_k"], routed_scaling_factor=fx["routed_scale"])
-    flat = x.reshape(-1, hidden)
-    h_lat = flat @ arr(fx["down_weight"]).T
+    p = moe_params(fx)
 
     def dense(e):
-        return tuple(arr(fx[f"experts_{e}_{m}_weight"]) for m in ("w1", "w3", "w2"))
+        return tuple(p[f"experts_{e}_{m}_weight"] for m in ("w1", "w3", "w2"))
 
-    routed = oracle.routed_forward(h_lat, idx, w, None, act="situ", dense=dense)
-    if fx["latent_norm"]:
-        routed = oracle.rms_norm(routed, arr(fx["norm_weight"]), eps=fx["rms_eps"])
-    got = shared + (routed @ arr(fx["up_weight"]).T).reshape(shared.shape)
-    assert_matches(got, arr(fx["out"]), abs_tol=2e-4)
+    got, _, _ = oracle.latent_moe_forward(p["in"], p, dense=dense)
+    assert_matches(got, p["out"], abs_tol=2e-4)
+
+
+def test_quantize_mxfp4_round_trip():
+    """Representable weights survive quantisation exactly; others move by at most half a step
+    of their block's grid (the largest E2M1 step is 2, times the block scale)."""
+    rng = np.random.default_rng(8)
+    pk, sc = oracle.random_mx(rng, (16, 128), 110, 130)
+    w = oracle.dequant(pk, sc)
+    qp, qs = oracle.quantize_mxfp4(w)
+    assert np.array_equal(oracle.dequant(qp, qs), w)
+    x = rng.standard_normal((8, 64)) * np.exp(rng.standard_normal((8, 1)))
+    qp, qs = oracle.quantize_mxfp4(x)
+    back = oracle.dequant(qp, qs).astype(np.float64)
+    step = oracle.e8m0_table()[qs].astype(np.float64).repeat(32, axis=1)
+    assert np.all(np.abs(back - x) <= step + 1e-12)
+    assert np.all(np.sign(back[back != 0]) == np.sign(x[back != 0]))
 
 
 @pytest.mark.parametrize("act", ["swiglu", "situ"])
