@@ -147,6 +147,71 @@ def make_lora(r: int):
     return (adapter(D, F), adapter(D, F), adapter(F, D))
 
 
+def expert_main(args, k):
+    """Config 2: the single-expert MXFP4 GLU block (gate/up 2048x7168, down 7168x2048) forward at
+    M = 1, 4, 16, 64, 256 tokens. One launch covers 32 distinct expert copies (749 MB, beyond the
+    256 MB MALL) with M tokens each, so every timed pass streams its weights from HBM; per-expert
+    figures are the launch's divided by 32."""
+    from lazylora_amd.experts import ExpertLayer
+    copies = 32
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2)
+    codes = lambda *sh: torch.randint(0, 256, sh, dtype=torch.uint8, device="cuda", generator=gen)
+    scales = lambda *sh: torch.randint(117, 122, sh, dtype=torch.uint8, device="cuda", generator=gen)
+    layer = ExpertLayer(codes(copies, F, D // 2), scales(copies, F, D // 32), codes(copies, F, D // 2),
+                        scales(copies, F, D // 32), codes(copies, D, F // 2), scales(copies, D, F // 32))
+    sweep = []
+    for M in (1, 4, 16, 64, 256):
+        n = copies * M
+        rng = np.random.default_rng(M)
+        H = torch.from_numpy(rng.standard_normal((n, D), dtype=np.float32)).cuda()
+        I = (torch.arange(n, device="cuda") // M).to(torch.int64).reshape(n, 1)
+        W = torch.ones((n, 1), device="cuda")
+        ws = torch.empty(k.moe_workspace_bytes(n, 1, copies, D, F), dtype=torch.uint8, device="cuda")
+        for _ in range(args.warmup):
+            k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
+        torch.cuda.synchronize()
+        k.set_timing(True)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / args.steps
+        calls = k.phase_times()
+        k.set_timing(False)
+        ph = {}
+        for call in calls:
+            for name, t in call:
+                ph.setdefault(name, []).append(t)
+        ph = {n_: float(np.mean(v)) for n_, v in ph.items()}
+        prod_ms = ph["fwd_gateup"] + ph["fwd_down"]
+        wbytes = copies * EXPERT_BYTES
+        row = {"M": M, "us_per_expert": ms * 1e3 / copies, "products_us_per_expert": prod_ms * 1e3 / copies,
+               "weight_GBps_products": wbytes / (prod_ms * 1e-3) / 1e9,
+               "frac_of_hbm_peak_products": wbytes / (prod_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+               "weight_GBps_whole_call": wbytes / (ms * 1e-3) / 1e9,
+               "TFLOPs_products": copies * 6.0 * F * D * M / (prod_ms * 1e-3) / 1e12,
+               "phases_ms": {n_: round(v, 4) for n_, v in ph.items()}}
+        sweep.append(row)
+        log(f"[bench] expert M={M:3d}: {row['us_per_expert']:7.2f} us/expert (products "
+            f"{row['products_us_per_expert']:6.2f} us, {row['weight_GBps_products']:7.1f} GB/s, "
+            f"{row['TFLOPs_products']:6.1f} TFLOP/s)")
+    line = {
+        "metric": "config 2: single-expert MXFP4 GLU block forward, weight GB/s of the products (M = 1)",
+        "value": sweep[0]["weight_GBps_products"],
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": sweep[0]["us_per_expert"] * copies / 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4", "data": "synthetic",
+        "config": {"workload": f"config 2: expert block gate/up {F}x{D}, down {D}x{F} MXFP4, M in 1..256 tokens, "
+                               f"{copies} distinct expert copies per launch", "act": args.act},
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def stream_main(args, k):
     """Config 5: an out-of-core sweep of `layers` routed-expert layers of the config-3 shape, each
     copied from pinned host memory (a ring of `ring` distinct layers, as 93 x 20.96 GB cannot be
@@ -226,8 +291,9 @@ def main():
     ap.add_argument("--act", choices=["swiglu", "situ"], default="swiglu")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["layer", "stream"], default="layer",
-                    help="layer: config 4 (the metric); stream: config 5, layers streamed from pinned host memory")
+    ap.add_argument("--workload", choices=["layer", "stream", "expert"], default="layer",
+                    help="layer: config 4 (the metric); stream: config 5, layers streamed from pinned host memory; "
+                         "expert: config 2, the single-expert block swept over token counts")
     ap.add_argument("--layers", type=int, default=93, help="stream: layers per sweep (Kimi K3 has 93 MoE layers)")
     ap.add_argument("--ring", type=int, default=2, help="stream: distinct pinned host layers cycled through")
     ap.add_argument("--lora-rank", type=int, default=0,
@@ -249,6 +315,9 @@ def main():
     torch.cuda.set_device(0)
     if args.workload == "stream":
         stream_main(args, k)
+        return
+    if args.workload == "expert":
+        expert_main(args, k)
         return
     t_setup = time.time()
     layer = make_layer(0)
