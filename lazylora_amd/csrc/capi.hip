@@ -95,7 +95,7 @@ long long pad32(long long v) { return (v + 31) / 32 * 32; }
 // Routed-layer workspace: one layout for forward and backward so the backward can reuse
 // what the forward left behind.
 struct MoeLayout {
-  size_t meta, counts, offsets, cursor, tiles, pair_token, pair_w, pair_of;
+  size_t meta, counts, offsets, cursor, tiles, small_tiles, groups, pair_token, pair_w, pair_of;
   size_t at_x, at_act;
   size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part;
   size_t l_u, l_delta, l_v, l_vsum, l_q, l_rq, l_dh, l_dsum, l_part;  // LoRA (rank <= kLoraMaxRank)
@@ -115,6 +115,8 @@ MoeLayout moe_layout(int N, int k, int E, int D, int F)
   L.offsets = o; o = align_up(o + sizeof(int) * (size_t)(E + 1));
   L.cursor = o; o = align_up(o + sizeof(int) * (size_t)E);
   L.tiles = o; o = align_up(o + sizeof(int4) * (size_t)L.max_tiles);
+  L.small_tiles = o; o = align_up(o + sizeof(int) * (size_t)L.max_tiles);
+  L.groups = o; o = align_up(o + sizeof(int4) * (size_t)L.max_tiles);
   L.pair_token = o; o = align_up(o + sizeof(int) * (size_t)P);
   L.pair_w = o; o = align_up(o + sizeof(float) * (size_t)P);
   L.pair_of = o; o = align_up(o + sizeof(int) * (size_t)P);
@@ -167,6 +169,15 @@ int check_moe_args(const void* h, int h_dtype, const void* idx, int idx_dtype, c
   return MXFP4_OK;
 }
 
+// Small-bucket tile list and large-bucket groups of the routed layer (see launch_route).
+void set_buckets(mx::FwdArgs& a, void* ws, const MoeLayout& L)
+{
+  a.small_tiles = at<int>(ws, L.small_tiles);
+  a.n_small = at<int>(ws, L.meta) + 2;
+  a.groups = at<int4>(ws, L.groups);
+  a.n_groups = at<int>(ws, L.meta) + 3;
+}
+
 // The layer's LoRA adapters, shared by all its experts (lazy_trainer.py:130-134).
 struct Lora {
   const float* m[6] = {};  // A_gate [r, D], B_gate [F, r], A_up [r, D], B_up [F, r], A_down [r, F], B_down [D, r]
@@ -204,7 +215,8 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
 {
   const long long P = (long long)N * k;
   MX_TRY(mx::launch_route(idx, idx_dtype == MXFP4_I64, w, N, k, E, at<int>(ws, L.counts), at<int>(ws, L.offsets),
-                          at<int>(ws, L.cursor), at<int4>(ws, L.tiles), at<int>(ws, L.meta), at<int>(ws, L.pair_token),
+                          at<int>(ws, L.cursor), at<int4>(ws, L.tiles), at<int>(ws, L.small_tiles),
+                          at<int4>(ws, L.groups), at<int>(ws, L.meta), at<int>(ws, L.pair_token),
                           at<float>(ws, L.pair_w), at<int>(ws, L.pair_of), s),
          "route");
   MX_PHASE("route", s);
@@ -224,6 +236,7 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   a.tiles = at<int4>(ws, L.tiles); a.n_tiles = at<int>(ws, L.meta);
   a.n_ct = F / 32;
   a.q_tiles = at<uint8_t>(ws, L.at_act);
+  set_buckets(a, ws, L);
   a.save = (save || lo.r) ? at<float>(ws, L.saved) : nullptr;
   a.act_kind = act_kind;
   const int r = lo.r;
@@ -379,6 +392,7 @@ int mxfp4_moe_forward_lora(float* out, const void* h, int h_dtype, const void* t
   a.n_ct = (D + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
   a.y = at<float>(workspace, L.ypair); a.ldy = D;
   a.row_w = at<float>(workspace, L.pair_w);
+  set_buckets(a, workspace, L);
   MX_TRY(mx::launch_fwd(a, mx::kFwdDown, L.max_tiles, stream), "moe_forward: down product");
   MX_PHASE("fwd_down", stream);
   MX_TRY(mx::launch_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D, stream),

@@ -53,22 +53,25 @@ struct WorkItem {
 // over the 8 XCDs (blockIdx % 8). Each XCD owns one contiguous run of work items, so the tiles
 // of one expert share that XCD's L2; its work-groups take the run's items in turn (iteration
 // `it` of slot s takes item s + it * slots). Returns false for the whole work-group at once.
-__device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, int M, int n_ct, int wave,
-                                            int it, WorkItem& w)
+typedef const __attribute__((address_space(4))) int* cint_ptr;
+
+__device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, const int* small_tiles,
+                                            const int* n_small, int M, int n_ct, int wave, int it, WorkItem& w)
 {
-  // The tile list is written before this kernel and only read here: scalar loads through the
+  // The tile lists are written before this kernel and only read here: scalar loads through the
   // constant address space, which do not wait for this work-group's outstanding stores.
-  typedef const __attribute__((address_space(4))) int* cint_ptr;
-  const int ntiles = tiles ? *(cint_ptr)n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  const int ntiles = small_tiles ? *(cint_ptr)n_small
+                                 : tiles ? *(cint_ptr)n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
   const int n_cg = (n_ct + kWavesPerGroup - 1) / kWavesPerGroup;
   const int total = ntiles * n_cg;
   const int per_xcd = (total + 7) >> 3;
   const int k = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
   const int item = (int)(blockIdx.x & 7) * per_xcd + k;
   if (k >= per_xcd || item >= total) return false;
-  const int t = item / n_cg;
+  const int i = item / n_cg;
+  const int t = small_tiles ? ((cint_ptr)small_tiles)[i] : i;
   w.tile = t;
-  w.ct0 = (item - t * n_cg) * kWavesPerGroup;
+  w.ct0 = (item - i * n_cg) * kWavesPerGroup;
   const int ct = w.ct0 + wave;
   w.active = ct < n_ct;
   w.ct = w.active ? ct : n_ct - 1;
@@ -214,6 +217,68 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
     }
   }
 }
+
+// Epilogue straight from the accumulators (one wave, no LDS): lane (j, g) holds rows 4g+v
+// (v = 0..3) of columns grp*16 + j.
+template <int MODE>
+__device__ __forceinline__ void epilogue_direct(const FwdArgs& a, const WorkItem& w, int lane, const f32x4 (&acc)[4],
+                                                const float (&tw)[4])
+{
+  const int j = lane & 15, g = lane >> 4;
+  if (MODE == kFwdGateUp) {
+    // rows 4g+v: gate features j and 16+j (groups 0, 1), up features the same (groups 2, 3)
+    const int F = a.R;
+    const int f0 = w.ct * 32;
+    uint8_t* qt = a.q_tiles + (long long)w.tile * at_tile_bytes(F);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int i = 4 * g + v;
+      float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
+      if (a.lora_delta && i < w.nrows) {  // LoRA gate/up delta of the row's token
+        const float* dl = a.lora_delta + (long long)a.row_token[w.row0 + i] * 2 * F + f0 + j;
+        ga += dl[0];
+        gb += dl[16];
+        ua += dl[F];
+        ub += dl[F + 16];
+      }
+      const float a0 = glu_fwd(ga, ua, a.act_kind), a1 = glu_fwd(gb, ub, a.act_kind);
+      if (a.save && i < w.nrows) {
+        float* sv = a.save + (long long)(w.row0 + i) * 2 * F;
+        sv[f0 + j] = ga;
+        sv[f0 + 16 + j] = gb;
+        sv[F + f0 + j] = ua;
+        sv[F + f0 + 16 + j] = ub;
+      }
+      // act -> the down product's A operand (AT layout, same tile). Unused row slots carry
+      // zeros (their inputs were zero), which is what the layout expects.
+      const Quant2 q = quant2_block16(a0, a1);  // the 16 lanes of row i hold its 32 features
+      qt[at_code_off(i, f0 + j, 0)] = (uint8_t)q.hi;
+      qt[at_code_off(i, f0 + 16 + j, 0)] = (uint8_t)(q.hi >> 8);
+      qt[at_code_off(i, f0 + j, 1)] = (uint8_t)q.lo;
+      qt[at_code_off(i, f0 + 16 + j, 1)] = (uint8_t)(q.lo >> 8);
+      if (j == 0) {
+        qt[at_scale_off(i, f0, 0)] = (uint8_t)q.s_hi;
+        qt[at_scale_off(i, f0, 1)] = (uint8_t)q.s_lo;
+      }
+    }
+    return;
+  }
+
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int i = 4 * g + v;
+    if (i >= w.nrows) continue;
+    const int row = w.row0 + i;
+    const float wv = MODE == kFwdDown ? tw[v] : 1.0f;
+    float* yr = a.y + (long long)row * a.ldy;
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      const int col = w.ct * kFwdColsPerTile + grp * 16 + j;
+      if (col < a.R) yr[col] = acc[grp][v] * wv;
+    }
+  }
+}
+
 
 // One work item: the 16 x 64 tile (w.tile, w.ct) over all of K, then its epilogue.
 template <int MODE, bool FAST>
@@ -384,62 +449,7 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
     return;
   }
 
-  if (!w.active) return;
-
-  // epilogue, straight from the accumulators: lane (j, g) holds rows 4g+v (v = 0..3) of
-  // columns grp*16 + j
-  if (MODE == kFwdGateUp) {
-    // rows 4g+v: gate features j and 16+j (groups 0, 1), up features the same (groups 2, 3)
-    const int F = a.R;
-    const int f0 = w.ct * 32;
-    uint8_t* qt = a.q_tiles + (long long)w.tile * at_tile_bytes(F);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int i = 4 * g + v;
-      float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
-      if (a.lora_delta && i < w.nrows) {  // LoRA gate/up delta of the row's token
-        const float* dl = a.lora_delta + (long long)a.row_token[w.row0 + i] * 2 * F + f0 + j;
-        ga += dl[0];
-        gb += dl[16];
-        ua += dl[F];
-        ub += dl[F + 16];
-      }
-      const float a0 = glu_fwd(ga, ua, a.act_kind), a1 = glu_fwd(gb, ub, a.act_kind);
-      if (a.save && i < w.nrows) {
-        float* sv = a.save + (long long)(w.row0 + i) * 2 * F;
-        sv[f0 + j] = ga;
-        sv[f0 + 16 + j] = gb;
-        sv[F + f0 + j] = ua;
-        sv[F + f0 + 16 + j] = ub;
-      }
-      // act -> the down product's A operand (AT layout, same tile). Unused row slots carry
-      // zeros (their inputs were zero), which is what the layout expects.
-      const Quant2 q = quant2_block16(a0, a1);  // the 16 lanes of row i hold its 32 features
-      qt[at_code_off(i, f0 + j, 0)] = (uint8_t)q.hi;
-      qt[at_code_off(i, f0 + 16 + j, 0)] = (uint8_t)(q.hi >> 8);
-      qt[at_code_off(i, f0 + j, 1)] = (uint8_t)q.lo;
-      qt[at_code_off(i, f0 + 16 + j, 1)] = (uint8_t)(q.lo >> 8);
-      if (j == 0) {
-        qt[at_scale_off(i, f0, 0)] = (uint8_t)q.s_hi;
-        qt[at_scale_off(i, f0, 1)] = (uint8_t)q.s_lo;
-      }
-    }
-    return;
-  }
-
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int i = 4 * g + v;
-    if (i >= w.nrows) continue;
-    const int row = w.row0 + i;
-    const float wv = MODE == kFwdDown ? tw[v] : 1.0f;
-    float* yr = a.y + (long long)row * a.ldy;
-#pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-      const int col = w.ct * kFwdColsPerTile + grp * 16 + j;
-      if (col < a.R) yr[col] = acc[grp][v] * wv;
-    }
-  }
+  if (w.active) epilogue_direct<MODE>(a, w, lane, acc, tw);
 }
 
 template <int MODE, bool FAST>
@@ -448,7 +458,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps control flow scalar
   WorkItem w;
-  for (int it = 0; decode_work(a.tiles, a.n_tiles, a.M, a.n_ct, wave, it, w); ++it) {
+  for (int it = 0; decode_work(a.tiles, a.n_tiles, a.small_tiles, a.n_small, a.M, a.n_ct, wave, it, w); ++it) {
     // the previous item's reads of LDS are complete before this item's copies land there;
     // its output stores drain while this item's first loads are in flight
     if (FAST && it > 0) __syncthreads();
@@ -456,6 +466,167 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
     int l = lane;
     asm volatile("" : "+v"(l));
     fwd_item<MODE, FAST>(a, w, wave, l);
+  }
+}
+
+// ---------------------------------------------------------------- large buckets
+// An expert with many rows would re-read each weight byte once per 16-row tile. Its tiles are
+// processed in groups of up to four: a work-group takes one column tile of the group, wave w
+// takes row tile w, and the column tile's weights go through LDS once per super-chunk for all
+// four waves (64 weight rows x 256 B of codes, plus 16 B of scales per row). Each wave streams
+// its own tile's activations from memory one super-chunk ahead.
+//
+// LDS layout of the codes: row rr (0..63, = column group * 16 + row in group) holds its 16
+// 16-byte units at unit rr * 16 + (u ^ (rr & 7)); the XOR spreads the eight rows read together
+// by one 128-bit LDS instruction over all 32 banks. The copies place units with LDS DMA, which
+// writes a wave's 64 lanes to one contiguous KiB, so the swizzle is applied to the source
+// addresses: LDS unit p of an instruction fetches unit (p % 16) ^ (rr & 7) of row rr.
+constexpr int kGrpRows = 64;
+constexpr int kGrpCodeBytes = kGrpRows * 256;
+constexpr int kGrpLdsBytes = kGrpCodeBytes + kGrpRows * 16;
+
+struct GroupLds {
+  uint8_t b[2][kGrpLdsBytes];
+};
+
+__device__ __forceinline__ bool decode_group(const FwdArgs& a, int wave, int it, WorkItem& w)
+{
+  const int ng = *(cint_ptr)a.n_groups;
+  const int total = ng * a.n_ct;
+  const int per_xcd = (total + 7) >> 3;
+  const int k = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
+  const int item = (int)(blockIdx.x & 7) * per_xcd + k;
+  if (k >= per_xcd || item >= total) return false;
+  const int gi = item / a.n_ct;
+  w.ct = item - gi * a.n_ct;
+  w.ct0 = w.ct;
+  const cint_ptr gg = (cint_ptr)(a.groups + gi);
+  w.expert = gg[0];
+  const int t0 = gg[1], nt = gg[2];
+  w.active = wave < nt;
+  w.tile = t0 + (w.active ? wave : 0);
+  const cint_ptr tt = (cint_ptr)(a.tiles + w.tile);
+  w.row0 = tt[1];
+  w.nrows = tt[2];
+  return true;
+}
+
+template <int MODE>
+__device__ __forceinline__ void fwd_group_item(const FwdArgs& a, const WorkItem& w, int wave, int lane)
+{
+  __shared__ GroupLds lds;
+  const int j = lane & 15, g = lane >> 4;
+  const int nb = a.K / kGroup;
+  const int nsc = at_nchunks(a.K);
+  const uint8_t* const at_tile = a.a_tiles + (long long)w.tile * at_tile_bytes(a.K);
+
+  auto grp_row = [&](int grp) {
+    return MODE == kFwdGateUp ? w.ct * 32 + (grp & 1) * 16 : w.ct * kFwdColsPerTile + grp * 16;
+  };
+  auto grp_wp = [&](int grp) {
+    return (MODE == kFwdGateUp && grp >= 2 ? a.wp1 : a.wp0) + (long long)w.expert * a.wp_estride;
+  };
+  auto grp_ws = [&](int grp) {
+    return (MODE == kFwdGateUp && grp >= 2 ? a.ws1 : a.ws0) + (long long)w.expert * a.ws_estride;
+  };
+
+  // B(c) -> lds.b[buf]: instruction u of wave `wave` covers rows 4 (4 wave + u) .. +3; wave 0
+  // also copies the 64 rows' 16 scale bytes of the chunk
+  auto issue_b = [&](int c, int buf) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int rr = (4 * wave + u) * 4 + (ln >> 4);
+      const int grp = rr >> 4;
+      const int n = min(grp_row(grp) + (rr & 15), a.R - 1);
+      const uint32_t off = (uint32_t)(n * (a.K / 2) + c * 256 + (((ln & 15) ^ (rr & 7)) << 4));
+      dma16(grp_wp(grp) + off, &lds.b[buf][(4 * wave + u) * 1024]);
+    }
+    if (wave == 0) {
+      const int grp = ln >> 4;
+      const int n = min(grp_row(grp) + (ln & 15), a.R - 1);
+      dma16(grp_ws(grp) + (uint32_t)(n * nb + c * 16), &lds.b[buf][kGrpCodeBytes]);
+    }
+  };
+  struct AChunk {
+    i32x4 v[16];
+    uint2 s;
+  };
+  auto load_a = [&](int c, AChunk& x) {
+    const uint8_t* p = at_tile + (long long)c * kAtChunkBytes + lane * 16;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) x.v[4 * q + h] = ldg16(p + q * 4096 + h * 1024);
+    x.s = *reinterpret_cast<const uint2*>(at_tile + (long long)c * kAtChunkBytes + kAtCodeBytes + lane * 8);
+  };
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) acc[grp] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float tw[4];
+  if (MODE == kFwdDown)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tw[v] = a.row_w[w.row0 + min(4 * g + v, w.nrows - 1)];
+
+  auto step = [&](int c, AChunk& cur, AChunk& nxt) {
+    wait_vm0();
+    __syncthreads();
+    const uint8_t* lb = lds.b[c & 1];
+    i32x4 b[4][4];
+    uint32_t sb[4];
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      const int rr = grp * 16 + j;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        b[grp][q] = *reinterpret_cast<const i32x4*>(lb + (rr * 16 + ((g * 4 + q) ^ (rr & 7))) * 16);
+      sb[grp] = *reinterpret_cast<const uint32_t*>(lb + kGrpCodeBytes + rr * 16 + g * 4);
+    }
+    wait_lgkm0();
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < nsc) {
+      issue_b(c + 1, (c + 1) & 1);
+      if (w.active) load_a(c + 1, nxt);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (w.active) {
+      sanitize(b, sb);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const i32x8 ah = cat8(cur.v[4 * q], cur.v[4 * q + 1]), al = cat8(cur.v[4 * q + 2], cur.v[4 * q + 3]);
+        if (q == 0) mfma_step<0>(acc, ah, al, b, sb, (int)cur.s.x, (int)cur.s.y);
+        if (q == 1) mfma_step<1>(acc, ah, al, b, sb, (int)cur.s.x, (int)cur.s.y);
+        if (q == 2) mfma_step<2>(acc, ah, al, b, sb, (int)cur.s.x, (int)cur.s.y);
+        if (q == 3) mfma_step<3>(acc, ah, al, b, sb, (int)cur.s.x, (int)cur.s.y);
+      }
+    }
+  };
+
+  AChunk a0, a1;
+  issue_b(0, 0);
+  if (w.active) load_a(0, a0);
+  for (int c = 0;;) {
+    step(c, a0, a1);
+    if (++c >= nsc) break;
+    step(c, a1, a0);
+    if (++c >= nsc) break;
+  }
+  if (w.active) epilogue_direct<MODE>(a, w, lane, acc, tw);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void fwd_group_kernel(FwdArgs a)
+{
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  WorkItem w;
+  for (int it = 0; decode_group(a, wave, it, w); ++it) {
+    if (it > 0) __syncthreads();  // every wave is done with the previous item's LDS buffers
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    fwd_group_item<MODE>(a, w, wave, l);
   }
 }
 
@@ -479,8 +650,15 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   if (total <= 0) return hipSuccess;
   const long long blocks = std::min<long long>((total + 7) / 8 * 8, resident_groups());
   const bool fast = (a.K % kChunk) == 0;
+  // the bucket split needs the tile list and the fast path; otherwise every tile takes fwd_kernel
+  const bool split = fast && a.tiles && a.small_tiles && a.groups;
+  FwdArgs b = a;
+  if (!split) {
+    b.small_tiles = nullptr;
+    b.groups = nullptr;
+  }
   dim3 grid((unsigned)blocks), block(64 * kWavesPerGroup);
-#define MX_LAUNCH(M, F) hipLaunchKernelGGL((fwd_kernel<M, F>), grid, block, 0, s, a)
+#define MX_LAUNCH(M, F) hipLaunchKernelGGL((fwd_kernel<M, F>), grid, block, 0, s, b)
   if (mode == kFwdPlain) {
     if (fast) MX_LAUNCH(kFwdPlain, true); else MX_LAUNCH(kFwdPlain, false);
   } else if (mode == kFwdGateUp) {
@@ -489,6 +667,12 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
     if (fast) MX_LAUNCH(kFwdDown, true); else MX_LAUNCH(kFwdDown, false);
   }
 #undef MX_LAUNCH
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !split) return e;
+  dim3 ggrid((unsigned)resident_groups());
+  if (mode == kFwdGateUp) hipLaunchKernelGGL(fwd_group_kernel<kFwdGateUp>, ggrid, block, 0, s, b);
+  else if (mode == kFwdDown) hipLaunchKernelGGL(fwd_group_kernel<kFwdDown>, ggrid, block, 0, s, b);
+  else hipLaunchKernelGGL(fwd_group_kernel<kFwdPlain>, ggrid, block, 0, s, b);
   return hipGetLastError();
 }
 

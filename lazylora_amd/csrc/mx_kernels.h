@@ -39,6 +39,14 @@ struct FwdArgs {
   // kFwdGateUp with LoRA: gate|up of row p gain lora_delta[row_token[p], 0:2R) before the GLU
   const int* row_token;
   const float* lora_delta;  // [tokens, 2R] fp32, or null
+  // Bucket split (with a tile list and K a multiple of 512): the tiles of small buckets
+  // (indices into `tiles`) take the one-row-tile work-groups; large-bucket groups of up to
+  // kGroupTiles tiles ({expert, first tile, tiles, 0}) take work-groups that share each column
+  // tile's weights over the group's row tiles. Null small_tiles: every tile takes the first shape.
+  const int* small_tiles;
+  const int* n_small;
+  const int4* groups;
+  const int* n_groups;
 };
 
 // ---------------------------------------------------------------- transposed products
@@ -81,6 +89,8 @@ struct BwdArgs {
 };
 
 constexpr int kFwdRowsPerTile = 16;
+constexpr int kGroupTiles = 4;     // row tiles of one large-bucket work-group
+constexpr int kGroupMinTiles = 4;  // experts with at least this many tiles take the large-bucket path
 constexpr int kFwdColsPerTile = 64;  // kFwdPlain / kFwdDown; kFwdGateUp covers 32 features
 constexpr int kBwdColsPerTile = 512;
 
@@ -99,9 +109,12 @@ hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int
                              uint16_t* lo, hipStream_t s);
 hipError_t launch_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R,
                           hipStream_t s);
+// Routing: per-expert counts, scan, the tile list (tiles[t] = {expert, first pair row, rows}),
+// the small-bucket tile indices and the large-bucket groups ({expert, first tile, tiles, 0}),
+// meta = {tiles, flags (bit 0: an id outside [0, E)), small tiles, groups}, and the pair maps.
 hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, int N, int k, int E,
-                        int* counts, int* offsets, int* cursor, int4* tiles, int* meta, int* pair_token,
-                        float* pair_w, int* pair_of, hipStream_t s);
+                        int* counts, int* offsets, int* cursor, int4* tiles, int* small_tiles, int4* groups,
+                        int* meta, int* pair_token, float* pair_w, int* pair_of, hipStream_t s);
 hipError_t launch_combine(float* out, const float* ypair, long long ldy, const int* pair_of, int N, int k,
                           int D, hipStream_t s);
 hipError_t launch_combine_bwd(float* grad_h, float* grad_w, const float* dxpair, long long ldy,

@@ -114,6 +114,39 @@ def test_skewed_routing_large_buckets(k):
     assert_close(gw.cpu().numpy(), gw64, "skew grad_w")
 
 
+@pytest.mark.parametrize("topk", [1, 2])
+def test_large_bucket_groups(k, topk):
+    """Buckets of 200, 65, 64, 49, 48, 17 and 1 rows: the experts with four or more 16-row tiles
+    take the grouped work-groups (groups of 4 tiles, ragged last group and last tile), the rest the
+    one-tile work-groups; K = 1024 and 512 keep both products on the path that splits them."""
+    case(f"large-bucket groups: E=8, D=1024, F=512, top-{topk}")
+    rng = np.random.default_rng(18 + topk)
+    E, D, F = 8, 1024, 512
+    ex = oracle.random_experts(rng, E, D, F, 118, 122)
+    sizes = [200, 65, 64, 49, 48, 17, 1, 0]
+    first = np.concatenate([np.full(c, e) for e, c in enumerate(sizes)]).astype(np.int64)
+    rng.shuffle(first)
+    N = first.size
+    if topk == 1:
+        idx = first[:, None]
+        w = rng.uniform(0.5, 1.5, (N, 1)).astype(np.float32)
+    else:
+        second = (first + 1 + rng.integers(0, E - 1, N)) % E
+        idx = np.stack([first, second], 1).astype(np.int64)
+        w = rng.dirichlet([1, 1], N).astype(np.float32)
+    h = rng.standard_normal((N, D)).astype(np.float32)
+    g = rng.standard_normal((N, D)).astype(np.float32)
+    L = layer_of(ex)
+    H, I, W, G = (torch.from_numpy(a).cuda() for a in (h, idx, w, g))
+    for act in ("swiglu", "situ"):
+        assert_close(k.routed_forward(H, I, W, L, act=act).cpu().numpy(), oracle.routed_forward(h, idx, w, ex, act),
+                     f"groups fwd {act}")
+    gh, gw = k.routed_backward(H, I, W, L, G)
+    gh64, gw64 = oracle.routed_backward(h, idx, w, ex, g)
+    assert_close(gh.cpu().numpy(), gh64, "groups grad_h")
+    assert_close(gw.cpu().numpy(), gw64, "groups grad_w")
+
+
 def test_input_dtypes(k):
     """bf16 h gives the fp32 result of the same (bf16-representable) values; int32 ids = int64."""
     case("bf16 h, int32 topk ids")
