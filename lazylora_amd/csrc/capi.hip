@@ -170,7 +170,8 @@ int check_moe_args(const void* h, int h_dtype, const void* idx, int idx_dtype, c
 }
 
 // Small-bucket tile list and large-bucket groups of the routed layer (see launch_route).
-void set_buckets(mx::FwdArgs& a, void* ws, const MoeLayout& L)
+template <typename Args>
+void set_buckets(Args& a, void* ws, const MoeLayout& L)
 {
   a.small_tiles = at<int>(ws, L.small_tiles);
   a.n_small = at<int>(ws, L.meta) + 2;
@@ -489,6 +490,7 @@ int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out,
   b.act_kind = act_kind;
   b.d_hi = at<uint16_t>(workspace, L.d_hi); b.d_lo = at<uint16_t>(workspace, L.d_lo);
   b.gw_part = at<float>(workspace, L.gw_part);
+  set_buckets(b, workspace, L);
   b.lora_rq = r ? at<float>(workspace, L.l_rq) : nullptr;
   MX_TRY(mx::launch_bwd(b, mx::kBwdDownT, L.max_tiles, stream), "moe_backward: W2 transposed product");
   MX_PHASE("bwd_down_t", stream);
@@ -502,6 +504,7 @@ int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out,
   c.tiles = at<int4>(workspace, L.tiles); c.n_tiles = at<int>(workspace, L.meta);
   c.n_ct = (D + mx::kBwdColsPerTile - 1) / mx::kBwdColsPerTile;
   c.y = at<float>(workspace, L.ypair); c.ldy = D;
+  set_buckets(c, workspace, L);
   MX_TRY(mx::launch_bwd(c, mx::kBwdGateUpT, L.max_tiles, stream), "moe_backward: W1|W3 transposed product");
   MX_PHASE("bwd_gateup_t", stream);
   MX_TRY(mx::launch_combine_bwd(grad_h, grad_w, at<float>(workspace, L.ypair), D, at<float>(workspace, L.gw_part),

@@ -45,36 +45,63 @@ __device__ __forceinline__ int slab_off(int row, int q)  // byte offset of quad 
 {
   return row * kRowBytes + quad_pos(row, q) * 8;
 }
-constexpr int kPrefetch = 8;  // weight steps in flight per work-group (even)
-
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef const __attribute__((address_space(4))) int* cint_ptr;
 
+#ifndef MX_BWD_GROUP_T
+#define MX_BWD_GROUP_T 2
+#endif
+constexpr int kBwdGroupT = MX_BWD_GROUP_T;  // row tiles per large-bucket work item (2 or 4)
+
+// One work item: column tile ct of up to T row tiles of one expert (T = 1: a small-bucket tile;
+// T = kGroupTiles: a large-bucket group, whose tiles share every decoded slab).
+template <int T>
 struct WorkItem {
-  int expert, row0, nrows, ct;
+  int expert, ct, ntl;
+  int row0[T], nrows[T], tile[T];
 };
 
-__device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, int M, int n_ct,
-                                            WorkItem& w)
+template <int T>
+__device__ __forceinline__ bool decode_work(const BwdArgs& a, WorkItem<T>& w)
 {
-  // the tile list is only read here: scalar loads through the constant address space
-  typedef const __attribute__((address_space(4))) int* cint_ptr;
-  const int ntiles = tiles ? *(cint_ptr)n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
-  const int total = ntiles * n_ct;
+  // the tile lists are only read here: scalar loads through the constant address space
+  int count;
+  constexpr int kParts = T == 1 ? 1 : kGroupTiles / T;  // work items per group
+  if (T == 1) count = a.small_tiles ? *(cint_ptr)a.n_small
+                                    : a.tiles ? *(cint_ptr)a.n_tiles : (a.M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  else count = *(cint_ptr)a.n_groups * kParts;
+  const int total = count * a.n_ct;
   const int per_xcd = (total + 7) >> 3;
   const int slot = (int)(blockIdx.x >> 3);
   const int item = (int)(blockIdx.x & 7) * per_xcd + slot;
   if (slot >= per_xcd || item >= total) return false;
-  const int t = item / n_ct;
-  w.ct = item - t * n_ct;
-  if (tiles) {
-    const cint_ptr tt = (cint_ptr)(tiles + t);
-    w.expert = tt[0];
-    w.row0 = tt[1];
-    w.nrows = tt[2];
+  const int i = item / a.n_ct;
+  w.ct = item - i * a.n_ct;
+  int t0;
+  if (T == 1) {
+    t0 = a.small_tiles ? ((cint_ptr)a.small_tiles)[i] : i;
+    w.ntl = 1;
   } else {
-    w.expert = 0;
-    w.row0 = t * kFwdRowsPerTile;
-    w.nrows = min(kFwdRowsPerTile, M - w.row0);
+    const int part = i % kParts;
+    const cint_ptr gg = (cint_ptr)(a.groups + i / kParts);
+    t0 = gg[1] + part * T;
+    w.ntl = min(T, gg[2] - part * T);
+    if (w.ntl <= 0) return false;  // this part of a short group is empty
+  }
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt) {
+    const int t = t0 + (tt < w.ntl ? tt : 0);
+    w.tile[tt] = t;
+    if (a.tiles) {
+      const cint_ptr tl = (cint_ptr)(a.tiles + t);
+      w.expert = tl[0];
+      w.row0[tt] = tl[1];
+      w.nrows[tt] = tl[2];
+    } else {
+      w.expert = 0;
+      w.row0[tt] = t * kFwdRowsPerTile;
+      w.nrows[tt] = min(kFwdRowsPerTile, a.M - w.row0[tt]);
+    }
   }
   return true;
 }
@@ -106,14 +133,18 @@ __device__ __forceinline__ void store_block(uint8_t* slab, int row, int blk, con
         i32x4{(int)dec[4 * j], (int)dec[4 * j + 1], (int)dec[4 * j + 2], (int)dec[4 * j + 3]};
 }
 
-template <int MODE>
-__global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
+// T = 1: weight steps in flight per work-group kPrefetch = 8, two work-groups per CU. T > 1:
+// T times the matrix work per step, so a shorter ring hides the loads; T = 2 still fits two
+// work-groups per CU, T = 4 needs the whole register file (one per CU).
+template <int MODE, int T>
+__global__ __launch_bounds__(256, T <= 2 ? 2 : 1) void bwd_kernel(BwdArgs a)
 {
+  constexpr int kPrefetch = T == 1 ? 8 : 4;  // even
   __shared__ __attribute__((aligned(16))) uint8_t slab[2][kSlabBytes];
   __shared__ float dotred[4][16];
 
-  WorkItem w;
-  if (!decode_work(a.tiles, a.n_tiles, a.M, a.n_ct, w)) return;
+  WorkItem<T> w;
+  if (!decode_work<T>(a, w)) return;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -139,7 +170,7 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
   // counters stay exact and nothing touches the loaded data before its decode step. Clamped
   // blocks are harmless: columns >= C are never stored, and rows >= nseg*R meet zero
   // activations (zero padding of A, or the padding steps below). Rows >= R read the second
-  // segment (W3 after W1). Weight bytes are read exactly once: streaming loads.
+  // segment (W3 after W1). Weight bytes are read exactly once per work-group: streaming loads.
   auto load_raw = [&](int step, i32x4& r0, i32x4& r1, uint8_t& s0, uint8_t& s1) {
     const int r = min(step * kSlabRows + lr, rtot - 1);
     const bool seg = r >= a.R;
@@ -152,15 +183,22 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
     s1 = S[colB_c / kGroup];
   };
 
-  // A operand rows (rows past the tile end repeat the last row; never stored)
-  const int ri = w.row0 + min(li, w.nrows - 1);
-  const int arow = a.a_row_map ? a.a_row_map[ri] : ri;
-  const uint16_t* pah = a.a_hi + (long long)arow * a.lda + 8 * g;
-  const uint16_t* pal = a.a_lo + (long long)arow * a.lda + 8 * g;
-
-  f32x4 acc[8];
+  // A operand rows of each tile (rows past a tile's end repeat its last row; never stored)
+  const uint16_t* pah[T];
+  const uint16_t* pal[T];
 #pragma unroll
-  for (int cg = 0; cg < 8; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int tt = 0; tt < T; ++tt) {
+    const int ri = w.row0[tt] + min(li, w.nrows[tt] - 1);
+    const int arow = a.a_row_map ? a.a_row_map[ri] : ri;
+    pah[tt] = a.a_hi + (long long)arow * a.lda + 8 * g;
+    pal[tt] = a.a_lo + (long long)arow * a.lda + 8 * g;
+  }
+
+  f32x4 acc[T][8];
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+    for (int cg = 0; cg < 8; ++cg) acc[tt][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Pipeline: the raw blocks of the next kPrefetch steps are in flight in a register ring.
   // Within a step the next step's A loads are issued before the ring refill, so waiting for
@@ -169,7 +207,12 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
   uint8_t rs0[kPrefetch], rs1[kPrefetch];
   // Issue order is pinned (A first, then the ring slot by slot) so the loop head can wait
   // for slot 0 alone, whether it is entered from here or from the back edge.
-  i32x4 ahv = ldg16(pah), alv = ldg16(pal);
+  i32x4 ahv[T], alv[T];
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt) {
+    ahv[tt] = ldg16(pah[tt]);
+    alv[tt] = ldg16(pal[tt]);
+  }
 #pragma unroll
   for (int p = 0; p < kPrefetch; ++p) {
     __builtin_amdgcn_sched_barrier(0);
@@ -190,18 +233,20 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
       store_block(sl, lr, lc + 8, ring1[p], rs1[p]);
       __syncthreads();
       const int sn = min(s + 1, nsteps - 1);
-      const i32x4 ahn = ldg16(pah + sn * kSlabRows);
-      const i32x4 aln = ldg16(pal + sn * kSlabRows);
+      i32x4 ahn[T], aln[T];
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) {
+        ahn[tt] = ldg16(pah[tt] + sn * kSlabRows);
+        aln[tt] = ldg16(pal[tt] + sn * kSlabRows);
+      }
       __builtin_amdgcn_sched_barrier(0);
       load_raw(s + kPrefetch, ring0[p], ring1[p], rs0[p], rs1[p]);
       __builtin_amdgcn_sched_barrier(0);
 
       // padding steps (s >= nsteps) see clamped weights: zero their activations instead
       const bool real = s < nsteps;
-      const bf16x8 ah = __builtin_bit_cast(bf16x8, real ? ahv : i32x4{0, 0, 0, 0});
-      const bf16x8 al = __builtin_bit_cast(bf16x8, real ? alv : i32x4{0, 0, 0, 0});
       // B operands of this wave's 8 column groups (rows 8g..8g+7 of column cg*16 + li), each
-      // read just before its two MFMAs
+      // read just before its MFMAs
 #pragma unroll
       for (int cg = 0; cg < 8; ++cg) {
         const int q = wave * 32 + cg * 4 + (li & 3);
@@ -211,71 +256,93 @@ __global__ __launch_bounds__(256, 2) void bwd_kernel(BwdArgs a)
             (lds_i16x4*)(&sl[slab_off(8 * g + 4 + (li >> 2), q)]));
         const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
         const bf16x8 b = __builtin_bit_cast(bf16x8, bs);
-        acc[cg] = mfma_bf16(ah, b, acc[cg]);
-        acc[cg] = mfma_bf16(al, b, acc[cg]);
+        // the hi terms of all tiles, then the lo terms: consecutive MFMAs never share an
+        // accumulator when T > 1
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt)
+          if (tt < w.ntl)
+            acc[tt][cg] = mfma_bf16(__builtin_bit_cast(bf16x8, real ? ahv[tt] : i32x4{0, 0, 0, 0}), b, acc[tt][cg]);
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt)
+          if (tt < w.ntl)
+            acc[tt][cg] = mfma_bf16(__builtin_bit_cast(bf16x8, real ? alv[tt] : i32x4{0, 0, 0, 0}), b, acc[tt][cg]);
       }
-      ahv = ahn;
-      alv = aln;
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) {
+        ahv[tt] = ahn[tt];
+        alv[tt] = aln[tt];
+      }
     }
   }
 
-  // epilogue: lane (li, g) holds rows 4g..4g+3 of column c0 + wave*128 + cg*16 + li
-  if (MODE == kBwdDownT) {
-    const int F = a.C;
-    float dots[4] = {0.f, 0.f, 0.f, 0.f};
+  // epilogue, tile by tile: lane (li, g) holds rows 4g..4g+3 of column c0 + wave*128 + cg*16 + li
+  // (conditionals rather than break / continue, so the loop unrolls and acc stays in registers)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int i = 4 * g + v;
-      const bool row_ok = i < w.nrows;
-      const int p = w.row0 + (row_ok ? i : 0);
-      const float tw = a.row_w[p];
-      const float* sv = a.saved + (long long)p * 2 * F;
-      // LoRA: the down adapter's A_d^T q of the row's token joins g . W2
-      const float* rq = a.lora_rq ? a.lora_rq + (long long)a.a_row_map[p] * F : nullptr;
+  for (int tt = 0; tt < T; ++tt) {
+    const bool live = tt < w.ntl;  // uniform
+    const int row0 = w.row0[tt], nrows = w.nrows[tt];
+    if (MODE == kBwdDownT) {
+      const int F = a.C;
+      float dots[4] = {0.f, 0.f, 0.f, 0.f};
+      if (live) {
 #pragma unroll
-      for (int cg = 0; cg < 8; ++cg) {
-        const int f = c0 + wave * 128 + cg * 16 + li;
-        if (f < F) {
-          const float h = rq ? acc[cg][v] + rq[f] : acc[cg][v];
-          const float gt = sv[f], up = sv[F + f];
-          dots[v] += glu_fwd(gt, up, a.act_kind) * h;
-          float dg, du;
-          glu_bwd(tw * h, gt, up, a.act_kind, dg, du);
-          if (row_ok) {
-            const long long o = (long long)p * 2 * F + f;
-            const __bf16 dgh = (__bf16)dg, duh = (__bf16)du;
-            a.d_hi[o] = __builtin_bit_cast(uint16_t, dgh);
-            a.d_lo[o] = __builtin_bit_cast(uint16_t, (__bf16)(dg - (float)dgh));
-            a.d_hi[o + F] = __builtin_bit_cast(uint16_t, duh);
-            a.d_lo[o + F] = __builtin_bit_cast(uint16_t, (__bf16)(du - (float)duh));
+        for (int v = 0; v < 4; ++v) {
+          const int i = 4 * g + v;
+          const bool row_ok = i < nrows;
+          const int p = row0 + (row_ok ? i : 0);
+          const float tw = a.row_w[p];
+          const float* sv = a.saved + (long long)p * 2 * F;
+          // LoRA: the down adapter's A_d^T q of the row's token joins g . W2
+          const float* rq = a.lora_rq ? a.lora_rq + (long long)a.a_row_map[p] * F : nullptr;
+#pragma unroll
+          for (int cg = 0; cg < 8; ++cg) {
+            const int f = c0 + wave * 128 + cg * 16 + li;
+            if (f < F) {
+              const float h = rq ? acc[tt][cg][v] + rq[f] : acc[tt][cg][v];
+              const float gt = sv[f], up = sv[F + f];
+              dots[v] += glu_fwd(gt, up, a.act_kind) * h;
+              float dg, du;
+              glu_bwd(tw * h, gt, up, a.act_kind, dg, du);
+              if (row_ok) {
+                const long long o = (long long)p * 2 * F + f;
+                const __bf16 dgh = (__bf16)dg, duh = (__bf16)du;
+                a.d_hi[o] = __builtin_bit_cast(uint16_t, dgh);
+                a.d_lo[o] = __builtin_bit_cast(uint16_t, (__bf16)(dg - (float)dgh));
+                a.d_hi[o + F] = __builtin_bit_cast(uint16_t, duh);
+                a.d_lo[o + F] = __builtin_bit_cast(uint16_t, (__bf16)(du - (float)duh));
+              }
+            }
           }
         }
       }
-    }
+      if (live) {
+        if (tt > 0) __syncthreads();  // the previous tile's partial dots have been read
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float d = group16_sum(dots[v]);
-      if (li == 0) dotred[wave][4 * g + v] = d;
-    }
-    __syncthreads();
-    if (tid < 16 && tid < w.nrows) {
-      const float d = dotred[0][tid] + dotred[1][tid] + dotred[2][tid] + dotred[3][tid];
-      a.gw_part[(long long)(w.row0 + tid) * a.n_ct + w.ct] = d;
-    }
-    return;
-  }
-
+        for (int v = 0; v < 4; ++v) {
+          const float d = group16_sum(dots[v]);
+          if (li == 0) dotred[wave][4 * g + v] = d;
+        }
+        __syncthreads();
+        if (tid < 16 && tid < nrows) {
+          const float d = dotred[0][tid] + dotred[1][tid] + dotred[2][tid] + dotred[3][tid];
+          a.gw_part[(long long)(row0 + tid) * a.n_ct + w.ct] = d;
+        }
+      }
+    } else if (live) {
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int i = 4 * g + v;
-    if (i >= w.nrows) continue;
-    float* yr = a.y + (long long)(w.row0 + i) * a.ldy;
+      for (int v = 0; v < 4; ++v) {
+        const int i = 4 * g + v;
+        if (i < nrows) {
+          float* yr = a.y + (long long)(row0 + i) * a.ldy;
 #pragma unroll
-    for (int cg = 0; cg < 8; ++cg) {
-      const int col = c0 + wave * 128 + cg * 16 + li;
-      if (col < a.C) {
-        if (a.accumulate) yr[col] += acc[cg][v];
-        else yr[col] = acc[cg][v];
+          for (int cg = 0; cg < 8; ++cg) {
+            const int col = c0 + wave * 128 + cg * 16 + li;
+            if (col < a.C) {
+              if (a.accumulate) yr[col] += acc[tt][cg][v];
+              else yr[col] = acc[tt][cg][v];
+            }
+          }
+        }
       }
     }
   }
@@ -287,11 +354,26 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
 {
   const long long total = (long long)max_tiles * a.n_ct;
   if (total <= 0) return hipSuccess;
+  const bool split = a.tiles && a.small_tiles && a.groups;
+  BwdArgs b = a;
+  if (!split) {
+    b.small_tiles = nullptr;
+    b.groups = nullptr;
+  }
   const long long blocks = (total + 7) / 8 * 8;
   dim3 grid((unsigned)blocks), block(256);
-  if (mode == kBwdPlain) hipLaunchKernelGGL(bwd_kernel<kBwdPlain>, grid, block, 0, s, a);
-  else if (mode == kBwdDownT) hipLaunchKernelGGL(bwd_kernel<kBwdDownT>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(bwd_kernel<kBwdGateUpT>, grid, block, 0, s, a);
+  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, 1>), grid, block, 0, s, b);
+  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, 1>), grid, block, 0, s, b);
+  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, 1>), grid, block, 0, s, b);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !split) return e;
+  // groups come from experts of at least kGroupMinTiles tiles: at most max_tiles / 2 of them,
+  // each split into kGroupTiles / kBwdGroupT work items
+  const long long gtotal = ((long long)max_tiles / 2 + 1) * (kGroupTiles / kBwdGroupT) * a.n_ct;
+  dim3 ggrid((unsigned)((gtotal + 7) / 8 * 8));
+  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, kBwdGroupT>), ggrid, block, 0, s, b);
+  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, kBwdGroupT>), ggrid, block, 0, s, b);
+  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, kBwdGroupT>), ggrid, block, 0, s, b);
   return hipGetLastError();
 }
 

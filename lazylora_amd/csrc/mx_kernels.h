@@ -86,6 +86,12 @@ struct BwdArgs {
   // kBwdDownT with LoRA: h = g . W2 of row p gains lora_rq[a_row_map[p], 0:C) (the down
   // adapter's A^T q of the row's token), so both the GLU backward and grad_w see it
   const float* lora_rq;  // [tokens, C] fp32, or null
+  // Bucket split, as in FwdArgs: small-bucket tiles take one-tile work-groups, large-bucket
+  // groups work-groups that reuse each decoded weight slab for all of the group's tiles.
+  const int* small_tiles;
+  const int* n_small;
+  const int4* groups;
+  const int* n_groups;
 };
 
 constexpr int kFwdRowsPerTile = 16;
