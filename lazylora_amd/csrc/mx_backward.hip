@@ -21,6 +21,8 @@
 #include "mx_device.h"
 #include "mx_kernels.h"
 
+#include <algorithm>
+
 namespace mx {
 
 namespace {
@@ -61,32 +63,37 @@ struct WorkItem {
   int row0[T], nrows[T], tile[T];
 };
 
+// Work item `it` of this work-group (items are dealt round-robin over the XCDs, blockIdx % 8,
+// each XCD taking one contiguous run, in strides of the grid). Returns 0 when there is none
+// left, 2 for an empty part of a short group, 1 for an item.
 template <int T>
-__device__ __forceinline__ bool decode_work(const BwdArgs& a, WorkItem<T>& w)
+__device__ __forceinline__ int decode_work(const BwdArgs& a, int it, WorkItem<T>& w)
 {
   // the tile lists are only read here: scalar loads through the constant address space
   int count;
   constexpr int kParts = T == 1 ? 1 : kGroupTiles / T;  // work items per group
-  if (T == 1) count = a.small_tiles ? *(cint_ptr)a.n_small
-                                    : a.tiles ? *(cint_ptr)a.n_tiles : (a.M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  // with no large-bucket groups the small-bucket list is every tile in order: skip it
+  const bool use_small = a.small_tiles && *(cint_ptr)a.n_groups > 0;
+  if (T == 1) count = use_small ? *(cint_ptr)a.n_small
+                                : a.tiles ? *(cint_ptr)a.n_tiles : (a.M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
   else count = *(cint_ptr)a.n_groups * kParts;
   const int total = count * a.n_ct;
   const int per_xcd = (total + 7) >> 3;
-  const int slot = (int)(blockIdx.x >> 3);
+  const int slot = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
   const int item = (int)(blockIdx.x & 7) * per_xcd + slot;
-  if (slot >= per_xcd || item >= total) return false;
+  if (slot >= per_xcd || item >= total) return 0;
   const int i = item / a.n_ct;
   w.ct = item - i * a.n_ct;
   int t0;
   if (T == 1) {
-    t0 = a.small_tiles ? ((cint_ptr)a.small_tiles)[i] : i;
+    t0 = use_small ? ((cint_ptr)a.small_tiles)[i] : i;
     w.ntl = 1;
   } else {
     const int part = i % kParts;
     const cint_ptr gg = (cint_ptr)(a.groups + i / kParts);
     t0 = gg[1] + part * T;
     w.ntl = min(T, gg[2] - part * T);
-    if (w.ntl <= 0) return false;  // this part of a short group is empty
+    if (w.ntl <= 0) return 2;  // this part of a short group is empty
   }
 #pragma unroll
   for (int tt = 0; tt < T; ++tt) {
@@ -103,7 +110,7 @@ __device__ __forceinline__ bool decode_work(const BwdArgs& a, WorkItem<T>& w)
       w.nrows[tt] = min(kFwdRowsPerTile, a.M - w.row0[tt]);
     }
   }
-  return true;
+  return 1;
 }
 
 // 16 fp4 bytes (32 codes of one row) -> 32 bf16 in 16 dwords, scale byte s applied exactly;
@@ -137,14 +144,11 @@ __device__ __forceinline__ void store_block(uint8_t* slab, int row, int blk, con
 // T times the matrix work per step, so a shorter ring hides the loads; T = 2 still fits two
 // work-groups per CU, T = 4 needs the whole register file (one per CU).
 template <int MODE, int T>
-__global__ __launch_bounds__(256, T <= 2 ? 2 : 1) void bwd_kernel(BwdArgs a)
+__device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
 {
   constexpr int kPrefetch = T == 1 ? 8 : 4;  // even
   __shared__ __attribute__((aligned(16))) uint8_t slab[2][kSlabBytes];
   __shared__ float dotred[4][16];
-
-  WorkItem<T> w;
-  if (!decode_work<T>(a, w)) return;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -245,27 +249,36 @@ __global__ __launch_bounds__(256, T <= 2 ? 2 : 1) void bwd_kernel(BwdArgs a)
 
       // padding steps (s >= nsteps) see clamped weights: zero their activations instead
       const bool real = s < nsteps;
-      // B operands of this wave's 8 column groups (rows 8g..8g+7 of column cg*16 + li), each
-      // read just before its MFMAs
+      // B operands of this wave's 8 column groups (rows 8g..8g+7 of column cg*16 + li), read
+      // two groups at a time just before their MFMAs: the hi terms of both groups (and of every
+      // tile), then the lo terms, so no MFMA waits on the one issued just before it
 #pragma unroll
-      for (int cg = 0; cg < 8; ++cg) {
-        const int q = wave * 32 + cg * 4 + (li & 3);
-        const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(&sl[slab_off(8 * g + (li >> 2), q)]));
-        const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(&sl[slab_off(8 * g + 4 + (li >> 2), q)]));
-        const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
-        const bf16x8 b = __builtin_bit_cast(bf16x8, bs);
-        // the hi terms of all tiles, then the lo terms: consecutive MFMAs never share an
-        // accumulator when T > 1
+      for (int cp = 0; cp < 8; cp += 2) {
+        bf16x8 b[2];
 #pragma unroll
-        for (int tt = 0; tt < T; ++tt)
-          if (tt < w.ntl)
-            acc[tt][cg] = mfma_bf16(__builtin_bit_cast(bf16x8, real ? ahv[tt] : i32x4{0, 0, 0, 0}), b, acc[tt][cg]);
+        for (int h = 0; h < 2; ++h) {
+          const int q = wave * 32 + (cp + h) * 4 + (li & 3);
+          const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_i16x4*)(&sl[slab_off(8 * g + (li >> 2), q)]));
+          const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_i16x4*)(&sl[slab_off(8 * g + 4 + (li >> 2), q)]));
+          const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+          b[h] = __builtin_bit_cast(bf16x8, bs);
+        }
 #pragma unroll
-        for (int tt = 0; tt < T; ++tt)
-          if (tt < w.ntl)
-            acc[tt][cg] = mfma_bf16(__builtin_bit_cast(bf16x8, real ? alv[tt] : i32x4{0, 0, 0, 0}), b, acc[tt][cg]);
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int tt = 0; tt < T; ++tt)
+            if (tt < w.ntl)
+              acc[tt][cp + h] = mfma_bf16(__builtin_bit_cast(bf16x8, real ? ahv[tt] : i32x4{0, 0, 0, 0}), b[h],
+                                          acc[tt][cp + h]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int tt = 0; tt < T; ++tt)
+            if (tt < w.ntl)
+              acc[tt][cp + h] = mfma_bf16(__builtin_bit_cast(bf16x8, real ? alv[tt] : i32x4{0, 0, 0, 0}), b[h],
+                                          acc[tt][cp + h]);
       }
 #pragma unroll
       for (int tt = 0; tt < T; ++tt) {
@@ -348,6 +361,36 @@ __global__ __launch_bounds__(256, T <= 2 ? 2 : 1) void bwd_kernel(BwdArgs a)
   }
 }
 
+// T = 1: one item per work-group (the grid covers every item). T > 1: a resident grid that
+// loops over the large-bucket items, so launches with few or no groups cost almost nothing.
+template <int MODE, int T>
+__global__ __launch_bounds__(256, T <= 2 ? 2 : 1) void bwd_kernel(BwdArgs a)
+{
+  WorkItem<T> w;
+  if constexpr (T == 1) {
+    if (decode_work<T>(a, 0, w) == 1) bwd_item<MODE, T>(a, w);
+    return;
+  }
+  bool busy = false;
+  for (int it = 0;; ++it) {
+    const int st = decode_work<T>(a, it, w);
+    if (st == 0) break;
+    if (st == 2) continue;
+    if (busy) __syncthreads();  // the previous item's LDS reads are complete
+    bwd_item<MODE, T>(a, w);
+    busy = true;
+  }
+}
+
+int resident_groups(int per_cu)
+{
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return max(8, (per_cu * cus) / 8 * 8);
+}
+
 }  // namespace
 
 hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
@@ -370,7 +413,7 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
   // groups come from experts of at least kGroupMinTiles tiles: at most max_tiles / 2 of them,
   // each split into kGroupTiles / kBwdGroupT work items
   const long long gtotal = ((long long)max_tiles / 2 + 1) * (kGroupTiles / kBwdGroupT) * a.n_ct;
-  dim3 ggrid((unsigned)((gtotal + 7) / 8 * 8));
+  dim3 ggrid((unsigned)std::min<long long>((gtotal + 7) / 8 * 8, resident_groups(kBwdGroupT <= 2 ? 2 : 1)));
   if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, kBwdGroupT>), ggrid, block, 0, s, b);
   else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, kBwdGroupT>), ggrid, block, 0, s, b);
   else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, kBwdGroupT>), ggrid, block, 0, s, b);

@@ -56,12 +56,15 @@ struct WorkItem {
 typedef const __attribute__((address_space(4))) int* cint_ptr;
 
 __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, const int* small_tiles,
-                                            const int* n_small, int M, int n_ct, int wave, int it, WorkItem& w)
+                                            const int* n_small, const int* n_groups, int M, int n_ct, int wave,
+                                            int it, WorkItem& w)
 {
   // The tile lists are written before this kernel and only read here: scalar loads through the
   // constant address space, which do not wait for this work-group's outstanding stores.
-  const int ntiles = small_tiles ? *(cint_ptr)n_small
-                                 : tiles ? *(cint_ptr)n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  // with no large-bucket groups the small-bucket list is every tile in order: skip it
+  const bool use_small = small_tiles && *(cint_ptr)n_groups > 0;
+  const int ntiles = use_small ? *(cint_ptr)n_small
+                               : tiles ? *(cint_ptr)n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
   const int n_cg = (n_ct + kWavesPerGroup - 1) / kWavesPerGroup;
   const int total = ntiles * n_cg;
   const int per_xcd = (total + 7) >> 3;
@@ -69,7 +72,7 @@ __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tile
   const int item = (int)(blockIdx.x & 7) * per_xcd + k;
   if (k >= per_xcd || item >= total) return false;
   const int i = item / n_cg;
-  const int t = small_tiles ? ((cint_ptr)small_tiles)[i] : i;
+  const int t = use_small ? ((cint_ptr)small_tiles)[i] : i;
   w.tile = t;
   w.ct0 = (item - i * n_cg) * kWavesPerGroup;
   const int ct = w.ct0 + wave;
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps control flow scalar
   WorkItem w;
-  for (int it = 0; decode_work(a.tiles, a.n_tiles, a.small_tiles, a.n_small, a.M, a.n_ct, wave, it, w); ++it) {
+  for (int it = 0; decode_work(a.tiles, a.n_tiles, a.small_tiles, a.n_small, a.n_groups, a.M, a.n_ct, wave, it, w); ++it) {
     // the previous item's reads of LDS are complete before this item's copies land there;
     // its output stores drain while this item's first loads are in flight
     if (FAST && it > 0) __syncthreads();
