@@ -341,13 +341,15 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       if (wave == 0) dma16(src + kAtCodeBytes + (lane & 31) * 16, &lds.a[buf][kAtCodeBytes]);
     };
     // scale window win -> sw: instruction i covers rows 8i..8i+7 of this wave's 64, lane l
-    // copies 16 B (one super-chunk) of row 8i + l/8, chunk 8 win + l%8 (clamped to the row)
-    // (addresses are rebuilt at each call from uniform bases and 32-bit lane offsets rather
-    // than held in registers across the steps in between)
+    // copies 16 B (one super-chunk) of row 8i + l/8 into slot l%8 of that row; the slot holds
+    // chunk 8 win + ((l%8) ^ (row & 7)) (clamped to the row), so the 16 rows read together
+    // below spread over all 32 banks instead of sharing one (addresses are rebuilt at each call
+    // from uniform bases and 32-bit lane offsets rather than held in registers across the
+    // steps in between)
     auto issue_scales = [&](int win) {
       int ln = lane;
       asm volatile("" : "+v"(ln));
-      const int cc = min(win * kScaleWin + (ln & 7), nsc - 1);
+      const int cc = min(win * kScaleWin + ((ln & 7) ^ (ln >> 3)), nsc - 1);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int grp = i >> 1;
@@ -362,7 +364,8 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       uint32_t sb[4];
 #pragma unroll
       for (int grp = 0; grp < 4; ++grp)
-        sb[grp] = *reinterpret_cast<const uint32_t*>(sw + (grp * 16 + j) * kScaleRowBytes + (c % kScaleWin) * 16 + g * 4);
+        sb[grp] = *reinterpret_cast<const uint32_t*>(sw + (grp * 16 + j) * kScaleRowBytes +
+                                                     (((c % kScaleWin) ^ (j & 7)) * 16) + g * 4);
       const uint8_t* la = &lds.a[c & 1][lane * 16];
       i32x8 ah[4], al[4];
 #pragma unroll
