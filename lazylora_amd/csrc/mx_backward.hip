@@ -143,6 +143,13 @@ __device__ __forceinline__ void store_block(uint8_t* slab, int row, int blk, con
 // T = 1: weight steps in flight per work-group kPrefetch = 8, two work-groups per CU. T > 1:
 // T times the matrix work per step, so a shorter ring hides the loads; T = 2 still fits two
 // work-groups per CU, T = 4 needs the whole register file (one per CU).
+//
+// Step s of the main loop, after the barrier that publishes slab s: every wave issues all of
+// its transposed reads of slab s at once, then the loads that refill the rings, then decodes
+// step s + 1 into the other slab buffer in two halves, each followed by half of slab s's
+// MFMAs. The decode's VALU work and LDS writes thus overlap the matrix work and the read
+// latency is paid once per step. The other buffer held slab s - 1, whose reads every wave
+// finished (its MFMAs consumed them) before arriving at this step's barrier.
 template <int MODE, int T>
 __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
 {
@@ -156,38 +163,48 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
   const int c0 = w.ct * kBwdColsPerTile;
   const int rtot = a.nseg * a.R;
   const int nsteps = (rtot + kSlabRows - 1) / kSlabRows;
-  // the ring below is unrolled kPrefetch-fold; padding steps load nothing useful (zero weights)
+  // the ring below is unrolled kPrefetch-fold; padding steps read past the matrix (zeros)
   const int nsteps_pad = (nsteps + kPrefetch - 1) / kPrefetch * kPrefetch;
 
   // loader role: MX blocks lc and lc + 8 of slab row lr per step, so each load instruction
-  // of a wave reads whole 128-byte lines (8 rows x 8 blocks)
+  // of a wave reads whole 128-byte lines (8 rows x 8 blocks). Block lc + 8 sits 128 bytes
+  // (8 scale bytes) after block lc.
   const int lr = tid >> 3;
   const int lc = tid & 7;
-  const int cbs = a.C / kGroup;    // scale bytes per W row
-  const long long wpitch = a.C / 2;
-  const int colA = c0 + lc * 32, colB = c0 + (lc + 8) * 32;
-  const int colA_c = colA < a.C ? colA : 0, colB_c = colB < a.C ? colB : 0;
-  const long long wbase = (long long)w.expert * a.wp_estride;
-  const long long sbase = (long long)w.expert * a.ws_estride;
+  const uint32_t cbs = a.C / kGroup;  // scale bytes per W row
+  const uint32_t wpitch = a.C / 2;
+  const int colA = c0 + lc * 32;
+  const int colA_c = colA < a.C ? colA : 0;
+  // Each segment of this expert is one buffer resource: rows at or past the segment's end
+  // (the tail of a row count that is not a multiple of kSlabRows, and the padding steps) read
+  // as zero weights. Segments hold a multiple of kSlabRows rows whenever there are two, so a
+  // step never straddles them. Columns past C (lanes clamped to column 0, or block lc + 8 of a
+  // partial tile) read other finite weights that no stored column uses.
+  const uint8_t* const wp0 = a.wp0 + (long long)w.expert * a.wp_estride;
+  const uint8_t* const wp1 = a.wp1 + (long long)w.expert * a.wp_estride;
+  const uint8_t* const ws0 = a.ws0 + (long long)w.expert * a.ws_estride;
+  const uint8_t* const ws1 = a.ws1 + (long long)w.expert * a.ws_estride;
+  const rsrc_t rw0 = make_rsrc(wp0, (uint32_t)a.R * wpitch), rw1 = make_rsrc(wp1, (uint32_t)a.R * wpitch);
+  const rsrc_t rs0_ = make_rsrc(ws0, (uint32_t)a.R * cbs), rs1_ = make_rsrc(ws1, (uint32_t)a.R * cbs);
+  const uint32_t lane_w = (uint32_t)lr * wpitch + colA_c / 2;
+  const uint32_t lane_s = (uint32_t)lr * cbs + colA_c / kGroup;
 
-  // Always issues the loads, with rows and columns clamped into the matrix, so the wait
-  // counters stay exact and nothing touches the loaded data before its decode step. Clamped
-  // blocks are harmless: columns >= C are never stored, and rows >= nseg*R meet zero
-  // activations (zero padding of A, or the padding steps below). Rows >= R read the second
-  // segment (W3 after W1). Weight bytes are read exactly once per work-group: streaming loads.
+  // Weight bytes are read exactly once per work-group: streaming loads.
   auto load_raw = [&](int step, i32x4& r0, i32x4& r1, uint8_t& s0, uint8_t& s1) {
-    const int r = min(step * kSlabRows + lr, rtot - 1);
-    const bool seg = r >= a.R;
-    const int rr = seg ? r - a.R : r;
-    const uint8_t* P = (seg ? a.wp1 : a.wp0) + wbase + (long long)rr * wpitch;
-    const uint8_t* S = (seg ? a.ws1 : a.ws0) + sbase + (long long)rr * cbs;
-    r0 = ldg16_nt(P + colA_c / 2);
-    r1 = ldg16_nt(P + colB_c / 2);
-    s0 = S[colA_c / kGroup];
-    s1 = S[colB_c / kGroup];
+    const int row0 = step * kSlabRows;
+    const bool seg = a.nseg > 1 && row0 >= a.R;  // uniform
+    const uint32_t rr = (uint32_t)(seg ? row0 - a.R : row0);
+    const rsrc_t W = seg ? rw1 : rw0;
+    const rsrc_t S = seg ? rs1_ : rs0_;
+    const uint32_t ow = lane_w + rr * wpitch, os = lane_s + rr * cbs;
+    r0 = buf16_nt(W, ow);
+    r1 = buf16_nt(W, ow + 128);
+    s0 = buf8(S, os);
+    s1 = buf8(S, os + 8);
   };
 
-  // A operand rows of each tile (rows past a tile's end repeat its last row; never stored)
+  // A operand rows of each tile (rows past a tile's end repeat its last row; never stored).
+  // Padding steps meet zero weights, so their A (the last real step's, reloaded) adds zero.
   const uint16_t* pah[T];
   const uint16_t* pal[T];
 #pragma unroll
@@ -223,19 +240,31 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
     load_raw(p, ring0[p], ring1[p], rs0[p], rs1[p]);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // slab 0; the previous item's last reads of this buffer ended before the caller's barrier
+  store_block(slab[0], lr, lc, ring0[0], rs0[0]);
+  store_block(slab[0], lr, lc + 8, ring1[0], rs1[0]);
 
   for (int s0 = 0; s0 < nsteps_pad; s0 += kPrefetch) {
 #pragma unroll
     for (int p = 0; p < kPrefetch; ++p) {
       const int s = s0 + p;
-      uint8_t* const sl = slab[p & 1];  // kPrefetch is even, so this is slab[s & 1]
-      // keep later steps' use of the ring (and so their waits) below this point
+      const uint8_t* const sl = slab[p & 1];  // kPrefetch is even, so this is slab[s & 1]
+      uint8_t* const sn_buf = slab[(p + 1) & 1];
+      const int q = (p + 1) % kPrefetch;     // ring slot of step s + 1
       __builtin_amdgcn_sched_barrier(0);
-      // this buffer was last read two steps ago; the barrier of the previous step ordered
-      // those reads before these writes
-      store_block(sl, lr, lc, ring0[p], rs0[p]);
-      store_block(sl, lr, lc + 8, ring1[p], rs1[p]);
       __syncthreads();
+      // B operands of this wave's 8 column groups: rows 8g..8g+7 of column cg*16 + li
+      bf16x8 b[8];
+#pragma unroll
+      for (int cg = 0; cg < 8; ++cg) {
+        const int qd = wave * 32 + cg * 4 + (li & 3);
+        const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(&sl[slab_off(8 * g + (li >> 2), qd)]));
+        const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(&sl[slab_off(8 * g + 4 + (li >> 2), qd)]));
+        const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+        b[cg] = __builtin_bit_cast(bf16x8, bs);
+      }
       const int sn = min(s + 1, nsteps - 1);
       i32x4 ahn[T], aln[T];
 #pragma unroll
@@ -247,38 +276,25 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
       load_raw(s + kPrefetch, ring0[p], ring1[p], rs0[p], rs1[p]);
       __builtin_amdgcn_sched_barrier(0);
 
-      // padding steps (s >= nsteps) see clamped weights: zero their activations instead
-      const bool real = s < nsteps;
-      // B operands of this wave's 8 column groups (rows 8g..8g+7 of column cg*16 + li), read
-      // two groups at a time just before their MFMAs: the hi terms of both groups (and of every
-      // tile), then the lo terms, so no MFMA waits on the one issued just before it
+      // two halves: decode half h of step s + 1, then the MFMAs of column groups 4h..4h+3,
+      // the hi terms of each pair of groups (and of every tile) before their lo terms
 #pragma unroll
-      for (int cp = 0; cp < 8; cp += 2) {
-        bf16x8 b[2];
+      for (int h = 0; h < 2; ++h) {
+        if (h == 0) store_block(sn_buf, lr, lc, ring0[q], rs0[q]);
+        else store_block(sn_buf, lr, lc + 8, ring1[q], rs1[q]);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int q = wave * 32 + (cp + h) * 4 + (li & 3);
-          const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_i16x4*)(&sl[slab_off(8 * g + (li >> 2), q)]));
-          const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_i16x4*)(&sl[slab_off(8 * g + 4 + (li >> 2), q)]));
-          const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
-          b[h] = __builtin_bit_cast(bf16x8, bs);
+        for (int cp = 4 * h; cp < 4 * h + 4; cp += 2) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt)
+              if (tt < w.ntl) acc[tt][cp + e] = mfma_bf16(__builtin_bit_cast(bf16x8, ahv[tt]), b[cp + e], acc[tt][cp + e]);
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt)
+              if (tt < w.ntl) acc[tt][cp + e] = mfma_bf16(__builtin_bit_cast(bf16x8, alv[tt]), b[cp + e], acc[tt][cp + e]);
         }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int tt = 0; tt < T; ++tt)
-            if (tt < w.ntl)
-              acc[tt][cp + h] = mfma_bf16(__builtin_bit_cast(bf16x8, real ? ahv[tt] : i32x4{0, 0, 0, 0}), b[h],
-                                          acc[tt][cp + h]);
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int tt = 0; tt < T; ++tt)
-            if (tt < w.ntl)
-              acc[tt][cp + h] = mfma_bf16(__builtin_bit_cast(bf16x8, real ? alv[tt] : i32x4{0, 0, 0, 0}), b[h],
-                                          acc[tt][cp + h]);
       }
 #pragma unroll
       for (int tt = 0; tt < T; ++tt) {

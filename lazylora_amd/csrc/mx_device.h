@@ -160,6 +160,18 @@ MX_DEV i32x4 ldg16(const void* p) { return *reinterpret_cast<const i32x4*>(p); }
 // instruction reads again is fetched again.
 MX_DEV i32x4 ldg16_nt(const void* p) { return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p)); }
 
+// Buffer resources: a base address and a byte count held in SGPRs. A buffer load whose VGPR
+// offset plus immediate offset is at or past the count returns zeros instead of touching
+// memory (the SGPR offset is not range-checked, so variable offsets go in the VGPR one).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+MX_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes, streaming (non-temporal, as ldg16_nt)
+MX_DEV i32x4 buf16_nt(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2); }
+MX_DEV uint8_t buf8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0); }
+
 // Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes from src land at
 // lds + 16 l. lds must be the same for the whole wave. Completion is counted by vmcnt.
 MX_DEV void dma16(const void* src, void* lds)
