@@ -203,17 +203,34 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
     s1 = buf8(S, os + 8);
   };
 
-  // A operand rows of each tile (rows past a tile's end repeat its last row; never stored).
-  // Padding steps meet zero weights, so their A (the last real step's, reloaded) adds zero.
-  const uint16_t* pah[T];
-  const uint16_t* pal[T];
+  // A operands. A step's A tile (T tiles x hi/lo x 16 rows x 32 bf16 = 2T KiB) is loaded
+  // once per work-group, each thread its 8T bytes two steps ahead, and shared through a
+  // double-buffered LDS copy written one step ahead; every wave reads its MFMA operands from
+  // there (four waves loading the same operands from L2 would move as many bytes as the
+  // weights). Copy layout: [tile][term][row][four 16-byte K chunks], chunk c of row r at
+  // position c ^ ((r >> 1) & 3), so the 8 rows of a ds_read_b128 phase cover all banks.
+  // Rows past a tile's end repeat its last row (never stored). Padding steps meet zero
+  // weights, so their A (the last real step's, reloaded) adds zero.
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2][T * 2048];
+  constexpr int kABytes = 8 * T;  // per thread and step
+  typedef int av_t __attribute__((ext_vector_type(2 * T)));
+  const uint16_t* pa;
+  int a_dst;
+  {
+    const int b0 = tid * kABytes;
+    const int tt = b0 >> 11, term = (b0 >> 10) & 1, row = (b0 >> 6) & 15, kb = b0 & 63;
+    int r0 = w.row0[0], nr = w.nrows[0];  // tile tt's (selected, not indexed: no stack copy)
 #pragma unroll
-  for (int tt = 0; tt < T; ++tt) {
-    const int ri = w.row0[tt] + min(li, w.nrows[tt] - 1);
+    for (int i = 1; i < T; ++i)
+      if (tt == i) r0 = w.row0[i], nr = w.nrows[i];
+    const int ri = r0 + min(row, nr - 1);
     const int arow = a.a_row_map ? a.a_row_map[ri] : ri;
-    pah[tt] = a.a_hi + (long long)arow * a.lda + 8 * g;
-    pal[tt] = a.a_lo + (long long)arow * a.lda + 8 * g;
+    pa = (term ? a.a_lo : a.a_hi) + (long long)arow * a.lda + (kb >> 1);
+    a_dst = (b0 & ~63) + ((((kb >> 4) ^ (row >> 1)) & 3) << 4) + (kb & 15);
   }
+  auto load_a = [&](int step) { return *reinterpret_cast<const av_t*>(pa + min(step, nsteps - 1) * kSlabRows); };
+  auto store_a = [&](uint8_t* buf, const av_t& v) { *reinterpret_cast<av_t*>(buf + a_dst) = v; };
+  const int a_src = li * 64 + (((g ^ (li >> 1)) & 3) << 4);  // this lane's operand chunk
 
   f32x4 acc[T][8];
 #pragma unroll
@@ -222,25 +239,22 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
     for (int cg = 0; cg < 8; ++cg) acc[tt][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Pipeline: the raw blocks of the next kPrefetch steps are in flight in a register ring.
-  // Within a step the next step's A loads are issued before the ring refill, so waiting for
-  // A (vmcnt is an in-order counter) never waits for the far-ahead weight loads.
+  // Within a step the A load is issued before the ring refill.
   i32x4 ring0[kPrefetch], ring1[kPrefetch];
   uint8_t rs0[kPrefetch], rs1[kPrefetch];
   // Issue order is pinned (A first, then the ring slot by slot) so the loop head can wait
   // for slot 0 alone, whether it is entered from here or from the back edge.
-  i32x4 ahv[T], alv[T];
-#pragma unroll
-  for (int tt = 0; tt < T; ++tt) {
-    ahv[tt] = ldg16(pah[tt]);
-    alv[tt] = ldg16(pal[tt]);
-  }
+  av_t acur = load_a(0);
+  store_a(abuf[0], acur);
+  acur = load_a(1);
 #pragma unroll
   for (int p = 0; p < kPrefetch; ++p) {
     __builtin_amdgcn_sched_barrier(0);
     load_raw(p, ring0[p], ring1[p], rs0[p], rs1[p]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // slab 0; the previous item's last reads of this buffer ended before the caller's barrier
+  // slab 0 (and A copy 0 above); the previous item's last reads of these buffers ended before
+  // the caller's barrier
   store_block(slab[0], lr, lc, ring0[0], rs0[0]);
   store_block(slab[0], lr, lc + 8, ring1[0], rs1[0]);
 
@@ -250,6 +264,8 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
       const int s = s0 + p;
       const uint8_t* const sl = slab[p & 1];  // kPrefetch is even, so this is slab[s & 1]
       uint8_t* const sn_buf = slab[(p + 1) & 1];
+      const uint8_t* const ab = abuf[p & 1];
+      uint8_t* const an_buf = abuf[(p + 1) & 1];
       const int q = (p + 1) % kPrefetch;     // ring slot of step s + 1
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
@@ -265,13 +281,13 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
         const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
         b[cg] = __builtin_bit_cast(bf16x8, bs);
       }
-      const int sn = min(s + 1, nsteps - 1);
-      i32x4 ahn[T], aln[T];
+      i32x4 ahv[T], alv[T];
 #pragma unroll
       for (int tt = 0; tt < T; ++tt) {
-        ahn[tt] = ldg16(pah[tt] + sn * kSlabRows);
-        aln[tt] = ldg16(pal[tt] + sn * kSlabRows);
+        ahv[tt] = *reinterpret_cast<const i32x4*>(ab + tt * 2048 + a_src);
+        alv[tt] = *reinterpret_cast<const i32x4*>(ab + tt * 2048 + 1024 + a_src);
       }
+      const av_t anext = load_a(s + 2);
       __builtin_amdgcn_sched_barrier(0);
       load_raw(s + kPrefetch, ring0[p], ring1[p], rs0[p], rs1[p]);
       __builtin_amdgcn_sched_barrier(0);
@@ -280,8 +296,12 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
       // the hi terms of each pair of groups (and of every tile) before their lo terms
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        if (h == 0) store_block(sn_buf, lr, lc, ring0[q], rs0[q]);
-        else store_block(sn_buf, lr, lc + 8, ring1[q], rs1[q]);
+        if (h == 0) {
+          store_block(sn_buf, lr, lc, ring0[q], rs0[q]);
+          store_a(an_buf, acur);  // step s + 1's A
+        } else {
+          store_block(sn_buf, lr, lc + 8, ring1[q], rs1[q]);
+        }
 #pragma unroll
         for (int cp = 4 * h; cp < 4 * h + 4; cp += 2) {
 #pragma unroll
@@ -296,11 +316,7 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
               if (tt < w.ntl) acc[tt][cp + e] = mfma_bf16(__builtin_bit_cast(bf16x8, alv[tt]), b[cp + e], acc[tt][cp + e]);
         }
       }
-#pragma unroll
-      for (int tt = 0; tt < T; ++tt) {
-        ahv[tt] = ahn[tt];
-        alv[tt] = aln[tt];
-      }
+      acur = anext;
     }
   }
 
