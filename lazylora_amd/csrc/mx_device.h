@@ -168,6 +168,11 @@ MX_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes)
 {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+// voff: per-lane (range-checked) offset, soff: uniform offset added to it (not range-checked)
+MX_DEV i32x4 buf16(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+}
 // 16 bytes, streaming (non-temporal, as ldg16_nt)
 MX_DEV i32x4 buf16_nt(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2); }
 MX_DEV uint8_t buf8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0); }
@@ -177,6 +182,23 @@ MX_DEV uint8_t buf8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer
 MX_DEV void dma16(const void* src, void* lds)
 {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+// The same copy issued from inline assembly. While a copy the compiler knows of is in
+// flight, it makes every barrier wait for all outstanding loads (vmcnt(0)), which drains any
+// deeper load pipeline at each barrier; this one it does not see. The caller must wait for it
+// itself (wait_vm<N>) before the copied bytes are read, and nothing else may rely on M0.
+MX_DEV void dma16_async(const void* src, void* lds)
+{
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
+}
+// Wait until at most N vector-memory operations of this wave are outstanding (they retire in
+// issue order, so everything but the last N issued is complete).
+template <int N>
+MX_DEV void wait_vm()
+{
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 MX_DEV void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 MX_DEV void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }

@@ -336,9 +336,9 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int unit = 4 * wave + u;
-        dma16(src + unit * 1024 + lane * 16, &lds.a[buf][unit * 1024]);
+        dma16_async(src + unit * 1024 + lane * 16, &lds.a[buf][unit * 1024]);
       }
-      if (wave == 0) dma16(src + kAtCodeBytes + (lane & 31) * 16, &lds.a[buf][kAtCodeBytes]);
+      if (wave == 0) dma16_async(src + kAtCodeBytes + (lane & 31) * 16, &lds.a[buf][kAtCodeBytes]);
     };
     // scale window win -> sw: instruction i covers rows 8i..8i+7 of this wave's 64, lane l
     // copies 16 B (one super-chunk) of row 8i + l/8 into slot l%8 of that row; the slot holds
@@ -354,11 +354,37 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       for (int i = 0; i < 8; ++i) {
         const int grp = i >> 1;
         const uint32_t off = (uint32_t)(min(grp_row(grp) + 8 * (i & 1) + (ln >> 3), a.R - 1) * nb + cc * 16);
-        dma16(grp_ws(grp) + off, sw + i * 1024);
+        dma16_async(grp_ws(grp) + off, sw + i * 1024);
       }
     };
-    auto step = [&](int c, i32x4 (&cur)[4][4], i32x4 (&nxt)[4][4]) {
-      wait_vm0();
+    // weights of chunk c through one buffer resource per column group: a fixed per-lane offset
+    // + 256 c (uniform) + 16 q (immediate). A chunk past the last is requested from an empty
+    // resource: zeros, no memory traffic, and the same count of loads in vmcnt.
+    rsrc_t wr[4], wr_none[4];
+    uint32_t woff[4];
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      const uint8_t* base = grp_wp(grp);
+      wr[grp] = make_rsrc(base, (uint32_t)a.R * (uint32_t)(a.K / 2));
+      wr_none[grp] = make_rsrc(base, 0);
+      woff[grp] = (uint32_t)(wrow[grp] - base) + boff[grp];
+    }
+    auto load_b_buf = [&](int c, i32x4 (&b)[4][4]) {
+      const bool live = c < nsc;  // uniform
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[grp][q] = buf16(live ? wr[grp] : wr_none[grp], woff[grp] + 16 * q, (uint32_t)c * 256);
+    };
+
+    // Two chunks of weights in flight: a buffer is refilled with chunk c + 2 as soon as chunk
+    // c's MFMAs have read it, and chunk c + 1's loads are in flight meanwhile. The activation
+    // copy and scale window of chunk c are requested at the top of chunk c - 1, before the 16
+    // weight loads of chunk c + 1 (issued at the end of chunk c - 1), so at the top of chunk c
+    // everything but those 16 has landed. The copies are issued from
+    // inline assembly: a copy the compiler knows of makes it drain every load at each barrier.
+    auto step = [&](int c, i32x4 (&cur)[4][4]) {
+      wait_vm<16>();
       __syncthreads();
       // everything this chunk needs from LDS, before any new copy into LDS is requested
       uint32_t sb[4];
@@ -377,7 +403,6 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       wait_lgkm0();
       __builtin_amdgcn_sched_barrier(0);
       if (c + 1 < nsc) {
-        load_b(c + 1, nxt);
         issue_a(c + 1, (c + 1) & 1);
         if ((c + 1) % kScaleWin == 0) issue_scales((c + 1) / kScaleWin);
       }
@@ -387,21 +412,25 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       mfma_step<1>(acc, ah[1], al[1], cur, sb, (int)s2.x, (int)s2.y);
       mfma_step<2>(acc, ah[2], al[2], cur, sb, (int)s2.x, (int)s2.y);
       mfma_step<3>(acc, ah[3], al[3], cur, sb, (int)s2.x, (int)s2.y);
+      __builtin_amdgcn_sched_barrier(0);
+      load_b_buf(c + 2, cur);
     };
 
-    i32x4 b0[4][4], b1[4][4];
-    load_b(0, b0);
-    issue_a(0, 0);
-    issue_scales(0);
     if (MODE == kFwdDown)
 #pragma unroll
       for (int v = 0; v < 4; ++v) tw[v] = a.row_w[w.row0 + min(4 * g + v, w.nrows - 1)];
+    i32x4 b0[4][4], b1[4][4];
+    load_b_buf(0, b0);
+    issue_scales(0);
+    issue_a(0, 0);
+    load_b_buf(1, b1);
     for (int c = 0;;) {
-      step(c, b0, b1);
+      step(c, b0);
       if (++c >= nsc) break;
-      step(c, b1, b0);
+      step(c, b1);
       if (++c >= nsc) break;
     }
+    wait_vm0();  // (no copy is in flight past the last chunk; kept explicit for the epilogue)
   } else {
     if (MODE == kFwdDown)
 #pragma unroll
