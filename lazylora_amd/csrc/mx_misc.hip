@@ -35,21 +35,29 @@ __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long lo
   const bool valid = i < nrows;
   const long long src = valid ? (row_map ? row_map[row0 + i] : row0 + i) : 0;
   const long long cbase = (long long)c * kAtChunkBytes;  // at_*_off are tile-relative
+  // all 16 blocks' loads are issued before the first is quantised
+  float v0[kChunkBlocks], v1[kChunkBlocks];
+#pragma unroll
   for (int b = 0; b < kChunkBlocks; ++b) {
     const int k = c * kChunk + b * kGroup + 2 * l16;
-    float v0 = 0.f, v1 = 0.f;
+    v0[b] = 0.f;
+    v1[b] = 0.f;
     if (valid && k < K) {
       if (BF16) {
         const uint32_t u = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + src * ldx + k);
-        v0 = bf16_lo(u);
-        v1 = bf16_hi(u);
+        v0[b] = bf16_lo(u);
+        v1[b] = bf16_hi(u);
       } else {
         const float2 f = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(x) + src * ldx + k);
-        v0 = f.x;
-        v1 = f.y;
+        v0[b] = f.x;
+        v1[b] = f.y;
       }
     }
-    const Quant2 q = quant2_block16(v0, v1);
+  }
+#pragma unroll
+  for (int b = 0; b < kChunkBlocks; ++b) {
+    const int k = c * kChunk + b * kGroup + 2 * l16;
+    const Quant2 q = quant2_block16(v0[b], v1[b]);
     *reinterpret_cast<uint16_t*>(chunk + (at_code_off(i, k, 0) - cbase)) = (uint16_t)q.hi;
     *reinterpret_cast<uint16_t*>(chunk + (at_code_off(i, k, 1) - cbase)) = (uint16_t)q.lo;
     if (l16 == 0) {
