@@ -429,6 +429,8 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
 {
   const long long total = (long long)max_tiles * a.n_ct;
   if (total <= 0) return hipSuccess;
+  // each weight segment is addressed through one buffer resource with a 32-bit byte count
+  if ((long long)a.R * (a.C / 2) >= (1LL << 32)) return hipErrorInvalidValue;
   const bool split = a.tiles && a.small_tiles && a.groups;
   BwdArgs b = a;
   if (!split) {
