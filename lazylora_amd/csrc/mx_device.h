@@ -139,6 +139,12 @@ MX_DEV bool any_damaged_scale(uint32_t w)
   return ((w & 0xFFu) >= 253u) | (((w >> 8) & 0xFFu) >= 253u) | (((w >> 16) & 0xFFu) >= 253u) |
          ((w >> 24) >= 253u);
 }
+// Bit 7 of each byte of the result is set when that byte of w is >= 253 (0xFD..0xFF): its top
+// bit is set and its low 7 bits are >= 125, so adding 3 to them carries into bit 7.
+MX_DEV uint32_t damaged_scale_bits(uint32_t w)
+{
+  return w & ((w & 0x7F7F7F7Fu) + 0x03030303u) & 0x80808080u;
+}
 
 // Scaled MFMA, A = e4m3 (format 0), B = fp4 (format 4). QA / QB pick the scale bytes.
 template <int QA, int QB>

@@ -117,6 +117,16 @@ __device__ __forceinline__ void sanitize(i32x4 (&b)[4][4], uint32_t (&s)[4])
     }
 }
 
+// The fast path's version: such scale bytes do not occur in checkpoints written by a
+// quantiser, so the masking above runs only when some lane of the wave has one (a uniform
+// branch); the test is three operations per scale dword.
+__device__ __forceinline__ void sanitize_if_damaged(i32x4 (&b)[4][4], uint32_t (&s)[4])
+{
+  const uint32_t d = damaged_scale_bits(s[0]) | damaged_scale_bits(s[1]) | damaged_scale_bits(s[2]) |
+                     damaged_scale_bits(s[3]);
+  if (__builtin_amdgcn_ballot_w64(d != 0u) != 0) sanitize(b, s);
+}
+
 __device__ __forceinline__ i32x8 cat8(const i32x4& x, const i32x4& y)
 {
   return i32x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
@@ -407,7 +417,7 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
         if ((c + 1) % kScaleWin == 0) issue_scales((c + 1) / kScaleWin);
       }
       __builtin_amdgcn_sched_barrier(0);
-      sanitize(cur, sb);
+      sanitize_if_damaged(cur, sb);
       mfma_step<0>(acc, ah[0], al[0], cur, sb, (int)s2.x, (int)s2.y);
       mfma_step<1>(acc, ah[1], al[1], cur, sb, (int)s2.x, (int)s2.y);
       mfma_step<2>(acc, ah[2], al[2], cur, sb, (int)s2.x, (int)s2.y);
