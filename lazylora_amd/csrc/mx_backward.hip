@@ -291,6 +291,12 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
       __builtin_amdgcn_sched_barrier(0);
       load_raw(s + kPrefetch, ring0[p], ring1[p], rs0[p], rs1[p]);
       __builtin_amdgcn_sched_barrier(0);
+      // The decode / MFMA half of the step runs at a raised wave priority: of the two waves on a
+      // SIMD, the one in this phase is issued first, so it finishes its step while the other
+      // waits at its barrier or on its transposed reads, and the two phases overlap instead of
+      // alternating in lockstep (2-3% faster than the default level; raising it over the reads
+      // instead, or over only the MFMAs or only the decode, is not).
+      __builtin_amdgcn_s_setprio(1);
 
       // two halves: decode half h of step s + 1, then the MFMAs of column groups 4h..4h+3,
       // the hi terms of each pair of groups (and of every tile) before their lo terms
@@ -316,6 +322,7 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
               if (tt < w.ntl) acc[tt][cp + e] = mfma_bf16(__builtin_bit_cast(bf16x8, alv[tt]), b[cp + e], acc[tt][cp + e]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       acur = anext;
     }
   }
