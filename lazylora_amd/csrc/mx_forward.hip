@@ -694,7 +694,9 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   const long long total = (long long)max_tiles * n_cg;
   if (total <= 0) return hipSuccess;
   const long long blocks = std::min<long long>((total + 7) / 8 * 8, resident_groups());
-  const bool fast = (a.K % kChunk) == 0;
+  // the fast path addresses a weight matrix through one buffer resource (32-bit byte counts and
+  // offsets); larger matrices take the general path
+  const bool fast = (a.K % kChunk) == 0 && (long long)a.R * (a.K / 2) < (1LL << 32);
   // the bucket split needs the tile list and the fast path; otherwise every tile takes fwd_kernel
   const bool split = fast && a.tiles && a.small_tiles && a.groups;
   FwdArgs b = a;
