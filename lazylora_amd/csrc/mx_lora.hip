@@ -167,10 +167,19 @@ constexpr int kExpandRows = 16;
 
 __global__ __launch_bounds__(256) void lora_expand_kernel(ExpandArgs a)
 {
+  // The block's coefficient rows (16 rows x up to two segments x r) are the same for every
+  // thread: staged once in LDS and read back as broadcasts, rather than re-read from memory by
+  // every thread for every row.
+  __shared__ __attribute__((aligned(16))) float sc[kExpandRows][2][kLoraMaxRank];
   const int c = blockIdx.x * 256 + threadIdx.x;
   const int t0 = blockIdx.y * kExpandRows;
-  if (c >= a.Cout) return;
   const int nr = min(kExpandRows, a.rows - t0);
+  for (int i = threadIdx.x; i < kExpandRows * 2 * kLoraMaxRank; i += 256) {
+    const int u = i / (2 * kLoraMaxRank), sg = (i / kLoraMaxRank) & 1, j = i % kLoraMaxRank;
+    sc[u][sg][j] = (u < nr && sg < a.nseg && j < a.r) ? a.coef[(long long)(t0 + u) * a.ldc + a.coff[sg] + j] : 0.f;
+  }
+  __syncthreads();
+  if (c >= a.Cout) return;
   float acc[kExpandRows];
 #pragma unroll
   for (int u = 0; u < kExpandRows; ++u)
@@ -184,14 +193,15 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(ExpandArgs a)
     for (int j = 0; j < kLoraMaxRank; ++j) mc[j] = j < a.r ? factor_at(f, j, cc) : 0.f;
 #pragma unroll
     for (int u = 0; u < kExpandRows; ++u) {
-      if (u < nr) {
-        const float* cr = a.coef + (long long)(t0 + u) * a.ldc + a.coff[sg];
-        float s = 0.f;
+      float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < kLoraMaxRank; ++j)
-          if (j < a.r) s += cr[j] * mc[j];
-        acc[u] += f.scale * s;
+      for (int j4 = 0; j4 < kLoraMaxRank / 4; ++j4) {
+        if (j4 * 4 < a.r) {  // uniform
+          const float4 cv = *reinterpret_cast<const float4*>(&sc[u][sg][j4 * 4]);
+          s += cv.x * mc[j4 * 4] + cv.y * mc[j4 * 4 + 1] + cv.z * mc[j4 * 4 + 2] + cv.w * mc[j4 * 4 + 3];
+        }
       }
+      acc[u] += f.scale * s;
     }
   }
 #pragma unroll
@@ -308,8 +318,20 @@ __global__ __launch_bounds__(256) void lora_outer_reduce_kernel(const float* par
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (long long)m * C) return;
   const int j = (int)(idx / C), c = (int)(idx % C);
-  float s = 0.f;
-  for (int rs = 0; rs < RS; ++rs) s += partial[((long long)rs * m + j) * C + c];
+  // four independent running sums (slices rs = 4i + q) keep four loads in flight per thread;
+  // they are added in a fixed order, so the result does not depend on timing
+  const float* pp = partial + (long long)j * C + c;
+  const long long step = (long long)m * C;
+  float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f;
+  int rs = 0;
+  for (; rs + 4 <= RS; rs += 4) {
+    q0 += pp[(rs + 0) * step];
+    q1 += pp[(rs + 1) * step];
+    q2 += pp[(rs + 2) * step];
+    q3 += pp[(rs + 3) * step];
+  }
+  for (; rs < RS; ++rs) q0 += pp[rs * step];
+  const float s = (q0 + q1) + (q2 + q3);
   const int sg = (d.split_j > 0 && j >= d.split_j) ? 1 : 0;
   const int jj = sg ? j - d.split_j : j;
   const long long o = d.kmajor[sg] ? (long long)c * d.ld[sg] + jj : (long long)jj * d.ld[sg] + c;
