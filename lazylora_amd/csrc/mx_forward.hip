@@ -150,16 +150,32 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
     uint8_t* sq = lds.a[0];
     float* ss = reinterpret_cast<float*>(lds.a[1]);  // [row][gate 128 | up 128] fp32
     const int F = a.R;
+    // LoRA gate/up delta of each row's token: the four rows' token indices, then their sixteen
+    // delta values, each requested together (two round trips to memory rather than eight)
+    float dl[4][4] = {};
+    if (a.lora_delta && w.active) {
+      int tok[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tok[v] = 4 * g + v < w.nrows ? a.row_token[w.row0 + 4 * g + v] : -1;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (tok[v] >= 0) {
+          const float* d = a.lora_delta + (long long)tok[v] * 2 * F + w.ct * 32 + j;
+          dl[v][0] = d[0];
+          dl[v][1] = d[16];
+          dl[v][2] = d[F];
+          dl[v][3] = d[F + 16];
+        }
+    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int i = 4 * g + v;
       float ga = acc[0][v], gb = acc[1][v], ua = acc[2][v], ub = acc[3][v];
-      if (a.lora_delta && w.active && i < w.nrows) {  // LoRA gate/up delta of the row's token
-        const float* dl = a.lora_delta + (long long)a.row_token[w.row0 + i] * 2 * F + w.ct * 32 + j;
-        ga += dl[0];
-        gb += dl[16];
-        ua += dl[F];
-        ub += dl[F + 16];
+      if (a.lora_delta) {
+        ga += dl[v][0];
+        gb += dl[v][1];
+        ua += dl[v][2];
+        ub += dl[v][3];
       }
       Quant2 q = quant2_block16(glu_fwd(ga, ua, a.act_kind), glu_fwd(gb, ub, a.act_kind));
       if (!w.active) q = Quant2{0, 0, 0, 0};  // features past F: the padding of the layout is zero
