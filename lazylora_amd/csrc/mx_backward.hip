@@ -229,7 +229,20 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
     a_dst = (b0 & ~63) + ((((kb >> 4) ^ (row >> 1)) & 3) << 4) + (kb & 15);
   }
   auto load_a = [&](int step) { return *reinterpret_cast<const av_t*>(pa + min(step, nsteps - 1) * kSlabRows); };
-  auto store_a = [&](uint8_t* buf, const av_t& v) { *reinterpret_cast<av_t*>(buf + a_dst) = v; };
+  // T <= 2: the thread's bytes lie in one 16-byte chunk. T = 4: they are two whole chunks
+  // (kb = 0 or 32), each stored at its own swizzled position.
+  auto store_a = [&](uint8_t* buf, const av_t& v) {
+    if constexpr (kABytes <= 16) {
+      *reinterpret_cast<av_t*>(buf + a_dst) = v;
+    } else {
+      static_assert(kABytes == 32, "T is 1, 2 or 4");
+      const int b0 = tid * kABytes, row = (b0 >> 6) & 15, c0 = (b0 & 63) >> 4;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<i32x4*>(buf + (b0 & ~63) + ((((c0 + h) ^ (row >> 1)) & 3) << 4)) =
+            i32x4{v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+    }
+  };
   const int a_src = li * 64 + (((g ^ (li >> 1)) & 3) << 4);  // this lane's operand chunk
 
   f32x4 acc[T][8];
