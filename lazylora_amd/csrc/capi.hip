@@ -96,7 +96,7 @@ long long pad32(long long v) { return (v + 31) / 32 * 32; }
 // what the forward left behind.
 struct MoeLayout {
   size_t meta, counts, offsets, cursor, tiles, small_tiles, groups, pair_token, pair_w, pair_of;
-  size_t at_x, at_act;
+  size_t at_x, xt_x, at_act;
   size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part;
   size_t l_u, l_delta, l_v, l_vsum, l_q, l_rq, l_dh, l_dsum, l_part;  // LoRA (rank <= kLoraMaxRank)
   size_t end;
@@ -121,6 +121,7 @@ MoeLayout moe_layout(int N, int k, int E, int D, int F)
   L.pair_w = o; o = align_up(o + sizeof(float) * (size_t)P);
   L.pair_of = o; o = align_up(o + sizeof(int) * (size_t)P);
   L.at_x = o; o += at_bytes(L.max_tiles, D);
+  L.xt_x = o; o = align_up(o + (size_t)(mx::xt_rows(N) * mx::xt_row_bytes(D)));
   L.at_act = o; o += at_bytes(L.max_tiles, F);
   L.saved = o; o = align_up(o + sizeof(float) * (size_t)(P * 2 * F));
   L.ypair = o; o = align_up(o + sizeof(float) * (size_t)(P * D));
@@ -221,9 +222,13 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
                           at<float>(ws, L.pair_w), at<int>(ws, L.pair_of), s),
          "route");
   MX_PHASE("route", s);
+  // h once per token in the XT layout (with a zero row N for the unused slots of a tile), which
+  // the one-tile work-groups gather; the tiles of large buckets also in the AT layout, which the
+  // grouped work-groups re-read for every column tile
+  MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, at<uint8_t>(ws, L.xt_x), s), "quantise h");
   MX_TRY(mx::launch_quant_tiles(h, h_dtype == MXFP4_BF16, D, N, D, at<int4>(ws, L.tiles), at<int>(ws, L.meta),
-                                L.max_tiles, at<int>(ws, L.pair_token), at<uint8_t>(ws, L.at_x), s),
-         "quantise h");
+                                L.max_tiles, at<int>(ws, L.pair_token), 1, at<uint8_t>(ws, L.at_x), s),
+         "quantise h tiles");
   MX_PHASE("quant_h", s);
   if (F % mx::kChunk) {  // padding blocks of the act buffer are read by the down product
     MX_TRY(mx::launch_zero(at<void>(ws, L.at_act), at_bytes(L.max_tiles, F), s), "zero act");
@@ -234,6 +239,10 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   a.ws_estride = (long long)F * D / 32;
   a.R = F; a.K = D;
   a.a_tiles = at<uint8_t>(ws, L.at_x);
+  a.a_rows = at<uint8_t>(ws, L.xt_x);
+  a.a_row_bytes = mx::xt_row_bytes(D);
+  a.a_zero_row = N;
+  a.row_token = at<int>(ws, L.pair_token);
   a.tiles = at<int4>(ws, L.tiles); a.n_tiles = at<int>(ws, L.meta);
   a.n_ct = F / 32;
   a.q_tiles = at<uint8_t>(ws, L.at_act);
@@ -252,7 +261,6 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
     MX_TRY(mx::launch_lora_expand(at<float>(ws, L.l_u), 2 * r, N, r, 2, fb, coff, col0, ncol,
                                   at<float>(ws, L.l_delta), 2LL * F, 2 * F, 0, s),
            "LoRA: gate/up deltas");
-    a.row_token = at<int>(ws, L.pair_token);
     a.lora_delta = at<float>(ws, L.l_delta);
     MX_PHASE("lora_in", s);
   }
@@ -311,7 +319,7 @@ int mxfp4_gemm(float* y, const float* x, const uint8_t* packed, const uint8_t* s
   if (((uintptr_t)x & 7) != 0) return fail(MXFP4_EINVAL, "gemm: x must be 8-byte aligned%s");
   const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
   if (!workspace || workspace_bytes < at_bytes(tiles, K)) return fail(MXFP4_EWORKSPACE, "gemm: workspace too small%s");
-  MX_TRY(mx::launch_quant_tiles(x, 0, K, M, K, nullptr, nullptr, tiles, nullptr, at<uint8_t>(workspace, 0), stream),
+  MX_TRY(mx::launch_quant_tiles(x, 0, K, M, K, nullptr, nullptr, tiles, nullptr, 0, at<uint8_t>(workspace, 0), stream),
          "gemm: quantise x");
   mx::FwdArgs a = {};
   a.wp0 = packed; a.ws0 = scales;

@@ -75,6 +75,34 @@ MX_DEV long long at_scale_off(int i, int k, int plane)
   return (long long)c * kAtChunkBytes + kAtCodeBytes + (16 * g + i) * 8 + plane * 4 + q;
 }
 
+// ------------------------------------------------------------------ XT activation layout
+// The same codes and scales stored once per row of x instead of once per work tile ("XT",
+// token-major): the routed gate/up product gathers each tile lane's pieces from the row of its
+// token, so a token chosen by k experts is quantised and stored once, not k times. Per (row,
+// super-chunk): 1024 B of codes [q][plane][piece][g][16 B] (the 16-byte piece that tile lane
+// 16g + i takes from row i), then 32 B of scales [plane][g][4 B: byte q].
+constexpr int kXtCodeBytes = 1024;
+constexpr int kXtChunkBytes = kXtCodeBytes + 32;
+
+__host__ __device__ inline long long xt_row_bytes(int K) { return (long long)at_nchunks(K) * kXtChunkBytes; }
+
+// Byte offset, inside a row, of elements k..k+1 (k even) for one plane, and of the scale byte
+// of the 32-element block holding k (the per-lane offsets of at_code_off / at_scale_off).
+MX_DEV int xt_code_off(int k, int plane)
+{
+  const int c = k >> 9, b = (k >> 5) & 15, e = k & 31;
+  const int q = b & 3, gl = b >> 2;
+  const int piece = gl >> 1;
+  const int g = 2 * (gl & 1) + (e >> 4);
+  return c * kXtChunkBytes + (((q * 2 + plane) * 2 + piece) * 4 + g) * 16 + (e & 15);
+}
+MX_DEV int xt_scale_off(int k, int plane)
+{
+  const int c = k >> 9, b = (k >> 5) & 15;
+  const int q = b & 3, g = b >> 2;
+  return c * kXtChunkBytes + kXtCodeBytes + (plane * 4 + g) * 4 + q;
+}
+
 // ------------------------------------------------------------------ small helpers
 MX_DEV float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
 MX_DEV uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
@@ -198,6 +226,13 @@ MX_DEV void dma16_async(const void* src, void* lds)
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
+}
+// The 4-byte form (global_load_lds_dword): lane l's 4 bytes land at lds + 4 l.
+MX_DEV void dma4_async(const void* src, void* lds)
+{
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory");
 }
 // Wait until at most N vector-memory operations of this wave are outstanding (they retire in
 // issue order, so everything but the last N issued is complete).

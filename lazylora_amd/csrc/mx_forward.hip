@@ -132,6 +132,45 @@ __device__ __forceinline__ i32x8 cat8(const i32x4& x, const i32x4& y)
   return i32x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
 }
 
+// Where lane (i = lane % 16, g = lane / 16) of a one-tile work-group finds its A: piece u
+// (= (q * 2 + plane) * 2 + piece) of super-chunk c at base + c * kC + u * kU, its scale dwords
+// (plane 0, plane 1) at sbase + c * kC and + kS. AT: the tile's block. XT (the routed gate/up
+// product): the row of the slot's token (the all-zero row for unused slots), whose pieces sit
+// 64 bytes apart. Grouped work-groups read AT tiles: they re-read A for every column tile, and
+// 1 KiB runs from one tile serve that better than 64-byte runs from 16 rows.
+template <bool XT>
+struct ASrc {
+  static constexpr int kC = XT ? kXtChunkBytes : kAtChunkBytes;
+  static constexpr int kU = XT ? 64 : 1024;
+  static constexpr int kS = XT ? 16 : 4;
+  const uint8_t* base;   // the lane's piece 0 of super-chunk 0
+  const uint8_t* sbase;  // the lane's plane-0 scale dword of super-chunk 0
+
+  __device__ __forceinline__ ASrc(const FwdArgs& a, const WorkItem& w, int lane)
+  {
+    if constexpr (XT) {
+      const int i = lane & 15, g = lane >> 4;
+      const int tok = i < w.nrows ? a.row_token[w.row0 + i] : a.a_zero_row;
+      const uint8_t* row = a.a_rows + (long long)tok * a.a_row_bytes;
+      base = row + g * 16;
+      sbase = row + kXtCodeBytes + g * 4;
+    } else {
+      const uint8_t* t = a.a_tiles + (long long)w.tile * at_tile_bytes(a.K);
+      base = t + lane * 16;
+      sbase = t + kAtCodeBytes + lane * 8;
+    }
+  }
+  __device__ __forceinline__ const uint8_t* unit(int c, int u) const { return base + (long long)c * kC + u * kU; }
+  __device__ __forceinline__ uint2 scales(int c) const
+  {
+    const uint8_t* p = sbase + (long long)c * kC;
+    if constexpr (XT)
+      return uint2{*reinterpret_cast<const uint32_t*>(p), *reinterpret_cast<const uint32_t*>(p + kS)};
+    else
+      return *reinterpret_cast<const uint2*>(p);
+  }
+};
+
 // Epilogue of the fast path. The four waves stage the work-group's outputs in the (now idle)
 // activation buffers of LDS, then write them with 16-byte stores that cover whole runs of
 // memory: scattered 1-byte and 4-byte stores of the same data cost the weight stream about a
@@ -317,7 +356,8 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
   const int j = lane & 15, g = lane >> 4;
   const int nb = a.K / kGroup;
   const int nsc = at_nchunks(a.K);
-  const uint8_t* const at_tile = a.a_tiles + (long long)w.tile * at_tile_bytes(a.K);
+  constexpr bool kXt = MODE == kFwdGateUp;
+  const ASrc<kXt> as(a, w, lane);
 
   // first weight row of column group grp, and that group's packed / scale bases
   auto grp_row = [&](int grp) {
@@ -355,16 +395,25 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
   if constexpr (FAST) {
     uint8_t* const sw = lds.s[wave];
 
-    // A(c) -> lds.a[buf]: wave w copies KiB units 4w..4w+3 of the codes; wave 0 also copies
-    // the 512 B of scales (its upper 32 lanes repeat them into the spare half KiB)
+    // A(c) -> lds.a[buf]: wave w copies KiB units 4w..4w+3 of the codes (lane l's 16 bytes of
+    // unit u at u * 1024 + 16 l); wave 0 also copies the scales: AT, the tile's 512 B as they
+    // lie (lane l's two dwords at 8 l; its upper 32 lanes repeat them into the spare half KiB),
+    // XT, the lanes' plane-0 dwords at 4 l and plane-1 dwords at 256 + 4 l
     auto issue_a = [&](int c, int buf) {
-      const uint8_t* src = at_tile + (long long)c * kAtChunkBytes;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int unit = 4 * wave + u;
-        dma16_async(src + unit * 1024 + lane * 16, &lds.a[buf][unit * 1024]);
+        dma16_async(as.unit(c, unit), &lds.a[buf][unit * 1024]);
       }
-      if (wave == 0) dma16_async(src + kAtCodeBytes + (lane & 31) * 16, &lds.a[buf][kAtCodeBytes]);
+      if (wave == 0) {
+        if constexpr (kXt) {
+          const uint8_t* ss = as.sbase + (long long)c * as.kC;
+          dma4_async(ss, &lds.a[buf][kAtCodeBytes]);
+          dma4_async(ss + as.kS, &lds.a[buf][kAtCodeBytes + 256]);
+        } else {
+          dma16_async(as.unit(c, 0) - lane * 16 + kAtCodeBytes + (lane & 31) * 16, &lds.a[buf][kAtCodeBytes]);
+        }
+      }
     };
     // scale window win -> sw: instruction i covers rows 8i..8i+7 of this wave's 64, lane l
     // copies 16 B (one super-chunk) of row 8i + l/8 into slot l%8 of that row; the slot holds
@@ -425,7 +474,10 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
         ah[q] = cat8(*reinterpret_cast<const i32x4*>(la + q * 4096), *reinterpret_cast<const i32x4*>(la + q * 4096 + 1024));
         al[q] = cat8(*reinterpret_cast<const i32x4*>(la + q * 4096 + 2048), *reinterpret_cast<const i32x4*>(la + q * 4096 + 3072));
       }
-      const uint2 s2 = *reinterpret_cast<const uint2*>(&lds.a[c & 1][kAtCodeBytes + lane * 8]);
+      const uint8_t* ls = &lds.a[c & 1][kAtCodeBytes];
+      const uint2 s2 = kXt ? uint2{*reinterpret_cast<const uint32_t*>(ls + lane * 4),
+                                  *reinterpret_cast<const uint32_t*>(ls + 256 + lane * 4)}
+                          : *reinterpret_cast<const uint2*>(ls + lane * 8);
       wait_lgkm0();
       __builtin_amdgcn_sched_barrier(0);
       if (c + 1 < nsc) {
@@ -469,7 +521,6 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       const int n = min(grp_row(grp) + j, a.R - 1);
       bs[grp] = grp_ws(grp) + (long long)n * nb + g * 4;
     }
-    const uint8_t* at = at_tile + lane * 16;
     for (int c = 0; c < nsc; ++c) {
       i32x4 b[4][4];
       uint32_t sb[4];
@@ -488,14 +539,13 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
           }
         }
       }
-      const uint8_t* p = at + (long long)c * kAtChunkBytes;
       i32x8 ah[4], al[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        ah[q] = cat8(ldg16(p + q * 4096), ldg16(p + q * 4096 + 1024));
-        al[q] = cat8(ldg16(p + q * 4096 + 2048), ldg16(p + q * 4096 + 3072));
+        ah[q] = cat8(ldg16(as.unit(c, 4 * q)), ldg16(as.unit(c, 4 * q + 1)));
+        al[q] = cat8(ldg16(as.unit(c, 4 * q + 2)), ldg16(as.unit(c, 4 * q + 3)));
       }
-      const uint2 s2 = *reinterpret_cast<const uint2*>(at_tile + (long long)c * kAtChunkBytes + kAtCodeBytes + lane * 8);
+      const uint2 s2 = as.scales(c);
       sanitize(b, sb);
       mfma_step<0>(acc, ah[0], al[0], b, sb, (int)s2.x, (int)s2.y);
       mfma_step<1>(acc, ah[1], al[1], b, sb, (int)s2.x, (int)s2.y);

@@ -24,7 +24,13 @@ struct FwdArgs {
   // A operand: two-term e4m3 activations in the AT layout, one block of at_tile_bytes(K)
   // per work tile (tile t of the list below)
   const uint8_t* a_tiles;
-  // work: tiles[t] = {expert, first row, row count <= 16, 0}; null = dense, rows 16t.. of M
+  // kFwdGateUp, one-tile work-groups: A in the XT layout instead; pair row p reads row
+  // row_token[p] of a_rows (rows a_row_bytes apart), a tile's unused slots row a_zero_row. Its
+  // grouped work-groups read a_tiles, of which only the large buckets' tiles need be written.
+  const uint8_t* a_rows;
+  long long a_row_bytes;
+  int a_zero_row;
+  // work: tiles[t] = {expert, first row, row count <= 16, 1 in a large bucket}; null = dense, rows 16t.. of M
   const int4* tiles;
   const int* n_tiles;
   int M;
@@ -36,7 +42,8 @@ struct FwdArgs {
   uint8_t* q_tiles;      // kFwdGateUp: act in the AT layout with K = R (= F), same tiles
   float* save;           // kFwdGateUp: [rows, 2R] gate | up in fp32, or null
   int act_kind;
-  // kFwdGateUp with LoRA: gate|up of row p gain lora_delta[row_token[p], 0:2R) before the GLU
+  // token of each pair row (XT gather); with LoRA, gate|up of row p gain
+  // lora_delta[row_token[p], 0:2R) before the GLU
   const int* row_token;
   const float* lora_delta;  // [tokens, 2R] fp32, or null
   // Bucket split (with a tile list and K a multiple of 512): the tiles of small buckets
@@ -108,14 +115,19 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
 // holds row tiles[t].y + i (through row_map when given: the token of a (token, slot) pair);
 // with tiles == null the tiles are dense: tile t holds rows 16t.. of `rows`. Unused slots get
 // zeros. max_tiles bounds the grid; the live tile count is read from n_tiles on the device.
+// large_only: only the tiles of large buckets (tiles[t].w != 0); the others are left untouched.
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
-                              const int* n_tiles, int max_tiles, const int* row_map, uint8_t* out,
+                              const int* n_tiles, int max_tiles, const int* row_map, int large_only, uint8_t* out,
                               hipStream_t s);
+// Rows 0 .. rows - 1 of x into the XT layout (xt_row_bytes(K) per row), followed by zero rows
+// up to xt_rows(rows): row `rows` is the all-zero row a tile's unused slots gather.
+inline long long xt_rows(int rows) { return ((long long)rows + 16) / 16 * 16; }
+hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, uint8_t* out, hipStream_t s);
 hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int Kpad, uint16_t* hi,
                              uint16_t* lo, hipStream_t s);
 hipError_t launch_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R,
                           hipStream_t s);
-// Routing: per-expert counts, scan, the tile list (tiles[t] = {expert, first pair row, rows}),
+// Routing: per-expert counts, scan, the tile list (tiles[t] = {expert, first pair row, rows, large}),
 // the small-bucket tile indices and the large-bucket groups ({expert, first tile, tiles, 0}),
 // meta = {tiles, flags (bit 0: an id outside [0, E)), small tiles, groups}, and the pair maps.
 hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, int N, int k, int E,

@@ -15,7 +15,7 @@ namespace {
 template <bool BF16>
 __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long long ldx, int rows, int K,
                                                           const int4* tiles, const int* n_tiles, const int* row_map,
-                                                          uint8_t* out)
+                                                          int large_only, uint8_t* out)
 {
   __shared__ __attribute__((aligned(16))) uint8_t chunk[kAtChunkBytes];
   const int nsc = at_nchunks(K);
@@ -26,6 +26,7 @@ __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long lo
   int row0, nrows;
   if (tiles) {
     const int4 tt = tiles[t];
+    if (large_only && tt.w == 0) return;  // the whole work-group: a small bucket's tile
     row0 = tt.y;
     nrows = tt.z;
   } else {
@@ -210,7 +211,8 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int
     } else {
       for (int m = 0; m < et; ++m) small_tiles[small_off++] = tile_off + m;
     }
-    for (int m = 0; m < c; m += kFwdRowsPerTile) tiles[tile_off++] = make_int4(e, row_off + m, min(kFwdRowsPerTile, c - m), 0);
+    for (int m = 0; m < c; m += kFwdRowsPerTile)
+      tiles[tile_off++] = make_int4(e, row_off + m, min(kFwdRowsPerTile, c - m), et >= kGroupMinTiles ? 1 : 0);
     row_off += c;
   }
   if (t == 1023) {
@@ -282,6 +284,59 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(float* grad_h, float* 
   *reinterpret_cast<float4*>(grad_h + (long long)t * D + d) = acc;
 }
 
+// The same quantisation into the XT layout: one work-group per (16 rows, super-chunk), rows
+// r0 .. r0 + 15 of x; rows at or past `rows` (at least the one that follows the last) get zeros,
+// the row a tile's unused slots read.
+template <bool BF16>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const void* x, long long ldx, int rows, int K, uint8_t* out)
+{
+  __shared__ __attribute__((aligned(16))) uint8_t chunk[16 * kXtChunkBytes];
+  const int nsc = at_nchunks(K);
+  const int rg = (int)(blockIdx.x / nsc), c = (int)(blockIdx.x - (long long)rg * nsc);
+  const int i = threadIdx.x >> 4, l16 = threadIdx.x & 15;
+  const int row = rg * 16 + i;
+  const bool valid = row < rows;
+  const int cbase = c * kXtChunkBytes;  // xt_*_off are row-relative
+  float v0[kChunkBlocks], v1[kChunkBlocks];
+#pragma unroll
+  for (int b = 0; b < kChunkBlocks; ++b) {
+    const int k = c * kChunk + b * kGroup + 2 * l16;
+    v0[b] = 0.f;
+    v1[b] = 0.f;
+    if (valid && k < K) {
+      if (BF16) {
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + (long long)row * ldx + k);
+        v0[b] = bf16_lo(u);
+        v1[b] = bf16_hi(u);
+      } else {
+        const float2 f = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(x) + (long long)row * ldx + k);
+        v0[b] = f.x;
+        v1[b] = f.y;
+      }
+    }
+  }
+  uint8_t* mine = chunk + i * kXtChunkBytes;
+#pragma unroll
+  for (int b = 0; b < kChunkBlocks; ++b) {
+    const int k = c * kChunk + b * kGroup + 2 * l16;
+    const Quant2 q = quant2_block16(v0[b], v1[b]);
+    *reinterpret_cast<uint16_t*>(mine + (xt_code_off(k, 0) - cbase)) = (uint16_t)q.hi;
+    *reinterpret_cast<uint16_t*>(mine + (xt_code_off(k, 1) - cbase)) = (uint16_t)q.lo;
+    if (l16 == 0) {
+      mine[xt_scale_off(k, 0) - cbase] = (uint8_t)q.s_hi;
+      mine[xt_scale_off(k, 1) - cbase] = (uint8_t)q.s_lo;
+    }
+  }
+  __syncthreads();
+  // 16 rows x 66 sixteen-byte units, each row's chunk contiguous in memory
+  const long long rb = xt_row_bytes(K);
+  for (int u = threadIdx.x; u < 16 * (kXtChunkBytes / 16); u += 256) {
+    const int rr = u / (kXtChunkBytes / 16), o = (u - rr * (kXtChunkBytes / 16)) * 16;
+    *reinterpret_cast<i32x4*>(out + (long long)(rg * 16 + rr) * rb + cbase + o) =
+        *reinterpret_cast<const i32x4*>(chunk + rr * kXtChunkBytes + o);
+  }
+}
+
 __global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, long long n_words)
 {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n_words; i += (long long)gridDim.x * 256) p[i] = 0u;
@@ -290,15 +345,26 @@ __global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, long long n_word
 }  // namespace
 
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
-                              const int* n_tiles, int max_tiles, const int* row_map, uint8_t* out, hipStream_t s)
+                              const int* n_tiles, int max_tiles, const int* row_map, int large_only, uint8_t* out,
+                              hipStream_t s)
 {
   const long long groups = (long long)max_tiles * at_nchunks(K);  // (tile, super-chunk) work-groups
   if (groups == 0) return hipSuccess;
   dim3 grid((unsigned)groups), block(256);
   if (x_bf16)
-    hipLaunchKernelGGL(quant_tiles_kernel<true>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, out);
+    hipLaunchKernelGGL(quant_tiles_kernel<true>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, large_only, out);
   else
-    hipLaunchKernelGGL(quant_tiles_kernel<false>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, out);
+    hipLaunchKernelGGL(quant_tiles_kernel<false>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, large_only, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, uint8_t* out, hipStream_t s)
+{
+  const long long groups = (long long)xt_rows(rows) / 16 * at_nchunks(K);  // (16 rows, super-chunk)
+  if (groups == 0) return hipSuccess;
+  dim3 grid((unsigned)groups), block(256);
+  if (x_bf16) hipLaunchKernelGGL(quant_rows_kernel<true>, grid, block, 0, s, x, ldx, rows, K, out);
+  else hipLaunchKernelGGL(quant_rows_kernel<false>, grid, block, 0, s, x, ldx, rows, K, out);
   return hipGetLastError();
 }
 
