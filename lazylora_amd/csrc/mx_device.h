@@ -77,8 +77,9 @@ MX_DEV long long at_scale_off(int i, int k, int plane)
 
 // ------------------------------------------------------------------ XT activation layout
 // The same codes and scales stored once per row of x instead of once per work tile ("XT",
-// token-major): the routed gate/up product gathers each tile lane's pieces from the row of its
-// token, so a token chosen by k experts is quantised and stored once, not k times. Per (row,
+// token-major): the one-tile work-groups of the routed gate/up product gather each tile lane's
+// pieces from the row of its token, so a token chosen by k experts is quantised and stored once,
+// not k times. Per (row,
 // super-chunk): 1024 B of codes [q][plane][piece][g][16 B] (the 16-byte piece that tile lane
 // 16g + i takes from row i), then 32 B of scales [plane][g][4 B: byte q].
 constexpr int kXtCodeBytes = 1024;
