@@ -12,6 +12,11 @@
  *   K must be a multiple of 32. All array pointers are DEVICE pointers (HBM), except where
  *   noted. Every call is asynchronous on `stream` (0 = the null stream).
  *
+ * Alignment (checked; a violation returns MXFP4_EINVAL and launches nothing): packed weights
+ * and scales 16 bytes (mxfp4_dequant takes any alignment); mxfp4_gemm's x 8 bytes; mxfp4_gemm_t's dy 4 bytes; the routed layer's
+ * h 8 bytes (fp32) or 4 bytes (bf16), 16 bytes with LoRA, as are grad_out and the LoRA
+ * factors then. Buffers from hipMalloc or torch satisfy all of these.
+ *
  * Deviations from the reference signatures, all deliberate:
  *   - every call returns int status (0 = ok, see MXFP4_E*) instead of void;
  *   - every call takes a hipStream_t, and calls that need scratch take a caller-owned

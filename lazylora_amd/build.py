@@ -29,19 +29,37 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source into LIB (always recompiles). Returns the library path."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC] + FLAGS + srcs + ["-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd):
     res = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if verbose and err:
-        print(err, file=sys.stderr)
+    return res.returncode, err
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source into LIB (always recompiles; the translation units in parallel,
+    objects under _build/). Returns the library path."""
+    from concurrent.futures import ThreadPoolExecutor
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    jobs = []
+    for src in SOURCES:
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        jobs.append(([HIPCC] + compile_flags + ["-c", os.path.join(CSRC, src), "-o", obj], obj))
+    if verbose:
+        for cmd, _ in jobs:
+            print(" ".join(cmd), flush=True)
+    with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1, 16)) as ex:
+        results = list(ex.map(lambda j: _run(j[0]), jobs))
+    for (cmd, _), (rc, err) in zip(jobs, results):
+        if rc != 0:
+            raise RuntimeError(f"hipcc failed ({rc}) on {cmd[-3]}:\n{err}")
+        if verbose and err:
+            print(err, file=sys.stderr)
+    tmp = LIB + ".tmp"
+    rc, err = _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC"] + [o for _, o in jobs] + ["-o", tmp])
+    if rc != 0:
+        raise RuntimeError(f"link failed ({rc}):\n{err}")
     os.replace(tmp, LIB)
     return LIB
 

@@ -164,8 +164,11 @@ int check_moe_args(const void* h, int h_dtype, const void* idx, int idx_dtype, c
   if (N > 0 && (!h || !idx || !w)) return fail(MXFP4_EINVAL, "moe: null input pointer%s");
   for (int i = 0; i < 6; ++i) {
     if (!wts[i]) return fail(MXFP4_EINVAL, "moe: null expert weight pointer%s");
-    if (i % 2 == 0 && !aligned16(wts[i])) return fail(MXFP4_EINVAL, "moe: packed weights must be 16-byte aligned%s");
+    if (!aligned16(wts[i])) return fail(MXFP4_EINVAL, "moe: packed weights and scales must be 16-byte aligned%s");
   }
+  // the activation quantisers read h two elements at a time
+  if (N > 0 && ((uintptr_t)h & (h_dtype == MXFP4_BF16 ? 3 : 7)))
+    return fail(MXFP4_EINVAL, "moe: h must be 8-byte (fp32) or 4-byte (bf16) aligned%s");
   if ((long long)N * k > (1ll << 30)) return fail(MXFP4_EINVAL, "moe: too many (token, slot) pairs%s");
   return MXFP4_OK;
 }
@@ -280,6 +283,38 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   return MXFP4_OK;
 }
 
+// Argument checks of the single-expert forward product.
+int check_gemm_args(const float* y, const float* x, const uint8_t* packed, const uint8_t* scales, int M, int K,
+                    int R)
+{
+  if (M < 0 || R < 0 || K <= 0 || K % 32) return fail(MXFP4_EINVAL, "gemm: K must be a positive multiple of 32%s");
+  if (M == 0 || R == 0) return MXFP4_OK;
+  if (!y || !x || !packed || !scales) return fail(MXFP4_EINVAL, "gemm: null pointer%s");
+  if (!aligned16(packed) || !aligned16(scales)) return fail(MXFP4_EINVAL, "gemm: packed and scales must be 16-byte aligned%s");
+  if (((uintptr_t)x & 7) != 0) return fail(MXFP4_EINVAL, "gemm: x must be 8-byte aligned%s");
+  return MXFP4_OK;
+}
+
+// y[M, R] = x . W^T with x's two-term e4m3 tiles staged at `tiles` (at_bytes(ceil(M/16), K)
+// bytes, fully rewritten by the quantiser: unused row slots and K positions past the row end are
+// written as zeros, so the buffer needs no clearing between calls).
+int gemm_into(float* y, const float* x, const uint8_t* packed, const uint8_t* scales, int M, int K, int R,
+              uint8_t* tiles_dev, hipStream_t stream)
+{
+  const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
+  MX_TRY(mx::launch_quant_tiles(x, 0, K, M, K, nullptr, nullptr, tiles, nullptr, 0, tiles_dev, stream),
+         "gemm: quantise x");
+  mx::FwdArgs a = {};
+  a.wp0 = packed; a.ws0 = scales;
+  a.R = R; a.K = K;
+  a.a_tiles = tiles_dev;
+  a.M = M;
+  a.n_ct = (R + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
+  a.y = y; a.ldy = R;
+  MX_TRY(mx::launch_fwd(a, mx::kFwdPlain, tiles, stream), "gemm: product");
+  return MXFP4_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -312,24 +347,11 @@ size_t mxfp4_gemm_workspace_size(int M, int K, int R)
 int mxfp4_gemm(float* y, const float* x, const uint8_t* packed, const uint8_t* scales, int M, int K, int R,
                void* workspace, size_t workspace_bytes, hipStream_t stream)
 {
-  if (M < 0 || R < 0 || K <= 0 || K % 32) return fail(MXFP4_EINVAL, "gemm: K must be a positive multiple of 32%s");
-  if (M == 0 || R == 0) return MXFP4_OK;
-  if (!y || !x || !packed || !scales) return fail(MXFP4_EINVAL, "gemm: null pointer%s");
-  if (!aligned16(packed)) return fail(MXFP4_EINVAL, "gemm: packed must be 16-byte aligned%s");
-  if (((uintptr_t)x & 7) != 0) return fail(MXFP4_EINVAL, "gemm: x must be 8-byte aligned%s");
+  const int rc = check_gemm_args(y, x, packed, scales, M, K, R);
+  if (rc != MXFP4_OK || M == 0 || R == 0) return rc;
   const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
   if (!workspace || workspace_bytes < at_bytes(tiles, K)) return fail(MXFP4_EWORKSPACE, "gemm: workspace too small%s");
-  MX_TRY(mx::launch_quant_tiles(x, 0, K, M, K, nullptr, nullptr, tiles, nullptr, 0, at<uint8_t>(workspace, 0), stream),
-         "gemm: quantise x");
-  mx::FwdArgs a = {};
-  a.wp0 = packed; a.ws0 = scales;
-  a.R = R; a.K = K;
-  a.a_tiles = at<uint8_t>(workspace, 0);
-  a.M = M;
-  a.n_ct = (R + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
-  a.y = y; a.ldy = R;
-  MX_TRY(mx::launch_fwd(a, mx::kFwdPlain, tiles, stream), "gemm: product");
-  return MXFP4_OK;
+  return gemm_into(y, x, packed, scales, M, K, R, at<uint8_t>(workspace, 0), stream);
 }
 
 size_t mxfp4_gemm_t_workspace_size(int M, int K, int R)
@@ -345,7 +367,8 @@ int mxfp4_gemm_t(float* y, const float* dy, const uint8_t* packed, const uint8_t
   if (M < 0 || R < 0 || K <= 0 || K % 32) return fail(MXFP4_EINVAL, "gemm_t: K must be a positive multiple of 32%s");
   if (M == 0 || R == 0) return MXFP4_OK;
   if (!y || !dy || !packed || !scales) return fail(MXFP4_EINVAL, "gemm_t: null pointer%s");
-  if (!aligned16(packed)) return fail(MXFP4_EINVAL, "gemm_t: packed must be 16-byte aligned%s");
+  if (!aligned16(packed) || !aligned16(scales)) return fail(MXFP4_EINVAL, "gemm_t: packed and scales must be 16-byte aligned%s");
+  if (((uintptr_t)dy & 3) != 0) return fail(MXFP4_EINVAL, "gemm_t: dy must be 4-byte aligned%s");
   const size_t need = mxfp4_gemm_t_workspace_size(M, K, R);
   if (!workspace || workspace_bytes < need) return fail(MXFP4_EWORKSPACE, "gemm_t: workspace too small%s");
   const long long rp = pad32(R);

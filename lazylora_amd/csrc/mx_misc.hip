@@ -265,13 +265,14 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(float* grad_h, float* 
   const int t = blockIdx.y;
   const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (t >= N) return;
-  if (blockIdx.x == 0 && threadIdx.x < k) {
-    const int s = threadIdx.x;
-    const int p = pair_of[t * k + s];
-    float gsum = 0.f;
-    if (p >= 0)
-      for (int c = 0; c < n_ct; ++c) gsum += gw_part[(long long)p * n_ct + c];
-    grad_w[t * k + s] = gsum;
+  if (blockIdx.x == 0) {
+    for (int s = threadIdx.x; s < k; s += 256) {
+      const int p = pair_of[t * k + s];
+      float gsum = 0.f;
+      if (p >= 0)
+        for (int c = 0; c < n_ct; ++c) gsum += gw_part[(long long)p * n_ct + c];
+      grad_w[t * k + s] = gsum;
+    }
   }
   if (d >= D) return;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);

@@ -13,10 +13,13 @@ namespace mx {
 
 namespace {
 
-// (value, index) pair order for the selection: larger value first, then the lower index
+// (value, index) pair order for the selection: NaN first (torch.topk ranks NaN above every
+// number), then the larger value, then the lower index.
 __device__ __forceinline__ bool beats(float v, int i, float bv, int bi)
 {
-  return v > bv || (v == bv && i < bi);
+  const bool vn = v != v, bn = bv != bv;
+  if (vn != bn) return vn;
+  return (vn || v == bv) ? i < bi : v > bv;
 }
 
 template <int PER_LANE>
@@ -30,16 +33,19 @@ __global__ __launch_bounds__(256) void router_topk_kernel(long long* __restrict_
   if (token >= N) return;  // whole waves leave together
   const float* row = logits + (long long)token * E;
 
-  // this lane's experts e = lane + 64 m; absent experts can never be chosen
+  // this lane's experts e = lane + 64 m; `open` marks the ones still selectable (present and
+  // not yet chosen), so every round's winner is a real expert id whatever the scores hold
+  // (NaN, infinities) as long as top_k <= E, which the host checks
   float choice[PER_LANE];
+  uint64_t open = 0;
 #pragma unroll
   for (int m = 0; m < PER_LANE; ++m) {
     const int e = lane + 64 * m;
+    choice[m] = 0.f;
     if (e < E) {
       const float s = 1.0f / (1.0f + expf(-row[e]));
       choice[m] = bias ? s + bias[e] : s;
-    } else {
-      choice[m] = -__builtin_inff();
+      open |= 1ull << m;
     }
   }
 
@@ -48,11 +54,11 @@ __global__ __launch_bounds__(256) void router_topk_kernel(long long* __restrict_
   int mine_idx = 0;
   for (int t = 0; t < top_k; ++t) {
     float bv = -__builtin_inff();
-    int bi = 0x7fffffff;
+    int bi = 0x7fffffff;  // "none": loses to every open entry
 #pragma unroll
     for (int m = 0; m < PER_LANE; ++m) {
       const int e = lane + 64 * m;
-      if (beats(choice[m], e, bv, bi)) {
+      if (((open >> m) & 1) && (bi == 0x7fffffff || beats(choice[m], e, bv, bi))) {
         bv = choice[m];
         bi = e;
       }
@@ -61,17 +67,14 @@ __global__ __launch_bounds__(256) void router_topk_kernel(long long* __restrict_
     for (int off = 32; off >= 1; off >>= 1) {
       const float ov = __shfl_xor(bv, off, 64);
       const int oi = __shfl_xor(bi, off, 64);
-      if (beats(ov, oi, bv, bi)) {
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || beats(ov, oi, bv, bi))) {
         bv = ov;
         bi = oi;
       }
     }
+    if (bi >= E) bi = 0;  // unreachable while top_k <= E; keeps the read below in bounds
     // every lane now holds the winner; its owner retires it
-    if ((bi & 63) == lane) {
-#pragma unroll
-      for (int m = 0; m < PER_LANE; ++m)
-        if (lane + 64 * m == bi) choice[m] = -__builtin_inff();
-    }
+    if ((bi & 63) == lane) open &= ~(1ull << (bi >> 6));
     const float s = 1.0f / (1.0f + expf(-row[bi]));  // the unbiased score
     sum += s;
     if (lane == t) {

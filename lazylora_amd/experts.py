@@ -41,7 +41,7 @@ class ExpertLayer:
         self.device = torch.device(device)
         self.E, self.D, self.F = E, D, F
         (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s) = [
-            t.to(self.device, non_blocking=True).contiguous() for t in tensors]
+            _aligned16(t.to(self.device, non_blocking=True).contiguous()) for t in tensors]
 
     @classmethod
     def empty(cls, E: int, D: int, F: int, device=None) -> "ExpertLayer":
@@ -52,12 +52,46 @@ class ExpertLayer:
         return cls(*[torch.empty(s, dtype=torch.uint8, device=device) for s in shapes], device=device)
 
     @classmethod
-    def from_bundles(cls, bundles: Sequence, device=None) -> "ExpertLayer":
-        """Stack per-expert bundles with gate/up/down_packed and _scale attributes."""
-        def stack(attr):
-            return torch.stack([getattr(b, attr) for b in bundles])
-        return cls(stack("gate_packed"), stack("gate_scale"), stack("up_packed"), stack("up_scale"),
-                   stack("down_packed"), stack("down_scale"), device=device)
+    def from_bundles(cls, bundles: Sequence, device=None, num_experts: Optional[int] = None) -> "ExpertLayer":
+        """A layer from the reference's per-expert ExpertWeightBundle objects (packed form: the
+        gate/up/down_packed and _scale attributes, expert_streamer.py:27-50).
+
+        `bundles` is either a sequence of bundles, expert e at position e, or (expert_id,
+        bundle) pairs as DynamicExpertStreamer.stream_experts yields them (in disk order, only
+        the active experts, expert_streamer.py:315-369); then expert ids index a layer of
+        `num_experts` experts (default: the largest id + 1) whose absent experts are zero
+        weights, which no routing that only selects streamed experts reads."""
+        items = list(bundles)
+        pairs = bool(items) and isinstance(items[0], tuple)
+        if not pairs:
+            items = list(enumerate(items))
+        if not items:
+            raise ValueError("from_bundles needs at least one expert")
+        for eid, b in items:
+            if not getattr(b, "packed", b.gate_packed is not None) or b.gate_packed is None:
+                raise ValueError(f"expert {eid} is not in packed MXFP4 form")
+        ids = [int(eid) for eid, _ in items]
+        if len(set(ids)) != len(ids) or min(ids) < 0:
+            raise ValueError("expert ids must be distinct and non-negative")
+        E = num_experts if num_experts is not None else max(ids) + 1
+        if max(ids) >= E:
+            raise ValueError(f"expert id {max(ids)} does not fit a layer of {E} experts")
+        if device is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        attrs = ("gate_packed", "gate_scale", "up_packed", "up_scale", "down_packed", "down_scale")
+        first = items[0][1]
+        stacked = []
+        for attr in attrs:
+            t0 = getattr(first, attr)
+            dst = torch.zeros((E,) + tuple(t0.shape), dtype=torch.uint8, device=device)
+            for eid, b in items:
+                src = getattr(b, attr)
+                if tuple(src.shape) != tuple(t0.shape) or src.dtype != torch.uint8:
+                    raise ValueError(f"expert {eid}: {attr} must be uint8 {tuple(t0.shape)}, "
+                                     f"got {src.dtype} {tuple(src.shape)}")
+                dst[eid].copy_(src, non_blocking=True)
+            stacked.append(dst)
+        return cls(*stacked, device=device)
 
     def pointers(self):
         return (self.w1p.data_ptr(), self.w1s.data_ptr(), self.w3p.data_ptr(), self.w3s.data_ptr(),
@@ -73,3 +107,9 @@ class ExpertLayer:
 
     def tensors(self) -> Iterable[torch.Tensor]:
         return (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s)
+
+
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its data starts on a 16-byte boundary (the kernels' requirement for packed
+    weights and scales), else an aligned copy."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()

@@ -11,12 +11,17 @@ Differences from the reference, all deliberate:
     result is copied back, so the unmodified CPU trainer also works;
   * shape errors raise ValueError (the reference asserts), and K % 32 != 0 is rejected
     (the reference floors K/32 and reads uninitialised memory);
-  * a missing or unloadable library raises RuntimeError instead of returning None: a
-    silent fallback would hide that the GPU path is not running. LAZYLORA_NO_NATIVE=1
-    still returns None, as the reference's opt-out does (native/__init__.py:79-80).
+  * `kernel()` returns None, with a printed warning, when the library is missing or fails to
+    load or no HIP device is visible, as the reference's does (native/__init__.py:77-96), so
+    callers that probe `kernel() is not None` (expert_streamer.py:206-207) take their own
+    fallback. LAZYLORA_NATIVE_STRICT=1 makes those cases raise RuntimeError instead, for
+    deployments where the GPU path must run. LAZYLORA_NO_NATIVE=1 returns None silently.
+    Nothing here falls back to a CPU implementation: the MXFP4Kernel methods run on the GPU
+    or raise.
 """
 import ctypes
 import os
+import sys
 from typing import Optional, Tuple
 
 import torch
@@ -34,6 +39,7 @@ MOE_REUSE_FORWARD = 2
 
 _lib = None
 _kernel = None
+_tried = False
 
 
 def _load_library() -> ctypes.CDLL:
@@ -134,7 +140,7 @@ class MXFP4Kernel:
         R = packed.shape[0]
         _check_weight(packed, scales, R, K)
         dev = _device_for(x)
-        xd = x.to(dev, non_blocking=True).contiguous().float()
+        xd = _aligned(x.to(dev, non_blocking=True).contiguous().float())
         p, s = _u8(packed, dev, "packed"), _u8(scales, dev, "scales")
         y = torch.empty((M, R), dtype=torch.float32, device=dev)
         if M and R:
@@ -156,7 +162,7 @@ class MXFP4Kernel:
             raise ValueError(f"dy has {R} columns but W has {packed.shape[0]} rows")
         _check_weight(packed, scales, R, K)
         dev = _device_for(dy)
-        dyd = dy.to(dev, non_blocking=True).contiguous().float()
+        dyd = _aligned(dy.to(dev, non_blocking=True).contiguous().float())
         p, s = _u8(packed, dev, "packed"), _u8(scales, dev, "scales")
         y = torch.zeros((M, K), dtype=torch.float32, device=dev)
         if M and R:
@@ -216,6 +222,9 @@ class MXFP4Kernel:
         workspace must come from a routed_forward(save_for_backward=True) call on the same inputs
         and adapters; the routing and gate/up products are then not recomputed.
         """
+        if reuse_forward and workspace is None:
+            raise ValueError("reuse_forward=True needs the workspace of a routed_forward(save_for_backward=True) "
+                             "call on the same inputs")
         call = _RoutedCall(self.lib, h, topk_indices, topk_weights, experts, act, workspace)
         lo = _LoraCall(lora, call.dev, call.D, call.F)
         if grad_out.shape != (call.N, call.D):
@@ -412,11 +421,34 @@ class _LoraCall:
         self.scaling = (ctypes.c_float * 3)(*[float(m.scaling) for m in mods])
 
 
+def _unavailable(why: str) -> None:
+    if os.environ.get("LAZYLORA_NATIVE_STRICT", "") == "1":
+        raise RuntimeError(f"MI355X MXFP4 kernels unavailable: {why}")
+    print(f"[!] MI355X MXFP4 kernels not available ({why}); callers use their fallback path",
+          file=sys.stderr, flush=True)
+
+
 def kernel() -> Optional[MXFP4Kernel]:
-    """The MXFP4 kernel object, or None when LAZYLORA_NO_NATIVE=1 (native/__init__.py:77-97)."""
-    global _kernel
+    """The MXFP4 kernel object, or None (native/__init__.py:77-97): None when
+    LAZYLORA_NO_NATIVE=1, and, after one printed warning, when the library is missing or fails
+    to load or no HIP device is visible (LAZYLORA_NATIVE_STRICT=1: raise RuntimeError instead).
+    A failed attempt is not repeated, as in the reference."""
+    global _kernel, _tried
     if os.environ.get("LAZYLORA_NO_NATIVE", "") == "1":
         return None
-    if _kernel is None:
-        _kernel = MXFP4Kernel(_load_library())
+    if _kernel is not None:
+        return _kernel
+    strict = os.environ.get("LAZYLORA_NATIVE_STRICT", "") == "1"
+    if _tried and not strict:
+        return None
+    _tried = True
+    try:
+        lib = _load_library()
+    except (RuntimeError, OSError) as exc:
+        _unavailable(str(exc))
+        return None
+    if not torch.cuda.is_available():
+        _unavailable("no HIP device is visible")
+        return None
+    _kernel = MXFP4Kernel(lib)
     return _kernel

@@ -82,25 +82,96 @@ class RoutedExpertsFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h_latent, topk_weights, topk_indices, layer, act="swiglu", cached=None, lora=None):
         k = _native()
-        ws = torch.empty(max(k.moe_workspace_bytes(h_latent.shape[0], topk_indices.shape[1], layer.E,
-                                                   layer.D, layer.F), 1),
-                         dtype=torch.uint8, device=layer.device)
+        ws = None
         if cached is not None:
+            # the backward replay: the routed sum is already known, and the backward recomputes
+            # what it needs (lazy_trainer.py:60-66)
             out = cached.to(torch.float32)
-            reuse = False
         else:
+            ws = torch.empty(max(k.moe_workspace_bytes(h_latent.shape[0], topk_indices.shape[1], layer.E,
+                                                       layer.D, layer.F), 1),
+                             dtype=torch.uint8, device=layer.device)
             out = k.routed_forward(h_latent, topk_indices, topk_weights, layer, act=act,
                                    save_for_backward=True, workspace=ws, lora=lora)
-            reuse = True
         ctx.save_for_backward(h_latent, topk_weights, topk_indices)
-        ctx.layer, ctx.act, ctx.ws, ctx.reuse, ctx.lora = layer, act, ws, reuse, lora
+        # the workspace holds the forward's routing and gate|up only until the first backward
+        # has used them; a second backward (retain_graph=True) recomputes them
+        ctx.layer, ctx.act, ctx.ws, ctx.lora = layer, act, ws, lora
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
         h_latent, topk_weights, topk_indices = ctx.saved_tensors
+        ws, ctx.ws = ctx.ws, None
         grad_h, grad_w = routed_experts_backward(h_latent, topk_indices, topk_weights, ctx.layer,
-                                                 grad_out, act=ctx.act, reuse_forward=ctx.reuse,
-                                                 workspace=ctx.ws, lora=ctx.lora)
-        ctx.ws = None
+                                                 grad_out, act=ctx.act, reuse_forward=ws is not None,
+                                                 workspace=ws, lora=ctx.lora)
         return grad_h, grad_w, None, None, None, None, None
+
+
+def layer_from_stream(expert_streamer, layer_idx, active_experts, num_experts=None, device=None) -> ExpertLayer:
+    """The active experts of one layer, supplied by the reference's streamer as packed
+    ExpertWeightBundles (DynamicExpertStreamer.stream_experts, expert_streamer.py:315-369, in disk
+    order), placed by expert id in an HBM ExpertLayer."""
+    pairs = list(expert_streamer.stream_experts(layer_idx, active_experts))
+    return ExpertLayer.from_bundles(pairs, device=device, num_experts=num_experts)
+
+
+class StreamedRoutedExpertsFunction(torch.autograd.Function):
+    """The reference node's own signature (lazy_trainer.py:45-77):
+    apply(h_latent, topk_weights, topk_indices, trainer, layer_idx, bundle, active_experts, cached).
+
+    As in the reference, the experts are streamed once in forward (skipped when `cached` holds
+    the routed sum) and once more in backward, and nothing expert-sized stays alive between the
+    two: each pass takes the packed bundles of `trainer.expert_streamer.stream_experts(layer_idx,
+    active_experts)` into HBM and runs the whole layer in one call. The activation is SiTU-GLU and
+    `bundle` is the layer's LoRALayerBundle (its gate/up/down adapters), as in
+    _routed_experts_forward/_backward (lazy_trainer.py:806-880); the adapters' gradients are
+    accumulated into them with accumulate_grad. The streamer must hand over packed bundles
+    (keep_packed, which holds whenever kernel() is not None)."""
+
+    @staticmethod
+    def forward(ctx, h_latent, topk_weights, topk_indices, trainer, layer_idx, bundle, active_experts, cached=None):
+        if cached is not None:
+            out = cached.to(torch.float32)
+        else:
+            layer = layer_from_stream(trainer.expert_streamer, layer_idx, active_experts,
+                                      num_experts=_num_experts(trainer, topk_indices, active_experts),
+                                      device=h_latent.device if h_latent.is_cuda else None)
+            out = routed_experts_forward(h_latent, topk_indices, topk_weights, layer, act="situ", lora=_lora(bundle))
+            del layer
+            out = out.to(h_latent.device)
+        ctx.save_for_backward(h_latent, topk_weights, topk_indices)
+        ctx.trainer, ctx.layer_idx, ctx.bundle, ctx.active_experts = trainer, layer_idx, bundle, active_experts
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        h_latent, topk_weights, topk_indices = ctx.saved_tensors
+        layer = layer_from_stream(ctx.trainer.expert_streamer, ctx.layer_idx, ctx.active_experts,
+                                  num_experts=_num_experts(ctx.trainer, topk_indices, ctx.active_experts),
+                                  device=h_latent.device if h_latent.is_cuda else None)
+        grad_h, grad_w = routed_experts_backward(h_latent, topk_indices, topk_weights, layer, grad_out,
+                                                 act="situ", lora=_lora(ctx.bundle))
+        return (grad_h.to(h_latent.device), grad_w.to(topk_weights.device), None, None, None, None, None, None)
+
+
+def _lora(bundle):
+    """The layer's routed-expert adapters, or None when the bundle carries none."""
+    if bundle is None or getattr(bundle, "gate_lora", None) is None:
+        return None
+    mods = _adapters(bundle)
+    if any(getattr(m, "r", 1) == 0 or getattr(m, "lora_A", None) is None for m in mods):
+        return None
+    return bundle
+
+
+def _num_experts(trainer, topk_indices, active_experts) -> int:
+    """Experts of the layer: the trainer's configured count when it has one, else enough for every
+    routed id (ids are validated against it by the routed call)."""
+    cfg = getattr(getattr(trainer, "config", None), "model", None)
+    n = getattr(cfg, "n_routed_experts", None) or getattr(cfg, "num_experts", None)
+    if n:
+        return int(n)
+    hi = int(topk_indices.max()) if topk_indices.numel() else 0
+    return max([hi] + [int(e) for e in active_experts]) + 1

@@ -134,11 +134,14 @@ def glu_backward(grad, gate, up, act: str):
 def router_select(logits, bias=None, top_k=2, routed_scaling_factor=1.0, renormalize=True):
     """The selection half of KimiK3MoERouter.forward on given logits [N, E]
     (lazy_lora/core/moe_router.py:106-123): sigmoid scores, bias added for selection only,
-    top-k (stable: equal choices go to the lower expert id), gather unbiased scores,
-    renormalise (+1e-20) when top_k > 1, scale. Returns (indices [N, k] int64, weights float64)."""
+    top-k (stable: equal choices go to the lower expert id; NaN ranks above every number, as in
+    torch.topk), gather unbiased scores, renormalise (+1e-20) when top_k > 1, scale. Returns
+    (indices [N, k] int64, weights float64)."""
     scores = _sigmoid(np.asarray(logits, np.float64))
     choice = scores + np.asarray(bias, np.float64) if bias is not None else scores
-    idx = np.argsort(-choice, axis=-1, kind="stable")[:, :top_k]
+    nan = np.isnan(choice)
+    # lexsort's last key is the primary one: NaN first, then descending value; stable in the id
+    idx = np.lexsort((-np.where(nan, 0.0, choice), (~nan).astype(np.int8)), axis=-1)[:, :top_k]
     w = np.take_along_axis(scores, idx, axis=-1)
     if top_k > 1 and renormalize:
         w = w / (w.sum(-1, keepdims=True) + 1e-20)

@@ -64,9 +64,9 @@ def test_host_side_argument_errors(lib):
     assert lib.mxfp4_router_topk_backward(dummy, dummy, dummy, dummy, 4, 8, 9, 1.0, 1, None) == -1
 
 
-def test_python_api_validation():
-    from lazylora_amd.native import kernel
-    k = kernel()
+def test_python_api_validation(lib):
+    from lazylora_amd import native
+    k = native.MXFP4Kernel(lib)  # the shape checks run before any device is needed
     x = torch.zeros(2, 64)
     with pytest.raises(ValueError):
         k.gemm(x, torch.zeros(8, 16, dtype=torch.uint8), torch.zeros(8, 2, dtype=torch.uint8))
@@ -89,10 +89,109 @@ def test_no_native_opt_out(monkeypatch):
     assert native.kernel() is None
 
 
-def test_missing_library_fails_loudly(monkeypatch, tmp_path):
-    from lazylora_amd import native
+def _fresh(monkeypatch, native):
     monkeypatch.setattr(native, "_lib", None)
     monkeypatch.setattr(native, "_kernel", None)
+    monkeypatch.setattr(native, "_tried", False)
+    monkeypatch.delenv("LAZYLORA_NO_NATIVE", raising=False)
+    monkeypatch.delenv("LAZYLORA_NATIVE_STRICT", raising=False)
+
+
+def test_missing_library_gives_none(monkeypatch, tmp_path, capsys):
+    """The reference's contract (native/__init__.py:77-96): an unavailable library is None plus a
+    warning, so a caller that probes `kernel() is not None` (expert_streamer.py:206-207) falls
+    back instead of crashing."""
+    from lazylora_amd import native
+    _fresh(monkeypatch, native)
     monkeypatch.setattr(native, "LIB_PATH", str(tmp_path / "absent.so"))
+    assert native.kernel() is None
+    assert "not available" in capsys.readouterr().err
+    assert native.kernel() is None  # the failed attempt is not repeated
+    keep_packed = native.kernel() is not None  # the streamer's probe
+    assert keep_packed is False
+
+
+def test_unloadable_library_gives_none(monkeypatch, tmp_path):
+    from lazylora_amd import native
+    _fresh(monkeypatch, native)
+    bad = tmp_path / "broken.so"
+    bad.write_bytes(b"not an ELF file")
+    monkeypatch.setattr(native, "LIB_PATH", str(bad))
+    assert native.kernel() is None
+
+
+def test_strict_mode_raises(monkeypatch, tmp_path):
+    from lazylora_amd import native
+    _fresh(monkeypatch, native)
+    monkeypatch.setattr(native, "LIB_PATH", str(tmp_path / "absent.so"))
+    monkeypatch.setenv("LAZYLORA_NATIVE_STRICT", "1")
     with pytest.raises(RuntimeError, match="missing"):
         native.kernel()
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device case")
+def test_no_device_gives_none(monkeypatch):
+    from lazylora_amd import native
+    _fresh(monkeypatch, native)
+    assert native.kernel() is None
+
+
+def test_alignment_rejected_on_host(lib):
+    """Packed weights and scales need 16-byte alignment, gemm's x 8 bytes, gemm_t's dy 4 bytes
+    and the routed layer's h 8 bytes (fp32) / 4 bytes (bf16); violations return EINVAL before any
+    launch (include/lazylora_mxfp4.h)."""
+    vp = ctypes.c_void_p
+    ok, odd8, odd4, odd1 = vp(4096), vp(4096 + 8), vp(4096 + 4), vp(4096 + 1)
+    ws = vp(1 << 20)
+    assert lib.mxfp4_gemm(ok, ok, ok, odd8, 4, 64, 4, ws, 1 << 30, None) == -1      # scales
+    assert b"16-byte" in lib.mxfp4_last_error()
+    assert lib.mxfp4_gemm(ok, odd4, ok, ok, 4, 64, 4, ws, 1 << 30, None) == -1      # x
+    assert lib.mxfp4_gemm_t(ok, ok, ok, odd8, 4, 64, 4, ws, 1 << 30, None) == -1    # scales
+    assert lib.mxfp4_gemm_t(ok, odd1, ok, ok, 4, 64, 4, ws, 1 << 30, None) == -1    # dy
+    wts = [ok] * 6
+    for i in range(6):  # every packed and scale array of the experts
+        w = list(wts)
+        w[i] = odd8
+        args = [ok, ok, 0, ok, 3, ok, 4, 2] + w + [8, 64, 32]
+        assert lib.mxfp4_moe_forward(*args, 0, 0, ws, 1 << 40, None) == -1, i
+    args = [ok, odd4, 0, ok, 3, ok, 4, 2] + wts + [8, 64, 32]                   # fp32 h at 4 bytes
+    assert lib.mxfp4_moe_forward(*args, 0, 0, ws, 1 << 40, None) == -1
+    assert b"h must be" in lib.mxfp4_last_error()
+    args = [ok, odd1, 1, ok, 3, ok, 4, 2] + wts + [8, 64, 32]                   # bf16 h at 1 byte
+    assert lib.mxfp4_moe_forward(*args, 0, 0, ws, 1 << 40, None) == -1
+
+
+def test_from_bundles_places_streamed_experts_by_id():
+    """ExpertLayer.from_bundles takes the reference's ExpertWeightBundle objects, either as a
+    list (expert e at position e) or as the (expert_id, bundle) pairs stream_experts yields in
+    disk order (expert_streamer.py:315-369); absent experts are zeros."""
+    from types import SimpleNamespace
+    from lazylora_amd.experts import ExpertLayer
+    D, F = 64, 32
+    g = torch.Generator().manual_seed(0)
+
+    def bundle(e):
+        def r(*shape):
+            return torch.randint(0, 256, shape, generator=g, dtype=torch.uint8)
+        return SimpleNamespace(expert_idx=e, packed=True,
+                               gate_packed=r(F, D // 2), gate_scale=r(F, D // 32), up_packed=r(F, D // 2),
+                               up_scale=r(F, D // 32), down_packed=r(D, F // 2), down_scale=r(D, F // 32))
+
+    streamed = [(5, bundle(5)), (1, bundle(1)), (3, bundle(3))]  # disk order, not id order
+    layer = ExpertLayer.from_bundles(streamed, device="cpu", num_experts=8)
+    assert (layer.E, layer.D, layer.F) == (8, D, F)
+    for eid, b in streamed:
+        assert torch.equal(layer.w1p[eid], b.gate_packed) and torch.equal(layer.w1s[eid], b.gate_scale)
+        assert torch.equal(layer.w3p[eid], b.up_packed) and torch.equal(layer.w3s[eid], b.up_scale)
+        assert torch.equal(layer.w2p[eid], b.down_packed) and torch.equal(layer.w2s[eid], b.down_scale)
+    for eid in (0, 2, 4, 6, 7):
+        assert int(layer.w1p[eid].abs().sum()) == 0 and int(layer.w2s[eid].abs().sum()) == 0
+    listed = ExpertLayer.from_bundles([b for _, b in sorted(streamed)], device="cpu")
+    assert listed.E == 3 and torch.equal(listed.w2p[2], streamed[0][1].down_packed)
+    with pytest.raises(ValueError):
+        ExpertLayer.from_bundles([(2, bundle(2)), (2, bundle(2))], device="cpu")
+    with pytest.raises(ValueError):
+        ExpertLayer.from_bundles(streamed, device="cpu", num_experts=4)
+    unpacked = SimpleNamespace(packed=False, gate_packed=None)
+    with pytest.raises(ValueError):
+        ExpertLayer.from_bundles([unpacked], device="cpu")

@@ -120,6 +120,38 @@ def test_exact_ties_go_to_lower_id(k):
     assert np.allclose(w.cpu().numpy(), want_w, rtol=1e-6)
 
 
+@pytest.mark.parametrize("E", [100, 1024, 4096])
+def test_nan_logits_select_real_experts(k, E):
+    """NaN logits rank first, as in torch.topk; every chosen id is a real expert, including rows
+    with fewer numeric scores than top_k and E filling every lane slot (1024, 4096)."""
+    case(f"NaN logits E={E}")
+    rng = np.random.default_rng(5)
+    N, top_k = 96, 8
+    logits = rng.standard_normal((N, E)).astype(np.float32)
+    logits[rng.random(logits.shape) < 0.02] = np.nan
+    logits[:8, :] = np.nan                        # rows with no numeric score at all
+    logits[8:16, top_k // 2:] = np.nan            # rows with fewer numeric scores than top_k
+    bias = (0.05 * rng.standard_normal(E)).astype(np.float32)
+    idx, w = k.router_topk(torch.from_numpy(logits).cuda(), torch.from_numpy(bias).cuda(), top_k)
+    idx = idx.cpu().numpy()
+    assert ((idx >= 0) & (idx < E)).all()
+    want_idx, _ = oracle.router_select(logits, bias, top_k)
+    assert idx[:16].tolist() == want_idx[:16].tolist()   # decided by NaN ranks and ids alone
+    choice = oracle._sigmoid(logits.astype(np.float64)) + bias
+    loose = 0
+    for r in range(16, N):
+        nan = np.isnan(choice[r])
+        m = min(int(nan.sum()), top_k)
+        assert idx[r, :m].tolist() == want_idx[r, :m].tolist(), r
+        num = np.sort(choice[r][~nan])[::-1]
+        kth = top_k - m
+        if kth < len(num) and kth > 0 and num[kth - 1] - num[kth] < NEAR:
+            loose += 1                                   # fp32 may order the boundary pair either way
+            continue
+        assert sorted(idx[r, m:].tolist()) == sorted(want_idx[r, m:].tolist()), r
+    assert loose <= 2
+
+
 def test_selection_is_deterministic_and_zero_tokens(k):
     case("determinism over repeated calls; N = 0")
     rng = np.random.default_rng(4)

@@ -118,3 +118,65 @@ def test_streaming_only_active_experts(k):
         out = k.routed_forward(H, I, W, layer)
         assert torch.equal(out, k.routed_forward(H, I, W, resident[order[i]]))
     assert s.bytes_copied == sum(len(x) for x in ids) * hosts[0].nbytes // E
+
+
+def _random_layer_into(layer, seed):
+    """Fill an HBM layer with seeded MXFP4 bytes (codes uniform, scales 117..121: the config-2
+    weights) on the GPU; the same seed always gives the same bytes."""
+    gen = torch.Generator(device=layer.device)
+    gen.manual_seed(seed)
+    for t, is_scale in zip(layer.tensors(), (False, True, False, True, False, True)):
+        if is_scale:
+            t.random_(117, 122, generator=gen)
+        else:
+            t.random_(0, 256, generator=gen)
+    return layer
+
+
+def test_config5_full_size_stream(k, clib):
+    """BASELINE config 5 at its real size: four distinct 896-expert layers of the config-2 shape
+    (20.96 GB each) streamed through LayerStreamer's two HBM slots from a ring of two pinned
+    host layers (expert_streamer.py:315-369 at layer granularity). Each streamed layer's forward
+    for 1024 tokens (top-8) must equal, bit for bit, the forward of the same layer regenerated
+    from its seed in HBM, and the first layer's whole forward must match the C restatement."""
+    from lazylora_amd.experts import ExpertLayer
+    from lazylora_amd.loader import HostLayer
+    from lazylora_amd.streaming import LayerStreamer
+    E, D, F, N, topk, n_layers = 896, 7168, 2048, 1024, 8, 4
+    seeds = [501 + 17 * i for i in range(n_layers)]
+    case("config 5: allocating 2 pinned host layers + 3 HBM layers (~105 GB)")
+    ring = [HostLayer(E, D, F, pin=True) for _ in range(2)]
+    scratch = ExpertLayer.empty(E, D, F)
+    streamer = LayerStreamer(E, D, F, slots=2, timing=True)
+    rng = np.random.default_rng(61)
+    h = rng.standard_normal((N, D)).astype(np.float32)
+    idx, w = oracle.softmax_topk(rng.standard_normal((N, E)).astype(np.float32), topk)
+    H, I, W = (torch.from_numpy(a).cuda() for a in (h, idx, w))
+
+    def host_layers():
+        for i, seed in enumerate(seeds):
+            torch.cuda.synchronize()  # every earlier copy out of this ring slot has completed
+            _random_layer_into(scratch, seed)
+            host = ring[i % 2]
+            for src, dst in zip(scratch.tensors(), host.tensors):
+                dst.copy_(src)
+            print(f"[config5] host slot {i % 2} <- layer {i} (seed {seed})", flush=True)
+            yield host
+
+    n_seen = 0
+    for i, layer in streamer.stream(host_layers()):
+        out = k.routed_forward(H, I, W, layer)
+        if i == 0:  # the ring slot still holds layer 0's bytes: check the whole layer on the CPU
+            torch.cuda.synchronize()
+            ex = oracle.ExpertSet(*[t.numpy() for t in ring[0].tensors])
+            assert_close(out.cpu().numpy(), clib.moe_forward(h, idx, w, ex), "config5 layer 0 vs C oracle")
+        twin = k.routed_forward(H, I, W, _random_layer_into(scratch, seeds[i]))
+        assert torch.equal(out, twin), f"streamed layer {i} differs from its resident twin"
+        print(f"[config5] layer {i}: streamed forward == resident forward", flush=True)
+        n_seen += 1
+    assert n_seen == n_layers
+    ms, nbytes = streamer.copy_stats()
+    assert nbytes == n_layers * ring[0].nbytes
+    print(f"[config5] H2D {nbytes / 1e9:.2f} GB in {ms:.0f} ms of copy time ({nbytes / ms / 1e6:.1f} GB/s)")
+    del streamer, scratch, ring
+    torch.cuda.empty_cache()

@@ -111,6 +111,32 @@ def test_router_select_ties_and_bias_only_in_selection():
     assert idx.tolist() == [[5, 0]] and np.allclose(w, 0.5)
 
 
+def test_router_select_nan_ranks_first_like_torch_topk():
+    """torch.topk, which KimiK3MoERouter.forward calls (moe_router.py:90), ranks NaN above every
+    number. The oracle does the same: the NaN experts of a row come first (torch leaves their
+    mutual order, and which of them it keeps when there are more than k, unspecified; the
+    oracle takes the lowest ids), then the rest by value, exactly as torch orders them."""
+    import torch
+    rng = np.random.default_rng(11)
+    N, E, top_k = 300, 37, 6
+    logits = rng.normal(size=(N, E))
+    logits[rng.random(logits.shape) < 0.08] = np.nan
+    bias = 0.1 * rng.normal(size=E)
+    idx, w = oracle.router_select(logits, bias, top_k)
+    choice = torch.sigmoid(torch.from_numpy(logits)) + torch.from_numpy(bias)
+    ti = torch.topk(choice, top_k, dim=-1, sorted=True).indices.numpy()
+    nan_rows = 0
+    for r in range(N):
+        nan_ids = np.flatnonzero(np.isnan(choice[r].numpy()))
+        m = min(len(nan_ids), top_k)
+        nan_rows += m > 0
+        assert set(idx[r, :m]) <= set(nan_ids) and set(ti[r, :m]) <= set(nan_ids), r
+        assert idx[r, :m].tolist() == sorted(nan_ids)[:m]
+        assert idx[r, m:].tolist() == ti[r, m:].tolist(), r
+    assert nan_rows > N // 2
+    assert ((0 <= idx) & (idx < E)).all()
+
+
 def moe_params(fx):
     return {k: (arr(v) if isinstance(v, dict) else v) for k, v in fx.items()}
 
