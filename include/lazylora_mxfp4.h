@@ -13,7 +13,7 @@
  *   noted. Every call is asynchronous on `stream` (0 = the null stream).
  *
  * Alignment (checked; a violation returns MXFP4_EINVAL and launches nothing): packed weights
- * and scales 16 bytes (mxfp4_dequant takes any alignment); mxfp4_gemm's x 8 bytes; mxfp4_gemm_t's dy 4 bytes; the routed layer's
+ * and scales 16 bytes (mxfp4_dequant takes any alignment); mxfp4_gemm's x 8 bytes; mxfp4_gemm_t's dy 4 bytes and y 16 bytes; the routed layer's
  * h 8 bytes (fp32) or 4 bytes (bf16), 16 bytes with LoRA, as are grad_out and the LoRA
  * factors then. Buffers from hipMalloc or torch satisfy all of these.
  *

@@ -14,6 +14,11 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblazylora_mxfp4.so")
 SOURCES = ["capi.hip", "mx_forward.hip", "mx_backward.hip", "mx_misc.hip", "mx_router.hip", "mx_lora.hip"]
 
+# per-file flags: the transposed products keep their accumulators in VGPRs (the MFMA's VGPR
+# form); with the default heuristics the compiler splits them over AGPRs and VGPRs and shuffles
+# them with v_accvgpr moves inside the main loop
+FILE_FLAGS = {"mx_backward.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [
@@ -45,7 +50,8 @@ def build(verbose: bool = False) -> str:
     jobs = []
     for src in SOURCES:
         obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
-        jobs.append(([HIPCC] + compile_flags + ["-c", os.path.join(CSRC, src), "-o", obj], obj))
+        jobs.append(([HIPCC] + compile_flags + FILE_FLAGS.get(src, []) + ["-c", os.path.join(CSRC, src), "-o", obj],
+                     obj))
     if verbose:
         for cmd, _ in jobs:
             print(" ".join(cmd), flush=True)

@@ -369,6 +369,7 @@ int mxfp4_gemm_t(float* y, const float* dy, const uint8_t* packed, const uint8_t
   if (!y || !dy || !packed || !scales) return fail(MXFP4_EINVAL, "gemm_t: null pointer%s");
   if (!aligned16(packed) || !aligned16(scales)) return fail(MXFP4_EINVAL, "gemm_t: packed and scales must be 16-byte aligned%s");
   if (((uintptr_t)dy & 3) != 0) return fail(MXFP4_EINVAL, "gemm_t: dy must be 4-byte aligned%s");
+  if (!aligned16(y)) return fail(MXFP4_EINVAL, "gemm_t: y must be 16-byte aligned%s");
   const size_t need = mxfp4_gemm_t_workspace_size(M, K, R);
   if (!workspace || workspace_bytes < need) return fail(MXFP4_EWORKSPACE, "gemm_t: workspace too small%s");
   const long long rp = pad32(R);

@@ -1,53 +1,43 @@
-// Transposed MXFP4 products y[m, c] = sum_r A[m, r] W[r, c] (gfx950).
+// Transposed MXFP4 products y[m, c] = sum_r A[m, r] W[r, c] (gfx950), decoded in registers.
 //
 // The contraction runs over W's rows, the strided direction of the packed layout, and the
-// E8M0 scales group W along its columns, so the scaled MFMA cannot consume W directly here.
-// Each step a work-group (256 threads) cooperatively loads a 32-row x 512-column slab of W
-// (every thread two 16-byte MX blocks = 2 x 32 columns of one row), decodes it with
-// v_cvt_scalef32_pk_bf16_fp4 (bit-exact: e2m1 * 2^(s-127) is exact in bf16), and writes it
-// row-major (padded, see slab_off) into LDS. Each wave then owns 128 output columns and pulls
-// its B operands with ds_read_b64_tr_b16, which hands lane i of a 16-lane group column i of
-// four consecutive rows. A (activation gradients) is split into bf16 hi + lo terms, so the
-// products carry ~16 significant bits of the activation against the exact weights. The slab
-// is double-buffered (2 x 32 KiB, XOR-swizzled instead of padded, so two work-groups fit per
-// CU): one barrier per step.
+// E8M0 scales group W along its columns, so the scaled MFMA cannot consume W directly here:
+// each bf16 MFMA (v_mfma_f32_16x16x32_bf16) lane needs 8 consecutive rows of ONE column. A
+// wave owns a 256-column stripe over all rows and builds those operands in registers, with no
+// LDS round trip:
 //
-// 512 columns per work-group: the E8M0 scales of one W row sit in the same 128-byte lines
-// for all column tiles, and every work-group that reads a line only for its own 16 bytes
-// costs a fetch of the whole line; wider tiles cut those fetches in half.
+//  * lane (n = l % 16, g = l / 16) loads, every 32-row step, 8 bytes of each of rows 8g..8g+7:
+//    columns 16n..16n+15 of the stripe (half an MX block), plus the 8 rows' scale bytes. The 16
+//    lanes of a row group read 128 contiguous bytes of a row;
+//  * byte p of a row holds columns 2p and 2p+1; v_cvt_scalef32_pk_bf16_fp4 turns it into those
+//    two bf16 values, exactly (e2m1 * 2^(s-127) is exact in bf16), and v_perm_b32 gathers the
+//    8 rows' column-2p halves into one B operand and their column-2p+1 halves into another;
+//  * so MFMA t (t = 0..15) of a step computes output columns {16n + t : n = 0..15} of the
+//    stripe, and a lane's accumulators end up holding 16 CONTIGUOUS columns (4 rows each), which
+//    the epilogue writes as whole 64-byte runs.
+// A (activation gradients) is split into bf16 hi + lo terms, so the products carry ~16
+// significant bits of the activation against the exact weights; fp32 accumulation.
 //
-// The whole contraction range (nseg * R rows) stays in one work-group, so every output
-// element has exactly one writer and the sum order is fixed: results are deterministic.
+// Per 4 KiB of weights a wave spends 64 decodes + 64 permutes (VALU) and 32 MFMAs. The four
+// waves of a work-group take four neighbouring stripes of one row tile and share its A operands:
+// the work-group copies them into LDS (global_load_lds, 16 steps at a time, double-buffered),
+// so A costs one read per 1024 columns instead of one per 256, and one barrier per 16 steps.
+// Large buckets (experts with many 16-row tiles) take items of T row tiles, which reuse every
+// decoded operand for all T tiles.
+//
+// The whole contraction range (nseg * R rows) stays in one wave, so every output element has
+// exactly one writer and the sum order is fixed: results are deterministic.
 #include "mx_device.h"
 #include "mx_kernels.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mx {
 
 namespace {
 
-constexpr int kSlabRows = 32;
-constexpr int kRowBytes = kBwdColsPerTile * 2;     // 1 KiB of bf16 per slab row, no padding
-constexpr int kSlabBytes = kSlabRows * kRowBytes;  // 32 KiB; two of them per work-group
-
-// LDS slab layout. LDS has 32 banks of 4 bytes; a ds_write_b128 is served 8 lanes per cycle
-// and a ds_read_b64_tr_b16 16 lanes per cycle (both measured on the hardware). A row is 128
-// "quads" of 4 bf16 (8 bytes); quad q of row r is stored at position
-//   q ^ (((q >> 4) & 3) << 1) ^ ((r & 3) << 2),
-// which only permutes bits 1-3 of q: aligned quad pairs stay together (16-byte writes stay
-// contiguous) and every quad stays in its aligned group of 16. The 8 lanes of a write phase
-// (one row, blocks lc = 0..7, same piece) then cover all 32 banks, and so do the 16 lanes of a
-// transposed-read phase (4 consecutive rows x 4 quads).
-__device__ __forceinline__ int quad_pos(int row, int q)
-{
-  return q ^ (((q >> 4) & 3) << 1) ^ ((row & 3) << 2);
-}
-__device__ __forceinline__ int slab_off(int row, int q)  // byte offset of quad q of row
-{
-  return row * kRowBytes + quad_pos(row, q) * 8;
-}
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+constexpr int kStepRows = 32;
 typedef const __attribute__((address_space(4))) int* cint_ptr;
 
 #ifndef MX_BWD_GROUP_T
@@ -55,17 +45,21 @@ typedef const __attribute__((address_space(4))) int* cint_ptr;
 #endif
 constexpr int kBwdGroupT = MX_BWD_GROUP_T;  // row tiles per large-bucket work item (2 or 4)
 
-// One work item: column tile ct of up to T row tiles of one expert (T = 1: a small-bucket tile;
-// T = kGroupTiles: a large-bucket group, whose tiles share every decoded slab).
+constexpr int kWaves = 4;  // waves (stripes) per work-group
+
+// One work item: the kWaves stripes from kWaves * ct4 on of up to T row tiles of one expert
+// (T = 1: a small-bucket tile; T > 1: part of a large-bucket group, whose tiles share every
+// decoded operand).
 template <int T>
 struct WorkItem {
-  int expert, ct, ntl;
-  int row0[T], nrows[T], tile[T];
+  int expert, ct4, ntl;
+  int row0[T], nrows[T];
 };
 
-// Work item `it` of this work-group (items are dealt round-robin over the XCDs, blockIdx % 8,
-// each XCD taking one contiguous run, in strides of the grid). Returns 0 when there is none
-// left, 2 for an empty part of a short group, 1 for an item.
+// Work item `it` of this wave (items are dealt round-robin over the XCDs, blockIdx % 8, each
+// XCD taking one contiguous run, in strides of the grid, so the stripes of one tile, which read
+// the same A rows, run on one XCD). Returns 0 when there is none left, 2 for an empty part of a
+// short group, 1 for an item.
 template <int T>
 __device__ __forceinline__ int decode_work(const BwdArgs& a, int it, WorkItem<T>& w)
 {
@@ -77,13 +71,14 @@ __device__ __forceinline__ int decode_work(const BwdArgs& a, int it, WorkItem<T>
   if (T == 1) count = use_small ? *(cint_ptr)a.n_small
                                 : a.tiles ? *(cint_ptr)a.n_tiles : (a.M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
   else count = *(cint_ptr)a.n_groups * kParts;
-  const int total = count * a.n_ct;
+  const int n_ct4 = (a.n_ct + kWaves - 1) / kWaves;
+  const int total = count * n_ct4;
   const int per_xcd = (total + 7) >> 3;
   const int slot = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
   const int item = (int)(blockIdx.x & 7) * per_xcd + slot;
   if (slot >= per_xcd || item >= total) return 0;
-  const int i = item / a.n_ct;
-  w.ct = item - i * a.n_ct;
+  const int i = item / n_ct4;
+  w.ct4 = item - i * n_ct4;
   int t0;
   if (T == 1) {
     t0 = use_small ? ((cint_ptr)a.small_tiles)[i] : i;
@@ -98,7 +93,6 @@ __device__ __forceinline__ int decode_work(const BwdArgs& a, int it, WorkItem<T>
 #pragma unroll
   for (int tt = 0; tt < T; ++tt) {
     const int t = t0 + (tt < w.ntl ? tt : 0);
-    w.tile[tt] = t;
     if (a.tiles) {
       const cint_ptr tl = (cint_ptr)(a.tiles + t);
       w.expert = tl[0];
@@ -113,314 +107,320 @@ __device__ __forceinline__ int decode_work(const BwdArgs& a, int it, WorkItem<T>
   return 1;
 }
 
-// 16 fp4 bytes (32 codes of one row) -> 32 bf16 in 16 dwords, scale byte s applied exactly;
-// s >= 253 gives zeros.
-__device__ __forceinline__ void decode_block_bf16(const i32x4& raw, uint32_t s, uint32_t (&out)[16])
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 8 bytes, streaming (non-temporal): weight bytes are read exactly once per wave, and the 16
+// lanes of a row group consume whole 128-byte lines
+MX_DEV u32x2 buf8B_nt(rsrc_t r, uint32_t off)
 {
-  const bool dead = s >= 253u;
-  const float scale = bits_f((dead ? 127u : s) << 23);
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 2));
+}
+
+// One step's weights for one lane: 8 rows x 8 bytes, and the 8 rows' scale bytes.
+struct StepRaw {
+  u32x2 w[8];
+  uint32_t s[8];
+};
+
+// B operands of MFMAs 2P and 2P+1 from byte P of the lane's 8 rows
+template <int P>
+MX_DEV void decode_pair(const StepRaw& r, const float (&sf)[8], bf16x8& b0, bf16x8& b1)
+{
+  uint32_t d[8];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const uint32_t word = dead ? 0u : (uint32_t)raw[d];
-    out[4 * d + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0));
-    out[4 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1));
-    out[4 * d + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2));
-    out[4 * d + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3));
+  for (int q = 0; q < 8; ++q)
+    d[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(r.w[q][P >> 2], sf[q], P & 3));
+  // d[q] = (column 2p | column 2p+1 << 16) of row q; B wants rows (2m, 2m+1) of one column
+  uint32_t e[4], o[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    e[m] = __builtin_amdgcn_perm(d[2 * m + 1], d[2 * m], 0x05040100u);
+    o[m] = __builtin_amdgcn_perm(d[2 * m + 1], d[2 * m], 0x07060302u);
+  }
+  b0 = __builtin_bit_cast(bf16x8, i32x4{(int)e[0], (int)e[1], (int)e[2], (int)e[3]});
+  b1 = __builtin_bit_cast(bf16x8, i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]});
+}
+
+// f(integral_constant<int, i>) for i = 0 .. N-1
+template <int N, int I = 0, typename Fn>
+MX_DEV void static_for(Fn&& f)
+{
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
   }
 }
 
-// Decoded block blk (32 columns = quads 8 blk .. 8 blk + 7) of a slab row: four 16-byte writes.
-__device__ __forceinline__ void store_block(uint8_t* slab, int row, int blk, const i32x4& raw, uint32_t s)
-{
-  uint32_t dec[16];
-  decode_block_bf16(raw, s, dec);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    *reinterpret_cast<i32x4*>(slab + slab_off(row, blk * 8 + 2 * j)) =
-        i32x4{(int)dec[4 * j], (int)dec[4 * j + 1], (int)dec[4 * j + 2], (int)dec[4 * j + 3]};
-}
+// Ring depth (steps of weights in flight per wave, each 4 KiB per wave) and A chunk (steps whose
+// A operands one LDS buffer holds: kChunk x T tiles x 2 terms x 1 KiB). T > 1 items do T times
+// the matrix work per step, so a shorter ring hides the loads. kChunk is a multiple of kRing.
+#ifndef MX_BWD_RING
+#define MX_BWD_RING 4
+#endif
+template <int T>
+struct Cfg {
+  static constexpr int kRing = T == 1 ? MX_BWD_RING : 2;
+  static constexpr int kChunk = 16 / T;
+  static constexpr int kChunkBytes = kChunk * T * 2 * 1024;
+};
 
-// T = 1: weight steps in flight per work-group kPrefetch = 8, two work-groups per CU. T > 1:
-// T times the matrix work per step, so a shorter ring hides the loads; T = 2 still fits two
-// work-groups per CU, T = 4 needs the whole register file (one per CU).
-//
-// Step s of the main loop, after the barrier that publishes slab s: every wave issues all of
-// its transposed reads of slab s at once, then the loads that refill the rings, then decodes
-// step s + 1 into the other slab buffer in two halves, each followed by half of slab s's
-// MFMAs. The decode's VALU work and LDS writes thus overlap the matrix work and the read
-// latency is paid once per step. The other buffer held slab s - 1, whose reads every wave
-// finished (its MFMAs consumed them) before arriving at this step's barrier.
 template <int MODE, int T>
-__device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w)
+__device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w, uint8_t* abuf)
 {
-  constexpr int kPrefetch = T == 1 ? 8 : 4;  // even
-  __shared__ __attribute__((aligned(16))) uint8_t slab[2][kSlabBytes];
-  __shared__ float dotred[4][16];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int li = lane & 15, g = lane >> 4;
-  const int c0 = w.ct * kBwdColsPerTile;
+  constexpr int kRing = Cfg<T>::kRing;
+  constexpr int kChunk = Cfg<T>::kChunk;
+  constexpr int kChunkBytes = Cfg<T>::kChunkBytes;
+  static_assert(kChunk % kRing == 0, "a ring pass never straddles an A chunk");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int ct = w.ct4 * kWaves + wave;  // this wave's stripe
+  const bool stripe_ok = ct < a.n_ct;    // uniform: stripes past C only help with the A copies
+  const int c0 = ct * kBwdColsPerTile;
   const int rtot = a.nseg * a.R;
-  const int nsteps = (rtot + kSlabRows - 1) / kSlabRows;
-  // the ring below is unrolled kPrefetch-fold; padding steps read past the matrix (zeros)
-  const int nsteps_pad = (nsteps + kPrefetch - 1) / kPrefetch * kPrefetch;
+  const int nsteps = (rtot + kStepRows - 1) / kStepRows;
+  // whole A chunks; padding steps read past the matrix (zeros)
+  const int nsteps_pad = (nsteps + kChunk - 1) / kChunk * kChunk;
 
-  // loader role: MX blocks lc and lc + 8 of slab row lr per step, so each load instruction
-  // of a wave reads whole 128-byte lines (8 rows x 8 blocks). Block lc + 8 sits 128 bytes
-  // (8 scale bytes) after block lc.
-  const int lr = tid >> 3;
-  const int lc = tid & 7;
   const uint32_t cbs = a.C / kGroup;  // scale bytes per W row
   const uint32_t wpitch = a.C / 2;
-  const int colA = c0 + lc * 32;
-  const int colA_c = colA < a.C ? colA : 0;
-  // Each segment of this expert is one buffer resource: rows at or past the segment's end
-  // (the tail of a row count that is not a multiple of kSlabRows, and the padding steps) read
-  // as zero weights. Segments hold a multiple of kSlabRows rows whenever there are two, so a
-  // step never straddles them. Columns past C (lanes clamped to column 0, or block lc + 8 of a
-  // partial tile) read other finite weights that no stored column uses.
-  const uint8_t* const wp0 = a.wp0 + (long long)w.expert * a.wp_estride;
-  const uint8_t* const wp1 = a.wp1 + (long long)w.expert * a.wp_estride;
-  const uint8_t* const ws0 = a.ws0 + (long long)w.expert * a.ws_estride;
-  const uint8_t* const ws1 = a.ws1 + (long long)w.expert * a.ws_estride;
-  const rsrc_t rw0 = make_rsrc(wp0, (uint32_t)a.R * wpitch), rw1 = make_rsrc(wp1, (uint32_t)a.R * wpitch);
-  const rsrc_t rs0_ = make_rsrc(ws0, (uint32_t)a.R * cbs), rs1_ = make_rsrc(ws1, (uint32_t)a.R * cbs);
-  const uint32_t lane_w = (uint32_t)lr * wpitch + colA_c / 2;
-  const uint32_t lane_s = (uint32_t)lr * cbs + colA_c / kGroup;
+  // this lane's 16 columns; a stripe may end past C (small C): such lanes read column 0's
+  // bytes, finite weights whose products are never stored
+  const int col = c0 + 16 * n;
+  const int col_c = col < a.C ? col : 0;
+  // Each segment of this expert is one buffer resource: rows at or past the segment's end (the
+  // tail of a row count that is not a multiple of kStepRows, and the padding steps) read as
+  // zero weights. Segments hold a multiple of kStepRows rows whenever there are two, so a step
+  // never straddles them. A stripe past C gets empty resources: zeros, no memory traffic.
+  const uint32_t wbytes = stripe_ok ? (uint32_t)a.R * wpitch : 0u, sbytes = stripe_ok ? (uint32_t)a.R * cbs : 0u;
+  const rsrc_t rw0 = make_rsrc(a.wp0 + (long long)w.expert * a.wp_estride, wbytes);
+  const rsrc_t rs0 = make_rsrc(a.ws0 + (long long)w.expert * a.ws_estride, sbytes);
+  const rsrc_t rw1 = a.nseg > 1 ? make_rsrc(a.wp1 + (long long)w.expert * a.wp_estride, wbytes) : rw0;
+  const rsrc_t rs1 = a.nseg > 1 ? make_rsrc(a.ws1 + (long long)w.expert * a.ws_estride, sbytes) : rs0;
+  const uint32_t lane_w = (uint32_t)(8 * g) * wpitch + (uint32_t)col_c / 2;
+  const uint32_t lane_s = (uint32_t)(8 * g) * cbs + (uint32_t)col_c / kGroup;
 
-  // Weight bytes are read exactly once per work-group: streaming loads.
-  auto load_raw = [&](int step, i32x4& r0, i32x4& r1, uint8_t& s0, uint8_t& s1) {
-    const int row0 = step * kSlabRows;
+  auto load_step = [&](int step, StepRaw& r) {
+    const int row0 = step * kStepRows;
     const bool seg = a.nseg > 1 && row0 >= a.R;  // uniform
     const uint32_t rr = (uint32_t)(seg ? row0 - a.R : row0);
     const rsrc_t W = seg ? rw1 : rw0;
-    const rsrc_t S = seg ? rs1_ : rs0_;
-    const uint32_t ow = lane_w + rr * wpitch, os = lane_s + rr * cbs;
-    r0 = buf16_nt(W, ow);
-    r1 = buf16_nt(W, ow + 128);
-    s0 = buf8(S, os);
-    s1 = buf8(S, os + 8);
+    const rsrc_t S = seg ? rs1 : rs0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) r.w[q] = buf8B_nt(W, lane_w + (rr + q) * wpitch);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) r.s[q] = buf8(S, lane_s + (rr + q) * cbs);
   };
 
-  // A operands. A step's A tile (T tiles x hi/lo x 16 rows x 32 bf16 = 2T KiB) is loaded
-  // once per work-group, each thread its 8T bytes two steps ahead, and shared through a
-  // double-buffered LDS copy written one step ahead; every wave reads its MFMA operands from
-  // there (four waves loading the same operands from L2 would move as many bytes as the
-  // weights). Copy layout: [tile][term][row][four 16-byte K chunks], chunk c of row r at
-  // position c ^ ((r >> 1) & 3), so the 8 rows of a ds_read_b128 phase cover all banks.
-  // Rows past a tile's end repeat its last row (never stored). Padding steps meet zero
-  // weights, so their A (the last real step's, reloaded) adds zero.
-  __shared__ __attribute__((aligned(16))) uint8_t abuf[2][T * 2048];
-  constexpr int kABytes = 8 * T;  // per thread and step
-  typedef int av_t __attribute__((ext_vector_type(2 * T)));
-  const uint16_t* pa;
-  int a_dst;
-  {
-    const int b0 = tid * kABytes;
-    const int tt = b0 >> 11, term = (b0 >> 10) & 1, row = (b0 >> 6) & 15, kb = b0 & 63;
-    int r0 = w.row0[0], nr = w.nrows[0];  // tile tt's (selected, not indexed: no stack copy)
+  // A operands: MFMA lane (i = n, g) takes elements 8g..8g+7 of the step's 32 contraction
+  // indices of row i of each tile, hi and lo terms (16 bytes each). The work-group copies them
+  // into abuf chunk by chunk: unit u = (step in chunk, tile, term) is 1 KiB, lane l's operand at
+  // 16 l, exactly as a ds_read_b128 of the MFMA lanes wants it; wave w copies units w, w + 4, ...
+  // Rows past a tile's end repeat its last row (never stored). Padding steps meet zero weights,
+  // so their A (the last real step's, copied again) adds zero.
+  const uint16_t* pa[T][2];
 #pragma unroll
-    for (int i = 1; i < T; ++i)
-      if (tt == i) r0 = w.row0[i], nr = w.nrows[i];
-    const int ri = r0 + min(row, nr - 1);
-    const int arow = a.a_row_map ? a.a_row_map[ri] : ri;
-    pa = (term ? a.a_lo : a.a_hi) + (long long)arow * a.lda + (kb >> 1);
-    a_dst = (b0 & ~63) + ((((kb >> 4) ^ (row >> 1)) & 3) << 4) + (kb & 15);
+  for (int tt = 0; tt < T; ++tt) {
+    const int ri = w.row0[tt] + min(n, w.nrows[tt] - 1);
+    const long long arow = a.a_row_map ? a.a_row_map[ri] : ri;
+    pa[tt][0] = a.a_hi + arow * a.lda + 8 * g;
+    pa[tt][1] = a.a_lo + arow * a.lda + 8 * g;
   }
-  auto load_a = [&](int step) { return *reinterpret_cast<const av_t*>(pa + min(step, nsteps - 1) * kSlabRows); };
-  // T <= 2: the thread's bytes lie in one 16-byte chunk. T = 4: they are two whole chunks
-  // (kb = 0 or 32), each stored at its own swizzled position.
-  auto store_a = [&](uint8_t* buf, const av_t& v) {
-    if constexpr (kABytes <= 16) {
-      *reinterpret_cast<av_t*>(buf + a_dst) = v;
-    } else {
-      static_assert(kABytes == 32, "T is 1, 2 or 4");
-      const int b0 = tid * kABytes, row = (b0 >> 6) & 15, c0 = (b0 & 63) >> 4;
+  // The copies are issued from inline assembly (the compiler does not see them, so it does not
+  // drain every load in flight at each barrier); each chunk is waited for explicitly.
+  auto copy_chunk = [&](int chunk) {
+    uint8_t* dst = abuf + (chunk & 1) * kChunkBytes;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        *reinterpret_cast<i32x4*>(buf + (b0 & ~63) + ((((c0 + h) ^ (row >> 1)) & 3) << 4)) =
-            i32x4{v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+    for (int k = 0; k < kChunk * T * 2 / kWaves; ++k) {
+      const int u = k * kWaves + wave;
+      const int si = u / (2 * T), tt = (u >> 1) % T, term = u & 1;
+      const int so = min(chunk * kChunk + si, nsteps - 1) * kStepRows;
+      // select tile tt's pointer without indexing (keeps pa in registers)
+      const uint16_t* src = pa[0][0];
+#pragma unroll
+      for (int t2 = 0; t2 < T; ++t2)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (tt == t2 && term == h) src = pa[t2][h];
+      dma16_async(src + so, dst + u * 1024);
     }
   };
-  const int a_src = li * 64 + (((g ^ (li >> 1)) & 3) << 4);  // this lane's operand chunk
 
-  f32x4 acc[T][8];
+  f32x4 acc[T][16];
 #pragma unroll
   for (int tt = 0; tt < T; ++tt)
 #pragma unroll
-    for (int cg = 0; cg < 8; ++cg) acc[tt][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 16; ++t) acc[tt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Pipeline: the raw blocks of the next kPrefetch steps are in flight in a register ring.
-  // Within a step the A load is issued before the ring refill.
-  i32x4 ring0[kPrefetch], ring1[kPrefetch];
-  uint8_t rs0[kPrefetch], rs1[kPrefetch];
-  // Issue order is pinned (A first, then the ring slot by slot) so the loop head can wait
-  // for slot 0 alone, whether it is entered from here or from the back edge.
-  av_t acur = load_a(0);
-  store_a(abuf[0], acur);
-  acur = load_a(1);
+  StepRaw ring[kRing];
+  // issue order is pinned (the first A chunk, then the ring slot by slot) so that each step
+  // waits for its own loads alone, whether it is entered from here or from the loop's back edge
+  copy_chunk(0);
 #pragma unroll
-  for (int p = 0; p < kPrefetch; ++p) {
+  for (int p = 0; p < kRing; ++p) {
     __builtin_amdgcn_sched_barrier(0);
-    load_raw(p, ring0[p], ring1[p], rs0[p], rs1[p]);
+    load_step(p, ring[p]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // slab 0 (and A copy 0 above); the previous item's last reads of these buffers ended before
-  // the caller's barrier
-  store_block(slab[0], lr, lc, ring0[0], rs0[0]);
-  store_block(slab[0], lr, lc + 8, ring1[0], rs1[0]);
 
-  for (int s0 = 0; s0 < nsteps_pad; s0 += kPrefetch) {
-#pragma unroll
-    for (int p = 0; p < kPrefetch; ++p) {
-      const int s = s0 + p;
-      const uint8_t* const sl = slab[p & 1];  // kPrefetch is even, so this is slab[s & 1]
-      uint8_t* const sn_buf = slab[(p + 1) & 1];
-      const uint8_t* const ab = abuf[p & 1];
-      uint8_t* const an_buf = abuf[(p + 1) & 1];
-      const int q = (p + 1) % kPrefetch;     // ring slot of step s + 1
-      __builtin_amdgcn_sched_barrier(0);
+  for (int s0 = 0; s0 < nsteps_pad; s0 += kRing) {
+    if (s0 % kChunk == 0) {  // uniform
+      // chunk c = s0 / kChunk was copied before the weights of steps s0 .. s0 + kRing - 1 were
+      // requested: with only those outstanding, this wave's part has landed; the barrier waits
+      // for the other waves' parts, and every wave has finished reading the buffer that chunk
+      // c + 1 now overwrites (it held chunk c - 1)
+      wait_vm<(kRing * 16 < 63 ? kRing * 16 : 63)>();  // (the counter holds at most 63)
       __syncthreads();
-      // B operands of this wave's 8 column groups: rows 8g..8g+7 of column cg*16 + li
-      bf16x8 b[8];
+      const int c = s0 / kChunk;
+      if ((c + 1) * kChunk < nsteps_pad) copy_chunk(c + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint8_t* ab = abuf + ((s0 / kChunk) & 1) * kChunkBytes + lane * 16;
 #pragma unroll
-      for (int cg = 0; cg < 8; ++cg) {
-        const int qd = wave * 32 + cg * 4 + (li & 3);
-        const i16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(&sl[slab_off(8 * g + (li >> 2), qd)]));
-        const i16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(&sl[slab_off(8 * g + 4 + (li >> 2), qd)]));
-        const short __attribute__((ext_vector_type(8))) bs = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
-        b[cg] = __builtin_bit_cast(bf16x8, bs);
-      }
-      i32x4 ahv[T], alv[T];
+    for (int p = 0; p < kRing; ++p) {
+      const int s = s0 + p;
+      const int si = s % kChunk;
+      StepRaw& r = ring[p];
+      // this step's A operands from the chunk in LDS
+      i32x4 ah[T], al[T];
 #pragma unroll
       for (int tt = 0; tt < T; ++tt) {
-        ahv[tt] = *reinterpret_cast<const i32x4*>(ab + tt * 2048 + a_src);
-        alv[tt] = *reinterpret_cast<const i32x4*>(ab + tt * 2048 + 1024 + a_src);
+        ah[tt] = *reinterpret_cast<const i32x4*>(ab + ((si * T + tt) * 2) * 1024);
+        al[tt] = *reinterpret_cast<const i32x4*>(ab + ((si * T + tt) * 2 + 1) * 1024);
       }
-      const av_t anext = load_a(s + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      load_raw(s + kPrefetch, ring0[p], ring1[p], rs0[p], rs1[p]);
-      __builtin_amdgcn_sched_barrier(0);
-      // The decode / MFMA half of the step runs at a raised wave priority: of the two waves on a
-      // SIMD, the one in this phase is issued first, so it finishes its step while the other
-      // waits at its barrier or on its transposed reads, and the two phases overlap instead of
-      // alternating in lockstep (2-3% faster than the default level; raising it over the reads
-      // instead, or over only the MFMAs or only the decode, is not).
-      __builtin_amdgcn_s_setprio(1);
+      // scales of this step's rows as E8M0 operands of the conversion; a scale byte >= 253
+      // makes its row contribute zero
+      float sf[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const bool dead = r.s[q] >= 253u;
+        r.w[q] = dead ? u32x2{0u, 0u} : r.w[q];
+        sf[q] = bits_f((dead ? 127u : r.s[q]) << 23);
+      }
 
-      // two halves: decode half h of step s + 1, then the MFMAs of column groups 4h..4h+3,
-      // the hi terms of each pair of groups (and of every tile) before their lo terms
+      // two byte positions (four MFMA column sets) at a time: the hi terms of the four, then
+      // their lo terms, so consecutive MFMAs never share an accumulator
+      auto bytes = [&](auto p2c) {
+        constexpr int p2 = decltype(p2c)::value;
+        bf16x8 b[4];
+        decode_pair<p2>(r, sf, b[0], b[1]);
+        decode_pair<p2 + 1>(r, sf, b[2], b[3]);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (h == 0) {
-          store_block(sn_buf, lr, lc, ring0[q], rs0[q]);
-          store_a(an_buf, acur);  // step s + 1's A
-        } else {
-          store_block(sn_buf, lr, lc + 8, ring1[q], rs1[q]);
-        }
+        for (int tt = 0; tt < T; ++tt)
+          if (tt < w.ntl)
 #pragma unroll
-        for (int cp = 4 * h; cp < 4 * h + 4; cp += 2) {
+            for (int j = 0; j < 4; ++j)
+              acc[tt][2 * p2 + j] = mfma_bf16(__builtin_bit_cast(bf16x8, ah[tt]), b[j], acc[tt][2 * p2 + j]);
 #pragma unroll
-          for (int e = 0; e < 2; ++e)
+        for (int tt = 0; tt < T; ++tt)
+          if (tt < w.ntl)
 #pragma unroll
-            for (int tt = 0; tt < T; ++tt)
-              if (tt < w.ntl) acc[tt][cp + e] = mfma_bf16(__builtin_bit_cast(bf16x8, ahv[tt]), b[cp + e], acc[tt][cp + e]);
-#pragma unroll
-          for (int e = 0; e < 2; ++e)
-#pragma unroll
-            for (int tt = 0; tt < T; ++tt)
-              if (tt < w.ntl) acc[tt][cp + e] = mfma_bf16(__builtin_bit_cast(bf16x8, alv[tt]), b[cp + e], acc[tt][cp + e]);
-        }
-      }
-      __builtin_amdgcn_s_setprio(0);
-      acur = anext;
+            for (int j = 0; j < 4; ++j)
+              acc[tt][2 * p2 + j] = mfma_bf16(__builtin_bit_cast(bf16x8, al[tt]), b[j], acc[tt][2 * p2 + j]);
+      };
+      bytes(std::integral_constant<int, 0>{});
+      bytes(std::integral_constant<int, 2>{});
+      bytes(std::integral_constant<int, 4>{});
+      bytes(std::integral_constant<int, 6>{});
+      __builtin_amdgcn_sched_barrier(0);
+      load_step(s + kRing, ring[p]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // epilogue, tile by tile: lane (li, g) holds rows 4g..4g+3 of column c0 + wave*128 + cg*16 + li
-  // (conditionals rather than break / continue, so the loop unrolls and acc stays in registers)
-#pragma unroll
-  for (int tt = 0; tt < T; ++tt) {
+  // epilogue, tile by tile: lane (n, g) holds rows 4g..4g+3 of columns col .. col + 15 (the
+  // tile index is a compile-time constant in each call, so acc is only ever indexed statically
+  // and stays in registers)
+  const bool col_ok = stripe_ok && col < a.C;  // C is a multiple of 32: all 16 columns or none
+  auto epilogue = [&](auto ttc) {
+    constexpr int tt = decltype(ttc)::value;
     const bool live = tt < w.ntl;  // uniform
-    const int row0 = w.row0[tt], nrows = w.nrows[tt];
+    const int row0 = w.row0[tt], nrows = live ? w.nrows[tt] : 0;
     if (MODE == kBwdDownT) {
       const int F = a.C;
-      float dots[4] = {0.f, 0.f, 0.f, 0.f};
-      if (live) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int i = 4 * g + v;
-          const bool row_ok = i < nrows;
-          const int p = row0 + (row_ok ? i : 0);
-          const float tw = a.row_w[p];
-          const float* sv = a.saved + (long long)p * 2 * F;
-          // LoRA: the down adapter's A_d^T q of the row's token joins g . W2
-          const float* rq = a.lora_rq ? a.lora_rq + (long long)a.a_row_map[p] * F : nullptr;
-#pragma unroll
-          for (int cg = 0; cg < 8; ++cg) {
-            const int f = c0 + wave * 128 + cg * 16 + li;
-            if (f < F) {
-              const float h = rq ? acc[tt][cg][v] + rq[f] : acc[tt][cg][v];
-              const float gt = sv[f], up = sv[F + f];
-              dots[v] += glu_fwd(gt, up, a.act_kind) * h;
-              float dg, du;
-              glu_bwd(tw * h, gt, up, a.act_kind, dg, du);
-              if (row_ok) {
-                const long long o = (long long)p * 2 * F + f;
-                const __bf16 dgh = (__bf16)dg, duh = (__bf16)du;
-                a.d_hi[o] = __builtin_bit_cast(uint16_t, dgh);
-                a.d_lo[o] = __builtin_bit_cast(uint16_t, (__bf16)(dg - (float)dgh));
-                a.d_hi[o + F] = __builtin_bit_cast(uint16_t, duh);
-                a.d_lo[o + F] = __builtin_bit_cast(uint16_t, (__bf16)(du - (float)duh));
-              }
-            }
-          }
-        }
-      }
-      if (live) {
-        if (tt > 0) __syncthreads();  // the previous tile's partial dots have been read
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float d = group16_sum(dots[v]);
-          if (li == 0) dotred[wave][4 * g + v] = d;
-        }
-        __syncthreads();
-        if (tid < 16 && tid < nrows) {
-          const float d = dotred[0][tid] + dotred[1][tid] + dotred[2][tid] + dotred[3][tid];
-          a.gw_part[(long long)(row0 + tid) * a.n_ct + w.ct] = d;
-        }
-      }
-    } else if (live) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = 4 * g + v;
-        if (i < nrows) {
-          float* yr = a.y + (long long)(row0 + i) * a.ldy;
+        const bool row_ok = i < nrows;
+        const int p = row0 + (row_ok ? i : 0);
+        float dot = 0.f;
+        if (col_ok) {
+          const float tw = a.row_w[p];
+          const float* sv = a.saved + (long long)p * 2 * F + col;
+          // LoRA: the down adapter's A_d^T q of the row's token joins g . W2
+          const float* rq = a.lora_rq ? a.lora_rq + (long long)a.a_row_map[p] * F + col : nullptr;
+          uint32_t dh[8], dl[8], uh[8], ul[8];
 #pragma unroll
-          for (int cg = 0; cg < 8; ++cg) {
-            const int col = c0 + wave * 128 + cg * 16 + li;
-            if (col < a.C) {
-              if (a.accumulate) yr[col] += acc[tt][cg][v];
-              else yr[col] = acc[tt][cg][v];
+          for (int c4 = 0; c4 < 4; ++c4) {
+            const f32x4 gt4 = *reinterpret_cast<const f32x4*>(sv + 4 * c4);
+            const f32x4 up4 = *reinterpret_cast<const f32x4*>(sv + F + 4 * c4);
+            f32x4 rq4 = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (rq) rq4 = *reinterpret_cast<const f32x4*>(rq + 4 * c4);
+            float dg[4], du[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float h = acc[tt][4 * c4 + e][v] + rq4[e];
+              dot += glu_fwd(gt4[e], up4[e], a.act_kind) * h;
+              glu_bwd(tw * h, gt4[e], up4[e], a.act_kind, dg[e], du[e]);
             }
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+              const uint32_t gh = pack_bf16(dg[e], dg[e + 1]);
+              const uint32_t hh = pack_bf16(du[e], du[e + 1]);
+              dh[2 * c4 + e / 2] = gh;
+              dl[2 * c4 + e / 2] = pack_bf16(dg[e] - bf16_lo(gh), dg[e + 1] - bf16_hi(gh));
+              uh[2 * c4 + e / 2] = hh;
+              ul[2 * c4 + e / 2] = pack_bf16(du[e] - bf16_lo(hh), du[e + 1] - bf16_hi(hh));
+            }
+          }
+          if (row_ok) {
+            const long long o = (long long)p * 2 * F + col;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int b = 4 * h2;
+              *reinterpret_cast<i32x4*>(a.d_hi + o + 8 * h2) = i32x4{(int)dh[b], (int)dh[b + 1], (int)dh[b + 2], (int)dh[b + 3]};
+              *reinterpret_cast<i32x4*>(a.d_lo + o + 8 * h2) = i32x4{(int)dl[b], (int)dl[b + 1], (int)dl[b + 2], (int)dl[b + 3]};
+              *reinterpret_cast<i32x4*>(a.d_hi + o + F + 8 * h2) = i32x4{(int)uh[b], (int)uh[b + 1], (int)uh[b + 2], (int)uh[b + 3]};
+              *reinterpret_cast<i32x4*>(a.d_lo + o + F + 8 * h2) = i32x4{(int)ul[b], (int)ul[b + 1], (int)ul[b + 2], (int)ul[b + 3]};
+            }
+          }
+        }
+        // this stripe's part of grad_w = <act, h> for the row: the 16 lanes of the row group
+        const float d = group16_sum(dot);
+        if (n == 0 && row_ok && stripe_ok) a.gw_part[(long long)(row0 + i) * a.n_ct + ct] = d;
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = 4 * g + v;
+        if (i < nrows && col_ok) {
+          float* yr = a.y + (long long)(row0 + i) * a.ldy + col;
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) {
+            f32x4 o = f32x4{acc[tt][4 * c4][v], acc[tt][4 * c4 + 1][v], acc[tt][4 * c4 + 2][v], acc[tt][4 * c4 + 3][v]};
+            if (a.accumulate) o += *reinterpret_cast<const f32x4*>(yr + 4 * c4);
+            *reinterpret_cast<f32x4*>(yr + 4 * c4) = o;
           }
         }
       }
     }
-  }
+  };
+  static_for<T>(epilogue);
 }
 
-// T = 1: one item per work-group (the grid covers every item). T > 1: a resident grid that
-// loops over the large-bucket items, so launches with few or no groups cost almost nothing.
+// One wave per work-group. T = 1: one item per wave (the grid covers every item). T > 1: a
+// resident grid that loops over the large-bucket items, so launches with few or no groups cost
+// almost nothing.
+// One work-group of kWaves waves per item. T = 1: one item per work-group (the grid covers every
+// item). T > 1: a resident grid that loops over the large-bucket items, so launches with few or
+// no groups cost almost nothing.
 template <int MODE, int T>
-__global__ __launch_bounds__(256, T <= 2 ? 2 : 1) void bwd_kernel(BwdArgs a)
+__global__ __launch_bounds__(64 * kWaves, T == 1 ? 2 : 1) void bwd_kernel(BwdArgs a)
 {
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * Cfg<T>::kChunkBytes];
   WorkItem<T> w;
   if constexpr (T == 1) {
-    if (decode_work<T>(a, 0, w) == 1) bwd_item<MODE, T>(a, w);
+    if (decode_work<T>(a, 0, w) == 1) bwd_item<MODE, T>(a, w, abuf);
     return;
   }
   bool busy = false;
@@ -428,8 +428,8 @@ __global__ __launch_bounds__(256, T <= 2 ? 2 : 1) void bwd_kernel(BwdArgs a)
     const int st = decode_work<T>(a, it, w);
     if (st == 0) break;
     if (st == 2) continue;
-    if (busy) __syncthreads();  // the previous item's LDS reads are complete
-    bwd_item<MODE, T>(a, w);
+    if (busy) __syncthreads();  // every wave has finished reading the previous item's A chunks
+    bwd_item<MODE, T>(a, w, abuf);
     busy = true;
   }
 }
@@ -447,10 +447,14 @@ int resident_groups(int per_cu)
 
 hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
 {
-  const long long total = (long long)max_tiles * a.n_ct;
+  const long long n_ct4 = (a.n_ct + kWaves - 1) / kWaves;
+  const long long total = (long long)max_tiles * n_ct4;
   if (total <= 0) return hipSuccess;
   // each weight segment is addressed through one buffer resource with a 32-bit byte count
   if ((long long)a.R * (a.C / 2) >= (1LL << 32)) return hipErrorInvalidValue;
+  // the epilogue's 16-byte accesses of rows assume these (true for every caller: C is a multiple
+  // of 32 and the row strides are multiples of 16 elements)
+  if (a.C % 32 || (a.y && a.ldy % 4) || a.lda % 8) return hipErrorInvalidValue;
   const bool split = a.tiles && a.small_tiles && a.groups;
   BwdArgs b = a;
   if (!split) {
@@ -458,7 +462,7 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
     b.groups = nullptr;
   }
   const long long blocks = (total + 7) / 8 * 8;
-  dim3 grid((unsigned)blocks), block(256);
+  dim3 grid((unsigned)blocks), block(64 * kWaves);
   if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, 1>), grid, block, 0, s, b);
   else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, 1>), grid, block, 0, s, b);
   else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, 1>), grid, block, 0, s, b);
@@ -466,8 +470,8 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
   if (e != hipSuccess || !split) return e;
   // groups come from experts of at least kGroupMinTiles tiles: at most max_tiles / 2 of them,
   // each split into kGroupTiles / kBwdGroupT work items
-  const long long gtotal = ((long long)max_tiles / 2 + 1) * (kGroupTiles / kBwdGroupT) * a.n_ct;
-  dim3 ggrid((unsigned)std::min<long long>((gtotal + 7) / 8 * 8, resident_groups(kBwdGroupT <= 2 ? 2 : 1)));
+  const long long gtotal = ((long long)max_tiles / 2 + 1) * (kGroupTiles / kBwdGroupT) * n_ct4;
+  dim3 ggrid((unsigned)std::min<long long>((gtotal + 7) / 8 * 8, resident_groups(1)));
   if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, kBwdGroupT>), ggrid, block, 0, s, b);
   else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, kBwdGroupT>), ggrid, block, 0, s, b);
   else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, kBwdGroupT>), ggrid, block, 0, s, b);

@@ -105,7 +105,7 @@ constexpr int kFwdRowsPerTile = 16;
 constexpr int kGroupTiles = 4;     // row tiles of one large-bucket work-group
 constexpr int kGroupMinTiles = 4;  // experts with at least this many tiles take the large-bucket path
 constexpr int kFwdColsPerTile = 64;  // kFwdPlain / kFwdDown; kFwdGateUp covers 32 features
-constexpr int kBwdColsPerTile = 512;
+constexpr int kBwdColsPerTile = 256;  // output columns of one transposed-product wave
 
 hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);

@@ -137,7 +137,7 @@ def test_nan_logits_select_real_experts(k, E):
     assert ((idx >= 0) & (idx < E)).all()
     want_idx, _ = oracle.router_select(logits, bias, top_k)
     assert idx[:16].tolist() == want_idx[:16].tolist()   # decided by NaN ranks and ids alone
-    choice = oracle._sigmoid(logits.astype(np.float64)) + bias
+    choice = 1.0 / (1.0 + np.exp(-logits.astype(np.float64))) + bias
     loose = 0
     for r in range(16, N):
         nan = np.isnan(choice[r])
