@@ -78,6 +78,18 @@ size_t mxfp4_gemm_workspace_size(int M, int K, int R);
 int mxfp4_gemm(float *y, const float *x, const uint8_t *packed, const uint8_t *scales, int M,
                int K, int R, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* mxfp4_gemm without a workspace: the same product (same kernels, bit-identical results), with
+ * x's activation tiles staged in a 16 MiB device array that the library holds on each GPU it runs
+ * on until the process ends. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc); it calls no hipMalloc, hipFree or allocating library routine. Limit:
+ * ceil(M/16) * ceil(K/512) * 16896 bytes <= 16 MiB (M <= 1120 at K = 7168), else
+ * MXFP4_EWORKSPACE and nothing is launched. All calls on one device share that array: calls
+ * that overlap on one device (different streams or host threads) race and must be serialised by
+ * the caller; consecutive calls on one stream are safe. */
+int mxfp4_gemm_noalloc(float *y, const float *x, const uint8_t *packed, const uint8_t *scales,
+                       int M, int K, int R, hipStream_t stream);
+
 /* Replaces void mxfp4_gemm_t(float *y, const float *dy, const uint8_t *packed,
  * const uint8_t *scales, int M, int K, int R) (mxfp4_gemm.c:96-129):
  * y[M, K] += dy[M, R] . W (accumulates into y, like the reference). */

@@ -4,10 +4,15 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/lazylora_mxfp4.h"
 #include "mx_device.h"
 #include "mx_kernels.h"
+
+// Device scratch of mxfp4_gemm_noalloc (see scratch_on_current_device below).
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
 
@@ -283,7 +288,7 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   return MXFP4_OK;
 }
 
-// Argument checks of the single-expert forward product.
+// Argument checks of the single-expert forward product (mxfp4_gemm and mxfp4_gemm_noalloc).
 int check_gemm_args(const float* y, const float* x, const uint8_t* packed, const uint8_t* scales, int M, int K,
                     int R)
 {
@@ -312,6 +317,34 @@ int gemm_into(float* y, const float* x, const uint8_t* packed, const uint8_t* sc
   a.n_ct = (R + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
   a.y = y; a.ldy = R;
   MX_TRY(mx::launch_fwd(a, mx::kFwdPlain, tiles, stream), "gemm: product");
+  return MXFP4_OK;
+}
+
+// ---------------------------------------------------------------- allocation-free scratch
+// mxfp4_gemm_noalloc stages its activation tiles in the file-scope device array `scratch` (top of
+// this file) instead of a caller workspace. Every GPU that loads the library holds its own copy
+// until the process ends.
+// Host code never uses the array's name as an address (on the host it is only a stand-in
+// symbol): the device address is looked up once per device with hipGetSymbolAddress, with that
+// device current, and kept in g_scratch. All calls on one device share the array, so calls that
+// overlap on one device (two streams, two host threads) race on it.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[kMaxDevices] = {};
+
+int scratch_on_current_device(uint8_t** out)
+{
+  int dev = 0;
+  MX_TRY(hipGetDevice(&dev), "gemm_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(MXFP4_EINVAL, "gemm_noalloc: device index out of range%s");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    MX_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "gemm_noalloc: hipGetSymbolAddress(scratch)");
+    if (!p) return fail(MXFP4_EHIP, "gemm_noalloc: no device address for the scratch array%s");
+    g_scratch[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch[dev];
   return MXFP4_OK;
 }
 
@@ -352,6 +385,22 @@ int mxfp4_gemm(float* y, const float* x, const uint8_t* packed, const uint8_t* s
   const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
   if (!workspace || workspace_bytes < at_bytes(tiles, K)) return fail(MXFP4_EWORKSPACE, "gemm: workspace too small%s");
   return gemm_into(y, x, packed, scales, M, K, R, at<uint8_t>(workspace, 0), stream);
+}
+
+int mxfp4_gemm_noalloc(float* y, const float* x, const uint8_t* packed, const uint8_t* scales, int M, int K, int R,
+                       hipStream_t stream)
+{
+  const int rc = check_gemm_args(y, x, packed, scales, M, K, R);
+  if (rc != MXFP4_OK || M == 0 || R == 0) return rc;
+  const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
+  if (at_bytes(tiles, K) > kScratchBytes)
+    return fail(MXFP4_EWORKSPACE,
+                "gemm_noalloc: the activation tiles of this M x K exceed the library's 16 MiB device scratch "
+                "(ceil(M/16) * ceil(K/512) * 16896 bytes); use mxfp4_gemm with a workspace%s");
+  uint8_t* tiles_dev = nullptr;
+  const int src = scratch_on_current_device(&tiles_dev);
+  if (src != MXFP4_OK) return src;
+  return gemm_into(y, x, packed, scales, M, K, R, tiles_dev, stream);
 }
 
 size_t mxfp4_gemm_t_workspace_size(int M, int K, int R)

@@ -62,6 +62,8 @@ def _load_library() -> ctypes.CDLL:
     lib.mxfp4_gemm_workspace_size.argtypes = [ci, ci, ci]
     lib.mxfp4_gemm.restype = ci
     lib.mxfp4_gemm.argtypes = [vp, vp, vp, vp, ci, ci, ci, vp, sz, vp]
+    lib.mxfp4_gemm_noalloc.restype = ci
+    lib.mxfp4_gemm_noalloc.argtypes = [vp, vp, vp, vp, ci, ci, ci, vp]
     lib.mxfp4_gemm_t_workspace_size.restype = sz
     lib.mxfp4_gemm_t_workspace_size.argtypes = [ci, ci, ci]
     lib.mxfp4_gemm_t.restype = ci
