@@ -14,7 +14,11 @@ kernel's algorithmic weight bytes per launch over its mean duration, measured wi
 recorded by the library on the launch stream inside the timed region; `cpu_baseline` is this
 repo's C restatement of the reference CPU path timed on a bounded sample of the same layer.
 
-    python bench.py [--steps 20] [--warmup 3] [--routing uniform|zipf] [--no-cpu]
+    python bench.py [--steps 20] [--warmup 3] [--routing uniform|zipf] [--no-cpu] [--no-extra]
+
+The default run also times the Zipf-skewed routing of the same layer (key "zipf") and config 2 at
+M = 1 and M = 256 tokens per expert (key "config2"), each in its own timed region after the
+headline's.
 """
 import argparse
 import json
@@ -92,44 +96,49 @@ def make_inputs(seed: int, routing: str):
     return torch.from_numpy(h).cuda(), idx.contiguous(), w.contiguous(), torch.from_numpy(g).cuda()
 
 
-def cpu_baseline(layer, H, I, W, G, n_active, budget_s: float):
-    """This repo's C restatement of the reference path (oracle/mxfp4_oracle.c, bit-identical to
-    lazy_lora/native/mxfp4_gemm.c where that runs) on a sample of the layer's experts, each with
-    its full token bucket: forward sweep + backward sweep (which recomputes the forward, as the
-    reference does). Extrapolated to the whole layer."""
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(layer, H, I, W, G, budget_s: float, act: str):
+    """The reference trainer's CPU path over the whole layer (every active expert, every token):
+    oracle/reference_path.py composes it as lazy_trainer.py:746-880 does, the fused C products
+    (oracle/mxfp4_oracle.c, the reference's schedule and flags) for buckets of at most 48 rows and
+    C dequantisation + torch's CPU sgemm above. One forward sweep + one backward sweep (which
+    recomputes the forward, as the reference does). The median of up to 3 runs that fit the
+    budget."""
     import oracle
+    from oracle import reference_path
     lib = oracle.oracle_lib()
-    idx = I.cpu().numpy()
-    active = np.unique(idx)
-    h, w, g = H.cpu().numpy(), W.cpu().numpy(), G.cpu().numpy()
-
-    def run(ids):
-        sel = torch.from_numpy(ids).cuda()
-        ex = oracle.ExpertSet(*[t[sel].cpu().numpy() for t in layer.tensors()])
-        remap = np.full(E, -1, np.int64)
-        remap[ids] = np.arange(len(ids))
-        sidx = remap[idx]
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    ex = oracle.ExpertSet(*[t.cpu().numpy() for t in layer.tensors()])
+    h, idx, w, g = H.cpu().numpy(), I.cpu().numpy(), W.cpu().numpy(), G.cpu().numpy()
+    times = []
+    while len(times) < 3:
         t0 = time.perf_counter()
-        lib.moe_forward(h, sidx, w, ex, "swiglu", order=np.arange(len(ids)))
-        lib.moe_backward(h, sidx, w, ex, g, "swiglu", order=np.arange(len(ids)))
-        return time.perf_counter() - t0
-
-    rng = np.random.default_rng(7)
-    probe = rng.choice(active, size=2, replace=False)
-    t_probe = run(np.sort(probe)) / 2
-    n = int(min(max(budget_s / max(t_probe, 1e-6), 4), len(active)))
-    ids = np.sort(rng.choice(active, size=n, replace=False)) if n < len(active) else active
-    times = [run(ids)]
-    while n == len(active) and sum(times) + times[0] <= budget_s:  # the whole layer: repeat within budget
-        times.append(run(ids))
-    t = float(np.mean(times))
-    layer_s = t / n * n_active
-    what = (f"the whole layer ({n_active} active experts, every token), {len(times)} run(s), {t:.1f} s each"
-            if n == len(active) else
-            f"{n} of {n_active} active experts with their full token buckets ({t:.1f} s), extrapolated "
-            f"x{n_active / n:.1f} to the layer")
-    return {"value": N / layer_s, "unit": "tokens/s", "cores": lib.threads(), "kind": "port",
-            "sample": f"C restatement (oracle/mxfp4_oracle.c, -O3 -mavx2 -mfma -fopenmp) fwd+bwd of {what}"}
+        reference_path.routed_forward(lib, h, idx, w, ex, act)
+        reference_path.routed_backward(lib, h, idx, w, ex, g, act)
+        times.append(time.perf_counter() - t0)
+        log(f"[bench] CPU run {len(times)}: {times[-1]:.2f} s")
+        if sum(times) + times[0] > budget_s:
+            break
+    t = float(np.median(times))
+    counts = np.bincount(idx.ravel(), minlength=E)
+    big = int((counts > reference_path.FUSED_MAX_ROWS).sum())
+    return {"value": N / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"the whole layer ({int((counts > 0).sum())} active experts, {big} of them above 48 rows, "
+                      f"every token), fwd+bwd, median of {len(times)} run(s): {[round(x, 2) for x in times]} s",
+            "cpu_model": _cpu_model(), "threads": {"openmp": lib.threads(), "torch": torch.get_num_threads()},
+            "compile_flags": "gcc -O3 -mavx2 -mfma -fopenmp (oracle/Makefile; the reference's build.sh flags)",
+            "path": "reference composition: fused C products for buckets <= 48 rows, C dequant + torch CPU "
+                    "sgemm above (lazy_trainer.py:746-880)"}
 
 
 def make_lora(r: int):
@@ -147,11 +156,11 @@ def make_lora(r: int):
     return (adapter(D, F), adapter(D, F), adapter(F, D))
 
 
-def expert_main(args, k):
+def expert_sweep(args, k, Ms):
     """Config 2: the single-expert MXFP4 GLU block (gate/up 2048x7168, down 7168x2048) forward at
-    M = 1, 4, 16, 64, 256 tokens. One launch covers 32 distinct expert copies (749 MB, beyond the
-    256 MB MALL) with M tokens each, so every timed pass streams its weights from HBM; per-expert
-    figures are the launch's divided by 32."""
+    M tokens. One launch covers 32 distinct expert copies (749 MB, beyond the 256 MB MALL) with M
+    tokens each, so every timed pass streams its weights from HBM; per-expert figures are the
+    launch's divided by 32."""
     from lazylora_amd.experts import ExpertLayer
     copies = 32
     gen = torch.Generator(device="cuda")
@@ -161,7 +170,7 @@ def expert_main(args, k):
     layer = ExpertLayer(codes(copies, F, D // 2), scales(copies, F, D // 32), codes(copies, F, D // 2),
                         scales(copies, F, D // 32), codes(copies, D, F // 2), scales(copies, D, F // 32))
     sweep = []
-    for M in (1, 4, 16, 64, 256):
+    for M in Ms:
         n = copies * M
         rng = np.random.default_rng(M)
         H = torch.from_numpy(rng.standard_normal((n, D), dtype=np.float32)).cuda()
@@ -198,6 +207,13 @@ def expert_main(args, k):
         log(f"[bench] expert M={M:3d}: {row['us_per_expert']:7.2f} us/expert (products "
             f"{row['products_us_per_expert']:6.2f} us, {row['weight_GBps_products']:7.1f} GB/s, "
             f"{row['TFLOPs_products']:6.1f} TFLOP/s)")
+    del layer
+    torch.cuda.empty_cache()
+    return sweep, copies
+
+
+def expert_main(args, k):
+    sweep, copies = expert_sweep(args, k, (1, 4, 16, 64, 256))
     line = {
         "metric": "config 2: single-expert MXFP4 GLU block forward, weight GB/s of the products (M = 1)",
         "value": sweep[0]["weight_GBps_products"],
@@ -290,7 +306,9 @@ def main():
     ap.add_argument("--routing", choices=["uniform", "zipf"], default="uniform")
     ap.add_argument("--act", choices=["swiglu", "situ"], default="swiglu")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=30.0, help="budget of the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the Zipf-routing step and the config-2 points reported beside the headline")
     ap.add_argument("--workload", choices=["layer", "stream", "expert"], default="layer",
                     help="layer: config 4 (the metric); stream: config 5, layers streamed from pinned host memory; "
                          "expert: config 2, the single-expert block swept over token counts")
@@ -328,49 +346,7 @@ def main():
     log(f"[bench] layer {layer.nbytes / 1e9:.2f} GB in HBM, {n_active} active experts, setup {time.time() - t_setup:.1f}s")
 
     lora = make_lora(args.lora_rank) if args.lora_rank else None
-
-    def step():
-        k.routed_forward(H, I, W, layer, act=args.act, save_for_backward=True, workspace=ws, lora=lora)
-        return k.routed_backward(H, I, W, layer, G, act=args.act, reuse_forward=True, workspace=ws, lora=lora)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    log(f"[bench] warmup {args.warmup} done")
-
-    if args.copy_calibration:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-
-    k.set_timing(True)
-    stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(args.steps):
-        step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms_total = start.elapsed_time(end)
-    calls = k.phase_times()
-    k.set_timing(False)
-    ms_step = ms_total / args.steps
-    log(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step")
-
-    phase_ms = {}
-    for call in calls:
-        for name, ms in call:
-            phase_ms.setdefault(name, []).append(ms)
-    phase_avg = {n: float(np.mean(v)) for n, v in phase_ms.items()}
-    for n, v in sorted(phase_avg.items(), key=lambda kv: -kv[1]):
-        extra = ""
-        if n in PHASE_BYTES:
-            extra = f"  {PHASE_BYTES[n] * n_active / (v * 1e-3) / 1e9:8.1f} GB/s algorithmic"
-        log(f"[bench]   {n:14s} {v:8.3f} ms{extra}")
+    ms_step, phase_avg = time_layer(args, k, layer, H, I, W, G, ws, lora, n_active, calibrate=args.copy_calibration)
 
     dom = max((n for n in phase_avg if n in PHASE_BYTES), key=lambda n: phase_avg[n])
     dom_bytes = PHASE_BYTES[dom] * n_active
@@ -378,10 +354,33 @@ def main():
     step_bytes = 2 * EXPERT_BYTES * n_active  # one forward pass + one transposed pass over the weights
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
 
+    extra = {}
+    if not args.no_extra and args.routing == "uniform" and not args.lora_rank:
+        # the skewed variant of configs 3/4 ([3]) on the same layer
+        Hz, Iz, Wz, Gz = make_inputs(1, "zipf")
+        nz = int(torch.unique(Iz).numel())
+        counts = torch.bincount(Iz.flatten(), minlength=E)
+        log(f"[bench] zipf routing: {nz} active experts, largest bucket {int(counts.max())}")
+        ms_z, ph_z = time_layer(args, k, layer, Hz, Iz, Wz, Gz, ws, None, nz)
+        extra["zipf"] = {"ms_per_step": ms_z, "tokens_per_s": N / (ms_z * 1e-3), "active_experts": nz,
+                         "largest_bucket": int(counts.max()),
+                         "weight_GBps": 2 * EXPERT_BYTES * nz / (ms_z * 1e-3) / 1e9,
+                         "phases_ms": {n: round(v, 4) for n, v in ph_z.items()}}
+        del Hz, Iz, Wz, Gz
+        # config 2 at its two ends, M = 1 (HBM-bound) and M = 256 (MFMA-bound)
+        del ws
+        torch.cuda.empty_cache()
+        sweep, copies = expert_sweep(args, k, (1, 256))
+        extra["config2"] = {f"M={r['M']}": {"us_per_expert": r["us_per_expert"],
+                                            "products_us_per_expert": r["products_us_per_expert"],
+                                            "weight_GBps_products": r["weight_GBps_products"],
+                                            "TFLOPs_products": r["TFLOPs_products"]} for r in sweep}
+        extra["config2"]["expert_copies_per_launch"] = copies
+
     cpu = None
     if not args.no_cpu:
-        log("[bench] CPU baseline (C restatement of the reference path) ...")
-        cpu = cpu_baseline(layer, H, I, W, G, n_active, args.cpu_seconds)
+        log("[bench] CPU baseline (the reference composition on the C restatement + torch CPU) ...")
+        cpu = cpu_baseline(layer, H, I, W, G, args.cpu_seconds, args.act)
         log(f"[bench] CPU baseline {cpu['value']:.2f} tokens/s on {cpu['cores']} threads")
 
     line = {
@@ -414,7 +413,53 @@ def main():
                      "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_ms": phase_avg[dom]},
         "cpu_baseline": cpu,
     }
+    line.update(extra)
     print(json.dumps(line), flush=True)
+
+
+def time_layer(args, k, layer, H, I, W, G, ws, lora, n_active, calibrate=False):
+    """(ms per fwd+bwd step, mean ms per phase) over args.steps timed steps after args.warmup."""
+    def step():
+        k.routed_forward(H, I, W, layer, act=args.act, save_for_backward=True, workspace=ws, lora=lora)
+        return k.routed_backward(H, I, W, layer, G, act=args.act, reuse_forward=True, workspace=ws, lora=lora)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done")
+    if calibrate:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    k.set_timing(True)
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(end)
+    calls = k.phase_times()
+    k.set_timing(False)
+    ms_step = ms_total / args.steps
+    log(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step")
+    phase_ms = {}
+    for call in calls:
+        for name, ms in call:
+            phase_ms.setdefault(name, []).append(ms)
+    phase_avg = {n: float(np.mean(v)) for n, v in phase_ms.items()}
+    for n, v in sorted(phase_avg.items(), key=lambda kv: -kv[1]):
+        extra = ""
+        if n in PHASE_BYTES:
+            extra = f"  {PHASE_BYTES[n] * n_active / (v * 1e-3) / 1e9:8.1f} GB/s algorithmic"
+        log(f"[bench]   {n:14s} {v:8.3f} ms{extra}")
+    return ms_step, phase_avg
 
 
 if __name__ == "__main__":
