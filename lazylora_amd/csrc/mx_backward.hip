@@ -40,11 +40,6 @@ namespace {
 constexpr int kStepRows = 32;
 typedef const __attribute__((address_space(4))) int* cint_ptr;
 
-#ifndef MX_BWD_GROUP_T
-#define MX_BWD_GROUP_T 2
-#endif
-constexpr int kBwdGroupT = MX_BWD_GROUP_T;  // row tiles per large-bucket work item (2 or 4)
-
 constexpr int kWaves = 4;  // waves (stripes) per work-group
 
 // One work item: the kWaves stripes from kWaves * ct4 on of up to T row tiles of one expert
@@ -56,21 +51,18 @@ struct WorkItem {
   int row0[T], nrows[T];
 };
 
-// Work item `it` of this wave (items are dealt round-robin over the XCDs, blockIdx % 8, each
-// XCD taking one contiguous run, in strides of the grid, so the stripes of one tile, which read
-// the same A rows, run on one XCD). Returns 0 when there is none left, 2 for an empty part of a
-// short group, 1 for an item.
+// Work item `it` of this work-group (items are dealt round-robin over the XCDs, blockIdx % 8, each
+// XCD taking one contiguous run, in strides of the grid, so the stripe blocks of one tile, which
+// read the same A rows, run on one XCD). Returns 0 when there is none left, 1 for an item.
 template <int T>
 __device__ __forceinline__ int decode_work(const BwdArgs& a, int it, WorkItem<T>& w)
 {
   // the tile lists are only read here: scalar loads through the constant address space
-  int count;
-  constexpr int kParts = T == 1 ? 1 : kGroupTiles / T;  // work items per group
+  static_assert(T == 1, "large buckets take bwd_group_kernel");
   // with no large-bucket groups the small-bucket list is every tile in order: skip it
   const bool use_small = a.small_tiles && *(cint_ptr)a.n_groups > 0;
-  if (T == 1) count = use_small ? *(cint_ptr)a.n_small
-                                : a.tiles ? *(cint_ptr)a.n_tiles : (a.M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
-  else count = *(cint_ptr)a.n_groups * kParts;
+  const int count = use_small ? *(cint_ptr)a.n_small
+                              : a.tiles ? *(cint_ptr)a.n_tiles : (a.M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
   const int n_ct4 = (a.n_ct + kWaves - 1) / kWaves;
   const int total = count * n_ct4;
   const int per_xcd = (total + 7) >> 3;
@@ -79,17 +71,8 @@ __device__ __forceinline__ int decode_work(const BwdArgs& a, int it, WorkItem<T>
   if (slot >= per_xcd || item >= total) return 0;
   const int i = item / n_ct4;
   w.ct4 = item - i * n_ct4;
-  int t0;
-  if (T == 1) {
-    t0 = use_small ? ((cint_ptr)a.small_tiles)[i] : i;
-    w.ntl = 1;
-  } else {
-    const int part = i % kParts;
-    const cint_ptr gg = (cint_ptr)(a.groups + i / kParts);
-    t0 = gg[1] + part * T;
-    w.ntl = min(T, gg[2] - part * T);
-    if (w.ntl <= 0) return 2;  // this part of a short group is empty
-  }
+  const int t0 = use_small ? ((cint_ptr)a.small_tiles)[i] : i;
+  w.ntl = 1;
 #pragma unroll
   for (int tt = 0; tt < T; ++tt) {
     const int t = t0 + (tt < w.ntl ? tt : 0);
@@ -159,7 +142,7 @@ MX_DEV void static_for(Fn&& f)
 #endif
 template <int T>
 struct Cfg {
-  static constexpr int kRing = T == 1 ? MX_BWD_RING : 2;
+  static constexpr int kRing = MX_BWD_RING;
   static constexpr int kChunk = 16 / T;
   static constexpr int kChunkBytes = kChunk * T * 2 * 1024;
 };
@@ -188,28 +171,34 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
   // bytes, finite weights whose products are never stored
   const int col = c0 + 16 * n;
   const int col_c = col < a.C ? col : 0;
-  // Each segment of this expert is one buffer resource: rows at or past the segment's end (the
-  // tail of a row count that is not a multiple of kStepRows, and the padding steps) read as
-  // zero weights. Segments hold a multiple of kStepRows rows whenever there are two, so a step
-  // never straddles them. A stripe past C gets empty resources: zeros, no memory traffic.
-  const uint32_t wbytes = stripe_ok ? (uint32_t)a.R * wpitch : 0u, sbytes = stripe_ok ? (uint32_t)a.R * cbs : 0u;
-  const rsrc_t rw0 = make_rsrc(a.wp0 + (long long)w.expert * a.wp_estride, wbytes);
-  const rsrc_t rs0 = make_rsrc(a.ws0 + (long long)w.expert * a.ws_estride, sbytes);
-  const rsrc_t rw1 = a.nseg > 1 ? make_rsrc(a.wp1 + (long long)w.expert * a.wp_estride, wbytes) : rw0;
-  const rsrc_t rs1 = a.nseg > 1 ? make_rsrc(a.ws1 + (long long)w.expert * a.ws_estride, sbytes) : rs0;
-  const uint32_t lane_w = (uint32_t)(8 * g) * wpitch + (uint32_t)col_c / 2;
-  const uint32_t lane_s = (uint32_t)(8 * g) * cbs + (uint32_t)col_c / kGroup;
+  // Weights and scales are read through buffer resources, one per step, based at the step's
+  // first row of its segment (scalar arithmetic only), so each lane's offsets stay fixed for the
+  // whole item: rows at or past the segment's end (the tail of a row count that is not a
+  // multiple of kStepRows, and the padding steps) fall outside the resource and read as zero
+  // weights. Segments hold a multiple of kStepRows rows whenever there are two, so a step never
+  // straddles them. A stripe past C gets empty resources: zeros, no memory traffic.
+  const uint8_t* const wbase0 = a.wp0 + (long long)w.expert * a.wp_estride;
+  const uint8_t* const sbase0 = a.ws0 + (long long)w.expert * a.ws_estride;
+  const uint8_t* const wbase1 = a.nseg > 1 ? a.wp1 + (long long)w.expert * a.wp_estride : wbase0;
+  const uint8_t* const sbase1 = a.nseg > 1 ? a.ws1 + (long long)w.expert * a.ws_estride : sbase0;
+  uint32_t offw[8], offs[8];  // row 8g + q of a step, this lane's columns
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    offw[q] = (uint32_t)(8 * g + q) * wpitch + (uint32_t)col_c / 2;
+    offs[q] = (uint32_t)(8 * g + q) * cbs + (uint32_t)col_c / kGroup;
+  }
 
   auto load_step = [&](int step, StepRaw& r) {
     const int row0 = step * kStepRows;
     const bool seg = a.nseg > 1 && row0 >= a.R;  // uniform
-    const uint32_t rr = (uint32_t)(seg ? row0 - a.R : row0);
-    const rsrc_t W = seg ? rw1 : rw0;
-    const rsrc_t S = seg ? rs1 : rs0;
+    const int rr = seg ? row0 - a.R : row0;
+    const int rows_left = stripe_ok ? max(a.R - rr, 0) : 0;
+    const rsrc_t W = make_rsrc((seg ? wbase1 : wbase0) + (long long)rr * wpitch, (uint32_t)rows_left * wpitch);
+    const rsrc_t S = make_rsrc((seg ? sbase1 : sbase0) + (long long)rr * cbs, (uint32_t)rows_left * cbs);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) r.w[q] = buf8B_nt(W, lane_w + (rr + q) * wpitch);
+    for (int q = 0; q < 8; ++q) r.w[q] = buf8B_nt(W, offw[q]);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) r.s[q] = buf8(S, lane_s + (rr + q) * cbs);
+    for (int q = 0; q < 8; ++q) r.s[q] = buf8(S, offs[q]);
   };
 
   // A operands: MFMA lane (i = n, g) takes elements 8g..8g+7 of the step's 32 contraction
@@ -411,25 +400,322 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
 // One wave per work-group. T = 1: one item per wave (the grid covers every item). T > 1: a
 // resident grid that loops over the large-bucket items, so launches with few or no groups cost
 // almost nothing.
-// One work-group of kWaves waves per item. T = 1: one item per work-group (the grid covers every
-// item). T > 1: a resident grid that loops over the large-bucket items, so launches with few or
-// no groups cost almost nothing.
-template <int MODE, int T>
-__global__ __launch_bounds__(64 * kWaves, T == 1 ? 2 : 1) void bwd_kernel(BwdArgs a)
+// One work-group of kWaves waves per item; the grid covers every item.
+template <int MODE>
+__global__ __launch_bounds__(64 * kWaves, 2) void bwd_kernel(BwdArgs a)
 {
-  __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * Cfg<T>::kChunkBytes];
-  WorkItem<T> w;
-  if constexpr (T == 1) {
-    if (decode_work<T>(a, 0, w) == 1) bwd_item<MODE, T>(a, w, abuf);
-    return;
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * Cfg<1>::kChunkBytes];
+  WorkItem<1> w;
+  if (decode_work<1>(a, 0, w) == 1) bwd_item<MODE, 1>(a, w, abuf);
+}
+
+// ---------------------------------------------------------------- large buckets
+// An expert with many rows would stream (and decode) its weights once per row tile. Its tiles
+// come in groups of up to kGroupTiles (8) consecutive tiles; a work item is GT of them (a part of
+// a group) x a block of 4 GS columns: every wave decodes a GS-column stripe of each 32-row step
+// once and applies it to all GT row tiles, and the item's A operands (GT tiles x hi/lo, 2 GT KiB
+// per step) come through LDS for the four waves. Each weight byte is read once per 16 GT rows
+// instead of once per 16, and each A fragment read from LDS feeds GS / 16 MFMAs.
+//
+// Lane (n, g) of a wave holds columns (GS / 16) n .. + GS / 16 - 1 of its stripe, whose weights
+// are GS / 32 bytes of each of its 8 rows: with GS = 128 the lane's own dword, with GS = 64 half
+// of the dword its lane pair shares. Byte p gives MFMAs 2p and 2p + 1. Scales come as the dword
+// holding the lane's scale byte, so the kernel requires C % 128 == 0 (whole dwords of scales per
+// row); launch_bwd sends other shapes through the one-tile kernel.
+#ifndef MX_BWD_GT
+#define MX_BWD_GT 4
+#endif
+#ifndef MX_BWD_GS
+#define MX_BWD_GS 128
+#endif
+#ifndef MX_BWD_GRING
+#define MX_BWD_GRING 2
+#endif
+#ifndef MX_BWD_GPER_CU
+#define MX_BWD_GPER_CU 2
+#endif
+constexpr int kGT = MX_BWD_GT;                // row tiles per item
+constexpr int kGS = MX_BWD_GS;                // columns per wave
+constexpr int kGParts = kGroupTiles / kGT;    // items per group and column block
+constexpr int kGCols = kWaves * kGS;          // columns per item
+constexpr int kGRing = MX_BWD_GRING;          // steps of weights in flight per wave
+constexpr int kGChunk = MX_BWD_GRING;         // steps per LDS A chunk (a multiple of kGRing)
+constexpr int kGUnit = 1024;                  // one tile x one term x one step of A
+constexpr int kGChunkBytes = kGChunk * kGT * 2 * kGUnit;
+constexpr int kGBytes = kGS / 32;             // weight bytes per row and lane
+static_assert(kGCols % kBwdColsPerTile == 0, "an item covers whole 256-column grad_w partials");
+
+struct GStep {
+  uint32_t w[8];  // the dword of each row holding this lane's weight bytes
+  uint32_t s[8];  // the dword of each row holding this lane's scale byte
+};
+
+template <int P>
+MX_DEV void gdecode_pair(const uint32_t (&wl)[8], const float (&sf)[8], bf16x8& b0, bf16x8& b1)
+{
+  uint32_t d[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    d[q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wl[q], sf[q], P));
+  uint32_t e[4], o[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    e[m] = __builtin_amdgcn_perm(d[2 * m + 1], d[2 * m], 0x05040100u);
+    o[m] = __builtin_amdgcn_perm(d[2 * m + 1], d[2 * m], 0x07060302u);
   }
+  b0 = __builtin_bit_cast(bf16x8, i32x4{(int)e[0], (int)e[1], (int)e[2], (int)e[3]});
+  b1 = __builtin_bit_cast(bf16x8, i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]});
+}
+
+template <int MODE>
+__device__ __forceinline__ void bwd_group_item(const BwdArgs& a, int expert, int t0, int ntl, int cb, uint8_t* abuf,
+                                               float* red)
+{
+  constexpr int T = kGT;
+  constexpr int NC = kGS / 16;  // MFMA column sets = columns per lane
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int c0w = cb * kGCols + wave * kGS;  // this wave's first column
+  const bool stripe_ok = c0w < a.C;          // uniform
+  const int col = c0w + NC * n;
+  const int rtot = a.nseg * a.R;
+  const int nsteps = (rtot + kStepRows - 1) / kStepRows;
+  const int nsteps_pad = (nsteps + kGChunk - 1) / kGChunk * kGChunk;
+  const uint32_t cbs = a.C / kGroup, wpitch = a.C / 2;
+
+  int row0[T], nrows[T];
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt) {
+    const cint_ptr tl = (cint_ptr)(a.tiles + t0 + (tt < ntl ? tt : 0));
+    row0[tt] = tl[1];
+    nrows[tt] = tt < ntl ? tl[2] : 0;
+  }
+
+  const uint8_t* const wbase0 = a.wp0 + (long long)expert * a.wp_estride;
+  const uint8_t* const sbase0 = a.ws0 + (long long)expert * a.ws_estride;
+  const uint8_t* const wbase1 = a.nseg > 1 ? a.wp1 + (long long)expert * a.wp_estride : wbase0;
+  const uint8_t* const sbase1 = a.nseg > 1 ? a.ws1 + (long long)expert * a.ws_estride : sbase0;
+  const int colc = stripe_ok ? col : 0;
+  // the lane's bytes sit at byte (colc / 2) % 4 of their dword
+  const uint32_t wsh = 8u * (((uint32_t)colc / 2) & 3u);
+  const uint32_t ssh = 8u * (((uint32_t)colc / kGroup) & 3u);
+  uint32_t offw[8], offs[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    offw[q] = ((uint32_t)(8 * g + q) * wpitch + (uint32_t)colc / 2) & ~3u;
+    offs[q] = ((uint32_t)(8 * g + q) * cbs + (uint32_t)colc / kGroup) & ~3u;
+  }
+  auto load_step = [&](int step, GStep& r) {
+    const int rs = step * kStepRows;
+    const bool seg = a.nseg > 1 && rs >= a.R;  // uniform
+    const int rr = seg ? rs - a.R : rs;
+    const int rows_left = stripe_ok ? max(a.R - rr, 0) : 0;
+    const rsrc_t W = make_rsrc((seg ? wbase1 : wbase0) + (long long)rr * wpitch, (uint32_t)rows_left * wpitch);
+    const rsrc_t S = make_rsrc((seg ? sbase1 : sbase0) + (long long)rr * cbs, (uint32_t)rows_left * cbs);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      r.w[q] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(W, (int)offw[q], 0, 2);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) r.s[q] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(S, (int)offs[q], 0, 0);
+  };
+
+  // A chunk copies: unit u = (step in chunk si, tile tt, term) at ((si * T + tt) * 2 + term) KiB;
+  // the four waves take the units in turn (wave w: u = w, w + 4, ...), which for every step
+  // keeps each wave on one term and a fixed set of tiles
+  constexpr int kUnits = kGChunk * T * 2;
+  static_assert(kUnits % kWaves == 0 && (T * 2) % kWaves == 0, "units split evenly over the waves");
+  constexpr int kMine = T * 2 / kWaves;  // units per step and wave
+  const uint16_t* pa[kMine];
+#pragma unroll
+  for (int k = 0; k < kMine; ++k) {
+    const int u = wave + kWaves * k;  // unit of step 0
+    const int tt = (u >> 1) % T, term = u & 1;
+    const int ri = row0[tt] + min(n, max(nrows[tt], 1) - 1);
+    const long long arow = a.a_row_map ? a.a_row_map[ri] : ri;
+    pa[k] = (term ? a.a_lo : a.a_hi) + arow * a.lda + 8 * g;
+  }
+  auto copy_chunk = [&](int chunk) {
+    uint8_t* dst = abuf + (chunk & 1) * kGChunkBytes;
+#pragma unroll
+    for (int si = 0; si < kGChunk; ++si) {
+      const int so = min(chunk * kGChunk + si, nsteps - 1) * kStepRows;
+#pragma unroll
+      for (int k = 0; k < kMine; ++k) dma16_async(pa[k] + so, dst + (si * T * 2 + wave + kWaves * k) * kGUnit);
+    }
+  };
+
+  f32x4 acc[T][NC];
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+    for (int t = 0; t < NC; ++t) acc[tt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  GStep ring[kGRing];
+  copy_chunk(0);
+#pragma unroll
+  for (int p = 0; p < kGRing; ++p) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_step(p, ring[p]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  constexpr int kPerStep = 16;  // vector-memory loads per step and wave
+  for (int s0 = 0; s0 < nsteps_pad; s0 += kGRing) {
+    if (s0 % kGChunk == 0) {  // uniform; see bwd_item for the protocol
+      wait_vm<(kGRing * kPerStep < 63 ? kGRing * kPerStep : 63)>();
+      __syncthreads();
+      const int c = s0 / kGChunk;
+      if ((c + 1) * kGChunk < nsteps_pad) copy_chunk(c + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint8_t* ab = abuf + ((s0 / kGChunk) & 1) * kGChunkBytes + lane * 16;
+#pragma unroll
+    for (int p = 0; p < kGRing; ++p) {
+      const int si = (s0 + p) % kGChunk;
+      GStep& r = ring[p];
+      // pin the step's loaded dwords here, so that nothing computed from them is scheduled into
+      // an earlier step (which would wait for this step's loads there)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        asm volatile("" : "+v"(r.w[q]));
+        asm volatile("" : "+v"(r.s[q]));
+      }
+      uint32_t wl[8];
+      float sf[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t sc = (r.s[q] >> ssh) & 0xFFu;
+        const bool dead = sc >= 253u;  // the row's block contributes zero
+        wl[q] = dead ? 0u : r.w[q] >> wsh;
+        sf[q] = bits_f((dead ? 127u : sc) << 23);
+      }
+      bf16x8 b[NC];
+      static_for<NC / 2>([&](auto pc) {
+        constexpr int P = decltype(pc)::value;
+        gdecode_pair<P>(wl, sf, b[2 * P], b[2 * P + 1]);
+      });
+      // every tile slot computes (a short part's empty slots work on copies of its first tile's
+      // rows and are never stored): no branch, so the A reads of the next tiles are issued while
+      // the MFMAs of the current ones run
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) {
+        const i32x4 ah = *reinterpret_cast<const i32x4*>(ab + ((si * T + tt) * 2) * kGUnit);
+        const i32x4 al = *reinterpret_cast<const i32x4*>(ab + ((si * T + tt) * 2 + 1) * kGUnit);
+#pragma unroll
+        for (int t = 0; t < NC; ++t) acc[tt][t] = mfma_bf16(__builtin_bit_cast(bf16x8, ah), b[t], acc[tt][t]);
+#pragma unroll
+        for (int t = 0; t < NC; ++t) acc[tt][t] = mfma_bf16(__builtin_bit_cast(bf16x8, al), b[t], acc[tt][t]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      load_step(s0 + p + kGRing, ring[p]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // epilogue: lane (n, g) holds rows 4g..4g+3 of columns col .. col + NC - 1 of every tile
+  const bool col_ok = stripe_ok && col < a.C;
+  auto epilogue = [&](auto ttc) {
+    constexpr int tt = decltype(ttc)::value;
+    const int r0 = row0[tt], nr = nrows[tt];
+    if (MODE == kBwdDownT) {
+      const int F = a.C;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = 4 * g + v;
+        const bool row_ok = i < nr;
+        const int p = r0 + (row_ok ? i : 0);
+        float dot = 0.f;
+        if (col_ok && row_ok) {
+          const float tw = a.row_w[p];
+          const float* sv = a.saved + (long long)p * 2 * F + col;
+          const float* rq = a.lora_rq ? a.lora_rq + (long long)a.a_row_map[p] * F + col : nullptr;
+          const long long o = (long long)p * 2 * F + col;
+#pragma unroll
+          for (int c4 = 0; c4 < NC / 4; ++c4) {
+            const f32x4 gt4 = *reinterpret_cast<const f32x4*>(sv + 4 * c4);
+            const f32x4 up4 = *reinterpret_cast<const f32x4*>(sv + F + 4 * c4);
+            f32x4 rq4 = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (rq) rq4 = *reinterpret_cast<const f32x4*>(rq + 4 * c4);
+            float dg[4], du[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float h = acc[tt][4 * c4 + e][v] + rq4[e];
+              dot += glu_fwd(gt4[e], up4[e], a.act_kind) * h;
+              glu_bwd(tw * h, gt4[e], up4[e], a.act_kind, dg[e], du[e]);
+            }
+            const uint32_t g0 = pack_bf16(dg[0], dg[1]), g1 = pack_bf16(dg[2], dg[3]);
+            const uint32_t u0 = pack_bf16(du[0], du[1]), u1 = pack_bf16(du[2], du[3]);
+            *reinterpret_cast<uint2*>(a.d_hi + o + 4 * c4) = uint2{g0, g1};
+            *reinterpret_cast<uint2*>(a.d_lo + o + 4 * c4) = uint2{
+                pack_bf16(dg[0] - bf16_lo(g0), dg[1] - bf16_hi(g0)), pack_bf16(dg[2] - bf16_lo(g1), dg[3] - bf16_hi(g1))};
+            *reinterpret_cast<uint2*>(a.d_hi + o + F + 4 * c4) = uint2{u0, u1};
+            *reinterpret_cast<uint2*>(a.d_lo + o + F + 4 * c4) = uint2{
+                pack_bf16(du[0] - bf16_lo(u0), du[1] - bf16_hi(u0)), pack_bf16(du[2] - bf16_lo(u1), du[3] - bf16_hi(u1))};
+          }
+        }
+        // the stripe's part of grad_w = <act, h>: the 16 lanes of the row group, then the waves
+        const float d = group16_sum(dot);
+        if (n == 0) red[(wave * T + tt) * 16 + i] = d;
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = 4 * g + v;
+        if (i < nr && col_ok) {
+          float* yr = a.y + (long long)(r0 + i) * a.ldy + col;
+#pragma unroll
+          for (int c4 = 0; c4 < NC / 4; ++c4) {
+            f32x4 o = f32x4{acc[tt][4 * c4][v], acc[tt][4 * c4 + 1][v], acc[tt][4 * c4 + 2][v], acc[tt][4 * c4 + 3][v]};
+            if (a.accumulate) o += *reinterpret_cast<const f32x4*>(yr + 4 * c4);
+            *reinterpret_cast<f32x4*>(yr + 4 * c4) = o;
+          }
+        }
+      }
+    }
+  };
+  static_for<T>(epilogue);
+  if (MODE == kBwdDownT) {
+    // grad_w partials per 256 columns: the waves of each 256-column part, in a fixed order
+    constexpr int kWavesPerPart = kBwdColsPerTile / kGS;
+    constexpr int kParts = kWaves / kWavesPerPart;
+    __syncthreads();
+    const int t = threadIdx.x;  // one (part, tile, row) per thread
+    if (t < kParts * T * 16) {
+      const int part = t / (T * 16), tt = (t / 16) % T, i = t & 15;
+      const int ct = cb * (kGCols / kBwdColsPerTile) + part;
+      if (tt < ntl && i < nrows[tt] && ct < a.n_ct) {
+        float d = 0.f;
+        for (int w = 0; w < kWavesPerPart; ++w) d += red[((part * kWavesPerPart + w) * T + tt) * 16 + i];
+        a.gw_part[(long long)(row0[tt] + i) * a.n_ct + ct] = d;
+      }
+    }
+  }
+}
+
+// Resident grid over the large-bucket items (group, part, column block), dealt round-robin over
+// the XCDs like the one-tile items, so launches with few or no groups cost almost nothing.
+template <int MODE>
+__global__ __launch_bounds__(64 * kWaves, MX_BWD_GPER_CU) void bwd_group_kernel(BwdArgs a)
+{
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * kGChunkBytes];
+  __shared__ float red[kWaves * kGT * 16];
+  const int ng = *(cint_ptr)a.n_groups;
+  const int ncb = (a.C + kGCols - 1) / kGCols;
+  const int total = ng * kGParts * ncb;
+  const int per_xcd = (total + 7) >> 3;
   bool busy = false;
   for (int it = 0;; ++it) {
-    const int st = decode_work<T>(a, it, w);
-    if (st == 0) break;
-    if (st == 2) continue;
-    if (busy) __syncthreads();  // every wave has finished reading the previous item's A chunks
-    bwd_item<MODE, T>(a, w, abuf);
+    const int slot = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
+    const int item = (int)(blockIdx.x & 7) * per_xcd + slot;
+    if (slot >= per_xcd || item >= total) break;
+    const int gp = item / ncb, cb = item - gp * ncb;
+    const int gi = gp / kGParts, part = gp - gi * kGParts;
+    const cint_ptr gg = (cint_ptr)(a.groups + gi);
+    const int ntl = gg[2] - part * kGT;
+    if (ntl <= 0) continue;  // the empty part of a short group
+    if (busy) __syncthreads();  // every wave has finished reading the previous item's LDS
+    bwd_group_item<MODE>(a, gg[0], gg[1] + part * kGT, min(ntl, kGT), cb, abuf, red);
     busy = true;
   }
 }
@@ -455,7 +741,8 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
   // the epilogue's 16-byte accesses of rows assume these (true for every caller: C is a multiple
   // of 32 and the row strides are multiples of 16 elements)
   if (a.C % 32 || (a.y && a.ldy % 4) || a.lda % 8) return hipErrorInvalidValue;
-  const bool split = a.tiles && a.small_tiles && a.groups;
+  // large buckets take the grouped kernel when their scale rows are whole dwords
+  const bool split = a.tiles && a.small_tiles && a.groups && a.C % 128 == 0;
   BwdArgs b = a;
   if (!split) {
     b.small_tiles = nullptr;
@@ -463,18 +750,17 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
   }
   const long long blocks = (total + 7) / 8 * 8;
   dim3 grid((unsigned)blocks), block(64 * kWaves);
-  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, 1>), grid, block, 0, s, b);
-  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, 1>), grid, block, 0, s, b);
-  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, 1>), grid, block, 0, s, b);
+  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain>), grid, block, 0, s, b);
+  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT>), grid, block, 0, s, b);
+  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT>), grid, block, 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !split) return e;
-  // groups come from experts of at least kGroupMinTiles tiles: at most max_tiles / 2 of them,
-  // each split into kGroupTiles / kBwdGroupT work items
-  const long long gtotal = ((long long)max_tiles / 2 + 1) * (kGroupTiles / kBwdGroupT) * n_ct4;
-  dim3 ggrid((unsigned)std::min<long long>((gtotal + 7) / 8 * 8, resident_groups(1)));
-  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, kBwdGroupT>), ggrid, block, 0, s, b);
-  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, kBwdGroupT>), ggrid, block, 0, s, b);
-  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, kBwdGroupT>), ggrid, block, 0, s, b);
+  // groups come from experts of at least kGroupMinTiles tiles: at most max_tiles / kGroupMinTiles + 1
+  const long long gtotal = ((long long)max_tiles / kGroupMinTiles + 1) * kGParts * ((a.C + kGCols - 1) / kGCols);
+  dim3 ggrid((unsigned)std::min<long long>((gtotal + 7) / 8 * 8, resident_groups(MX_BWD_GPER_CU)));
+  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_group_kernel<kBwdPlain>), ggrid, block, 0, s, b);
+  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_group_kernel<kBwdDownT>), ggrid, block, 0, s, b);
+  else hipLaunchKernelGGL((bwd_group_kernel<kBwdGateUpT>), ggrid, block, 0, s, b);
   return hipGetLastError();
 }
 

@@ -581,11 +581,11 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
 }
 
 // ---------------------------------------------------------------- large buckets
-// An expert with many rows would re-read each weight byte once per 16-row tile. Its tiles are
-// processed in groups of up to four: a work-group takes one column tile of the group, wave w
-// takes row tile w, and the column tile's weights go through LDS once per super-chunk for all
-// four waves (64 weight rows x 256 B of codes, plus 16 B of scales per row). Each wave streams
-// its own tile's activations from memory one super-chunk ahead.
+// An expert with many rows would re-read each weight byte once per 16-row tile. Its tiles come
+// in groups of up to eight, processed four at a time: a work-group takes one column tile of four
+// of a group's tiles, wave w takes row tile w, and the column tile's weights go through LDS once
+// per super-chunk for all four waves (64 weight rows x 256 B of codes, plus 16 B of scales per
+// row). Each wave streams its own tile's activations from memory one super-chunk ahead.
 //
 // LDS layout of the codes: row rr (0..63, = column group * 16 + row in group) holds its 16
 // 16-byte units at unit rr * 16 + (u ^ (rr & 7)); the XOR spreads the eight rows read together
@@ -600,26 +600,32 @@ struct GroupLds {
   uint8_t b[2][kGrpLdsBytes];
 };
 
-__device__ __forceinline__ bool decode_group(const FwdArgs& a, int wave, int it, WorkItem& w)
+// Item `it` of this work-group: (group, part of four of its up to kGroupTiles tiles, column
+// tile). Returns 0 when there is none left, 2 for the empty part of a short group, 1 for an item.
+constexpr int kGrpParts = kGroupTiles / kWavesPerGroup;
+
+__device__ __forceinline__ int decode_group(const FwdArgs& a, int wave, int it, WorkItem& w)
 {
   const int ng = *(cint_ptr)a.n_groups;
-  const int total = ng * a.n_ct;
+  const int total = ng * kGrpParts * a.n_ct;
   const int per_xcd = (total + 7) >> 3;
   const int k = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
   const int item = (int)(blockIdx.x & 7) * per_xcd + k;
-  if (k >= per_xcd || item >= total) return false;
-  const int gi = item / a.n_ct;
-  w.ct = item - gi * a.n_ct;
+  if (k >= per_xcd || item >= total) return 0;
+  const int gp = item / a.n_ct;
+  w.ct = item - gp * a.n_ct;
   w.ct0 = w.ct;
+  const int gi = gp / kGrpParts, part = gp - gi * kGrpParts;
   const cint_ptr gg = (cint_ptr)(a.groups + gi);
   w.expert = gg[0];
-  const int t0 = gg[1], nt = gg[2];
+  const int t0 = gg[1] + part * kWavesPerGroup, nt = gg[2] - part * kWavesPerGroup;
+  if (nt <= 0) return 2;
   w.active = wave < nt;
   w.tile = t0 + (w.active ? wave : 0);
   const cint_ptr tt = (cint_ptr)(a.tiles + w.tile);
   w.row0 = tt[1];
   w.nrows = tt[2];
-  return true;
+  return 1;
 }
 
 template <int MODE>
@@ -733,11 +739,16 @@ __global__ __launch_bounds__(256, 2) void fwd_group_kernel(FwdArgs a)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   WorkItem w;
-  for (int it = 0; decode_group(a, wave, it, w); ++it) {
-    if (it > 0) __syncthreads();  // every wave is done with the previous item's LDS buffers
+  bool busy = false;
+  for (int it = 0;; ++it) {
+    const int st = decode_group(a, wave, it, w);
+    if (st == 0) break;
+    if (st == 2) continue;
+    if (busy) __syncthreads();  // every wave is done with the previous item's LDS buffers
     int l = lane;
     asm volatile("" : "+v"(l));
     fwd_group_item<MODE>(a, w, wave, l);
+    busy = true;
   }
 }
 
