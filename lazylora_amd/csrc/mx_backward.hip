@@ -124,16 +124,6 @@ MX_DEV void decode_pair(const StepRaw& r, const float (&sf)[8], bf16x8& b0, bf16
   b1 = __builtin_bit_cast(bf16x8, i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]});
 }
 
-// f(integral_constant<int, i>) for i = 0 .. N-1
-template <int N, int I = 0, typename Fn>
-MX_DEV void static_for(Fn&& f)
-{
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<N, I + 1>(f);
-  }
-}
-
 // Ring depth (steps of weights in flight per wave, each 4 KiB per wave) and A chunk (steps whose
 // A operands one LDS buffer holds: kChunk x T tiles x 2 terms x 1 KiB). T > 1 items do T times
 // the matrix work per step, so a shorter ring hides the loads. kChunk is a multiple of kRing.
@@ -411,8 +401,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void bwd_kernel(BwdArgs a)
 
 // ---------------------------------------------------------------- large buckets
 // An expert with many rows would stream (and decode) its weights once per row tile. Its tiles
-// come in groups of up to kGroupTiles (8) consecutive tiles; a work item is GT of them (a part of
-// a group) x a block of 4 GS columns: every wave decodes a GS-column stripe of each 32-row step
+// come in groups of up to kGroupTiles (4) consecutive tiles; a work item is GT of them (a part of
+// a group when GT is smaller) x a block of 4 GS columns: every wave decodes a GS-column stripe of each 32-row step
 // once and applies it to all GT row tiles, and the item's A operands (GT tiles x hi/lo, 2 GT KiB
 // per step) come through LDS for the four waves. Each weight byte is read once per 16 GT rows
 // instead of once per 16, and each A fragment read from LDS feeds GS / 16 MFMAs.

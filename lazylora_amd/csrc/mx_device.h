@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -212,6 +214,16 @@ MX_DEV i32x4 buf16(rsrc_t r, uint32_t voff, uint32_t soff)
 MX_DEV i32x4 buf16_nt(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2); }
 MX_DEV uint8_t buf8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0); }
 
+// f(integral_constant<int, i>) for i = 0 .. N-1
+template <int N, int I = 0, typename Fn>
+MX_DEV void static_for(Fn&& f)
+{
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
 // Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes from src land at
 // lds + 16 l. lds must be the same for the whole wave. Completion is counted by vmcnt.
 MX_DEV void dma16(const void* src, void* lds)
@@ -235,6 +247,13 @@ MX_DEV void dma4_async(const void* src, void* lds)
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory");
 }
+// Mark registers as redefined here (no instruction). After an explicit wait_vm that has already
+// completed the loads behind them, this keeps the compiler from placing its own wait for those
+// loads further down, where copies it does not know of (dma16_async) would be counted as well
+// and the wait would hold for later loads too.
+MX_DEV void pin(i32x4& x) { asm volatile("" : "+v"(x)); }
+MX_DEV void pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
+
 // Wait until at most N vector-memory operations of this wave are outstanding (they retire in
 // issue order, so everything but the last N issued is complete).
 template <int N>

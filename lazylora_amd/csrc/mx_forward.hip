@@ -479,6 +479,11 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
                                   *reinterpret_cast<const uint32_t*>(ls + 256 + lane * 4)}
                           : *reinterpret_cast<const uint2*>(ls + lane * 8);
       wait_lgkm0();
+      // chunk c's weights are complete (wait_vm above)
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pin(cur[grp][q]);
       __builtin_amdgcn_sched_barrier(0);
       if (c + 1 < nsc) {
         issue_a(c + 1, (c + 1) & 1);
@@ -582,10 +587,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
 
 // ---------------------------------------------------------------- large buckets
 // An expert with many rows would re-read each weight byte once per 16-row tile. Its tiles come
-// in groups of up to eight, processed four at a time: a work-group takes one column tile of four
-// of a group's tiles, wave w takes row tile w, and the column tile's weights go through LDS once
-// per super-chunk for all four waves (64 weight rows x 256 B of codes, plus 16 B of scales per
-// row). Each wave streams its own tile's activations from memory one super-chunk ahead.
+// in groups of up to kGroupTiles (4): a work-group takes one column tile of a group's tiles, wave
+// w takes row tile w, and the column tile's weights go through LDS once per super-chunk for all
+// four waves (64 weight rows x 256 B of codes, plus 16 B of scales per row). Each wave streams its
+// own tile's activations from memory one super-chunk ahead.
 //
 // LDS layout of the codes: row rr (0..63, = column group * 16 + row in group) holds its 16
 // 16-byte units at unit rr * 16 + (u ^ (rr & 7)); the XOR spreads the eight rows read together

@@ -102,7 +102,7 @@ struct BwdArgs {
 };
 
 constexpr int kFwdRowsPerTile = 16;
-constexpr int kGroupTiles = 8;     // row tiles of one large-bucket group
+constexpr int kGroupTiles = 4;     // row tiles of one large-bucket group
 constexpr int kGroupMinTiles = 4;  // experts with at least this many tiles take the large-bucket path
 constexpr int kFwdColsPerTile = 64;  // kFwdPlain / kFwdDown; kFwdGateUp covers 32 features
 constexpr int kBwdColsPerTile = 256;  // output columns of one transposed-product wave
