@@ -357,10 +357,15 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
               const int b = 4 * h2;
-              *reinterpret_cast<i32x4*>(a.d_hi + o + 8 * h2) = i32x4{(int)dh[b], (int)dh[b + 1], (int)dh[b + 2], (int)dh[b + 3]};
-              *reinterpret_cast<i32x4*>(a.d_lo + o + 8 * h2) = i32x4{(int)dl[b], (int)dl[b + 1], (int)dl[b + 2], (int)dl[b + 3]};
-              *reinterpret_cast<i32x4*>(a.d_hi + o + F + 8 * h2) = i32x4{(int)uh[b], (int)uh[b + 1], (int)uh[b + 2], (int)uh[b + 3]};
-              *reinterpret_cast<i32x4*>(a.d_lo + o + F + 8 * h2) = i32x4{(int)ul[b], (int)ul[b + 1], (int)ul[b + 2], (int)ul[b + 3]};
+              // non-temporal: measured faster than write-back stores for these rows
+              auto st = [&](const uint32_t* v, uint16_t* dst) {
+                __builtin_nontemporal_store(i32x4{(int)v[b], (int)v[b + 1], (int)v[b + 2], (int)v[b + 3]},
+                                            reinterpret_cast<i32x4*>(dst));
+              };
+              st(dh, a.d_hi + o + 8 * h2);
+              st(dl, a.d_lo + o + 8 * h2);
+              st(uh, a.d_hi + o + F + 8 * h2);
+              st(ul, a.d_lo + o + F + 8 * h2);
             }
           }
         }
@@ -402,9 +407,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void bwd_kernel(BwdArgs a)
 // ---------------------------------------------------------------- large buckets
 // An expert with many rows would stream (and decode) its weights once per row tile. Its tiles
 // come in groups of up to kGroupTiles (4) consecutive tiles; a work item is GT of them (a part of
-// a group when GT is smaller) x a block of 4 GS columns: every wave decodes a GS-column stripe of each 32-row step
-// once and applies it to all GT row tiles, and the item's A operands (GT tiles x hi/lo, 2 GT KiB
-// per step) come through LDS for the four waves. Each weight byte is read once per 16 GT rows
+// a group when GT is smaller) x a block of 4 GS columns: every wave decodes a GS-column stripe of
+// each 32-row step once and applies it to all GT row tiles, and the item's A operands (GT tiles x
+// hi/lo, 2 GT KiB per step) come through LDS for the four waves. Each weight byte is read once per 16 GT rows
 // instead of once per 16, and each A fragment read from LDS feeds GS / 16 MFMAs.
 //
 // Lane (n, g) of a wave holds columns (GS / 16) n .. + GS / 16 - 1 of its stripe, whose weights
@@ -636,12 +641,14 @@ __device__ __forceinline__ void bwd_group_item(const BwdArgs& a, int expert, int
             }
             const uint32_t g0 = pack_bf16(dg[0], dg[1]), g1 = pack_bf16(dg[2], dg[3]);
             const uint32_t u0 = pack_bf16(du[0], du[1]), u1 = pack_bf16(du[2], du[3]);
-            *reinterpret_cast<uint2*>(a.d_hi + o + 4 * c4) = uint2{g0, g1};
-            *reinterpret_cast<uint2*>(a.d_lo + o + 4 * c4) = uint2{
-                pack_bf16(dg[0] - bf16_lo(g0), dg[1] - bf16_hi(g0)), pack_bf16(dg[2] - bf16_lo(g1), dg[3] - bf16_hi(g1))};
-            *reinterpret_cast<uint2*>(a.d_hi + o + F + 4 * c4) = uint2{u0, u1};
-            *reinterpret_cast<uint2*>(a.d_lo + o + F + 4 * c4) = uint2{
-                pack_bf16(du[0] - bf16_lo(u0), du[1] - bf16_hi(u0)), pack_bf16(du[2] - bf16_lo(u1), du[3] - bf16_hi(u1))};
+            __builtin_nontemporal_store(u32x2{g0, g1}, reinterpret_cast<u32x2*>(a.d_hi + o + 4 * c4));
+            __builtin_nontemporal_store(u32x2{pack_bf16(dg[0] - bf16_lo(g0), dg[1] - bf16_hi(g0)),
+                                               pack_bf16(dg[2] - bf16_lo(g1), dg[3] - bf16_hi(g1))},
+                                        reinterpret_cast<u32x2*>(a.d_lo + o + 4 * c4));
+            __builtin_nontemporal_store(u32x2{u0, u1}, reinterpret_cast<u32x2*>(a.d_hi + o + F + 4 * c4));
+            __builtin_nontemporal_store(u32x2{pack_bf16(du[0] - bf16_lo(u0), du[1] - bf16_hi(u0)),
+                                               pack_bf16(du[2] - bf16_lo(u1), du[3] - bf16_hi(u1))},
+                                        reinterpret_cast<u32x2*>(a.d_lo + o + F + 4 * c4));
           }
         }
         // the stripe's part of grad_w = <act, h>: the 16 lanes of the row group, then the waves

@@ -174,7 +174,8 @@ struct ASrc {
 // Epilogue of the fast path. The four waves stage the work-group's outputs in the (now idle)
 // activation buffers of LDS, then write them with 16-byte stores that cover whole runs of
 // memory: scattered 1-byte and 4-byte stores of the same data cost the weight stream about a
-// tenth of its bandwidth. Lane (j, g) holds rows 4g+v (v = 0..3) of columns grp*16 + j.
+// tenth of its bandwidth. The stores are non-temporal (streamed past the caches), which costs the
+// weight stream less than ordinary write-back stores. Lane (j, g) holds rows 4g+v (v = 0..3) of columns grp*16 + j.
 constexpr int kStagePitch = 260;  // floats per staged row: 256 + 4 keeps the row starts on distinct banks
 
 template <int MODE>
@@ -240,8 +241,8 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
     uint8_t* qbase = a.q_tiles + (long long)w.tile * at_tile_bytes(F) + (long long)c * kAtChunkBytes;
     {
       const int run = t >> 5, off = (t & 31) * 16;  // run = q * 2 + plane: 512 B each
-      *reinterpret_cast<i32x4*>(qbase + (run * 2 + (gl >> 1)) * 1024 + (gl & 1) * 512 + off) =
-          *reinterpret_cast<const i32x4*>(sq + run * 512 + off);
+      __builtin_nontemporal_store(*reinterpret_cast<const i32x4*>(sq + run * 512 + off),
+                                  reinterpret_cast<i32x4*>(qbase + (run * 2 + (gl >> 1)) * 1024 + (gl & 1) * 512 + off));
       if (t < 8)
         *reinterpret_cast<i32x4*>(qbase + kAtCodeBytes + gl * 128 + t * 16) =
             *reinterpret_cast<const i32x4*>(sq + 4096 + t * 16);
@@ -252,8 +253,8 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
       for (int it = 0; it < 4; ++it) {
         const int r = it * 4 + wave;
         if (r < w.nrows && f < F)
-          *reinterpret_cast<f32x4*>(a.save + (long long)(w.row0 + r) * 2 * F + part * F + f) =
-              *reinterpret_cast<const f32x4*>(ss + r * kStagePitch + part * 128 + idx);
+          __builtin_nontemporal_store(*reinterpret_cast<const f32x4*>(ss + r * kStagePitch + part * 128 + idx),
+                                      reinterpret_cast<f32x4*>(a.save + (long long)(w.row0 + r) * 2 * F + part * F + f));
       }
     }
     return;
@@ -277,7 +278,7 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
     const f32x4 val = *reinterpret_cast<const f32x4*>(ss + r * kStagePitch + lane * 4);
     float* yr = a.y + (long long)(w.row0 + r) * a.ldy;
     if (vec && col + 4 <= a.R) {
-      *reinterpret_cast<f32x4*>(yr + col) = val;
+      __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(yr + col));
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
