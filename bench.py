@@ -16,9 +16,9 @@ repo's C restatement of the reference CPU path timed on a bounded sample of the 
 
     python bench.py [--steps 20] [--warmup 3] [--routing uniform|zipf] [--no-cpu] [--no-extra]
 
-The default run also times the Zipf-skewed routing of the same layer (key "zipf") and config 2 at
-M = 1 and M = 256 tokens per expert (key "config2"), each in its own timed region after the
-headline's.
+The default run also times the Zipf-skewed routing of the same layer (key "zipf"), config 2 at
+M = 1 and M = 256 tokens per expert (key "config2") and a 12-layer sample of config 5's
+out-of-core sweep (key "config5_sample"), each in its own timed region after the headline's.
 """
 import argparse
 import json
@@ -228,26 +228,26 @@ def expert_main(args, k):
     print(json.dumps(line), flush=True)
 
 
-def stream_main(args, k):
+def stream_sweep(args, k, layers, ring, routing):
     """Config 5: an out-of-core sweep of `layers` routed-expert layers of the config-3 shape, each
     copied from pinned host memory (a ring of `ring` distinct layers, as 93 x 20.96 GB cannot be
     pinned) into one of two HBM slots on a copy stream while the compute stream runs the layer
-    forward for 1024 tokens on the previous slot."""
+    forward for 1024 tokens on the previous slot. Returns the sweep's timings."""
     from lazylora_amd.streaming import LayerStreamer, host_layer_from
     t_setup = time.time()
     hosts = []
-    for r in range(args.ring):
+    for r in range(ring):
         layer = make_layer(r)
         hosts.append(host_layer_from(layer, pin=True))
         del layer
         torch.cuda.empty_cache()
-    H, I, W, _ = make_inputs(1, args.routing)
+    H, I, W, _ = make_inputs(1, routing)
     ws = torch.empty(k.moe_workspace_bytes(N, TOPK, E, D, F), dtype=torch.uint8, device="cuda")
     streamer = LayerStreamer(E, D, F, slots=2, timing=True)
-    log(f"[bench] stream: {args.ring} pinned host layers of {hosts[0].nbytes / 1e9:.2f} GB, setup "
+    log(f"[bench] stream: {ring} pinned host layers of {hosts[0].nbytes / 1e9:.2f} GB, setup "
         f"{time.time() - t_setup:.1f}s")
     # one warm sweep of a few layers (first-touch of the slots and the workspace)
-    for _, layer in streamer.stream(hosts[i % args.ring] for i in range(min(3, args.layers))):
+    for _, layer in streamer.stream(hosts[i % ring] for i in range(min(3, layers))):
         k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
     torch.cuda.synchronize()
     streamer.copy_events.clear()
@@ -255,7 +255,7 @@ def stream_main(args, k):
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for i, layer in streamer.stream(hosts[i % args.ring] for i in range(args.layers)):
+    for i, layer in streamer.stream(hosts[i % ring] for i in range(layers)):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
@@ -270,6 +270,17 @@ def stream_main(args, k):
     copy_ms, copy_bytes = streamer.copy_stats()
     t_copy = copy_ms / 1e3
     hidden = max(0.0, min(1.0, (t_copy + t_comp - t_total) / t_comp)) if t_comp > 0 else 0.0
+    del hosts, streamer, ws
+    torch.cuda.empty_cache()
+    return {"total_s": t_total, "compute_s": t_comp, "copy_s": t_copy, "copy_bytes": copy_bytes,
+            "hidden_compute_fraction": hidden}
+
+
+def stream_main(args, k):
+    """Config 5 as the bench line (`--workload stream`): the full sweep of args.layers layers."""
+    r = stream_sweep(args, k, args.layers, args.ring, args.routing)
+    t_total, t_comp, t_copy, copy_bytes, hidden = (r["total_s"], r["compute_s"], r["copy_s"], r["copy_bytes"],
+                                                   r["hidden_compute_fraction"])
     h2d = copy_bytes / t_copy / 1e9
     line = {
         "metric": "config 5 out-of-core sweep: tokens/s through all layers (H2D-bound)",
@@ -376,6 +387,18 @@ def main():
                                             "weight_GBps_products": r["weight_GBps_products"],
                                             "TFLOPs_products": r["TFLOPs_products"]} for r in sweep}
         extra["config2"]["expert_copies_per_launch"] = copies
+        # config 5 on a sample of its sweep: 12 of the 93 layers streamed
+        # from pinned host memory; the full sweep is `--workload stream`
+        n5 = 12
+        r5 = stream_sweep(args, k, n5, 2, args.routing)
+        per_layer = r5["total_s"] / n5
+        extra["config5_sample"] = {
+            "layers_streamed": n5, "s_per_layer": per_layer,
+            "tokens_per_s_93_layers": N / (93 * per_layer),
+            "h2d_GBps": r5["copy_bytes"] / r5["copy_s"] / 1e9,
+            "hidden_compute_fraction": r5["hidden_compute_fraction"],
+            "note": "a 93-layer sweep costs 93 x s_per_layer (the sweep is H2D-bound, so the per-layer time "
+                    "does not depend on the layer count)"}
 
     cpu = None
     if not args.no_cpu:
