@@ -149,6 +149,32 @@ def test_large_bucket_groups(k, topk):
     assert_close(gw.cpu().numpy(), gw64, "groups grad_w")
 
 
+@pytest.mark.parametrize("D,F", [(640, 384), (1024, 352)])
+def test_large_bucket_ragged_columns(k, D, F):
+    """Large buckets with output widths that leave the grouped transposed products partial
+    column blocks (640 and 384: a 512-column item whose last stripes lie past the end) or send
+    them to the one-tile work-groups (352, not a multiple of 128)."""
+    case(f"large buckets, ragged widths: E=4, D={D}, F={F}, top-1")
+    rng = np.random.default_rng(D + F)
+    E = 4
+    ex = oracle.random_experts(rng, E, D, F, 118, 122)
+    sizes = [150, 70, 20, 3]
+    idx = np.concatenate([np.full(c, e) for e, c in enumerate(sizes)]).astype(np.int64)
+    rng.shuffle(idx)
+    N = idx.size
+    idx = idx[:, None]
+    w = rng.uniform(0.5, 1.5, (N, 1)).astype(np.float32)
+    h = rng.standard_normal((N, D)).astype(np.float32)
+    g = rng.standard_normal((N, D)).astype(np.float32)
+    L = layer_of(ex)
+    H, I, W, G = (torch.from_numpy(a).cuda() for a in (h, idx, w, g))
+    assert_close(k.routed_forward(H, I, W, L).cpu().numpy(), oracle.routed_forward(h, idx, w, ex), "ragged fwd")
+    gh, gw = k.routed_backward(H, I, W, L, G)
+    gh64, gw64 = oracle.routed_backward(h, idx, w, ex, g)
+    assert_close(gh.cpu().numpy(), gh64, "ragged grad_h")
+    assert_close(gw.cpu().numpy(), gw64, "ragged grad_w")
+
+
 def test_input_dtypes(k):
     """bf16 h gives the fp32 result of the same (bf16-representable) values; int32 ids = int64."""
     case("bf16 h, int32 topk ids")
