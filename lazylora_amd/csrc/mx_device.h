@@ -240,6 +240,17 @@ MX_DEV void dma16_async(const void* src, void* lds)
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
 }
+// The same copy with a uniform 64-bit base and a per-lane 32-bit byte offset (the saddr form:
+// one VGPR per address instead of two).
+MX_DEV void dma16_async_s(const void* base, uint32_t voff, void* lds)
+{
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)b), bhi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint64_t bs = ((uint64_t)bhi << 32) | blo;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "s"(m0) : "memory");
+}
 // The 4-byte form (global_load_lds_dword): lane l's 4 bytes land at lds + 4 l.
 MX_DEV void dma4_async(const void* src, void* lds)
 {

@@ -588,173 +588,215 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
 
 // ---------------------------------------------------------------- large buckets
 // An expert with many rows would re-read each weight byte once per 16-row tile. Its tiles come
-// in groups of up to kGroupTiles (4): a work-group takes one column tile of a group's tiles, wave
-// w takes row tile w, and the column tile's weights go through LDS once per super-chunk for all
-// four waves (64 weight rows x 256 B of codes, plus 16 B of scales per row). Each wave streams its
-// own tile's activations from memory one super-chunk ahead.
+// in groups of up to kGroupTiles (4). A work item is one group (up to 64 rows) x eight column
+// tiles (wave w takes column tile 8 fb + w: 512 weight rows in all); a work-group of eight waves
+// holds the CU's LDS alone. Both operands go through LDS one K-quarter (one MFMA's 128 K) at a
+// time: per quarter the work-group copies the 16 KiB of activations of its four tiles and the
+// 32 KiB of weight codes of its 512 rows, three quarters deep (the one being read and two in
+// flight), and each wave issues 4 tiles x 4 column groups x 2 terms = 32 MFMAs against them.
+// Every weight byte is read once per group and every activation byte once per 512 weight rows.
 //
-// LDS layout of the codes: row rr (0..63, = column group * 16 + row in group) holds its 16
-// 16-byte units at unit rr * 16 + (u ^ (rr & 7)); the XOR spreads the eight rows read together
-// by one 128-bit LDS instruction over all 32 banks. The copies place units with LDS DMA, which
-// writes a wave's 64 lanes to one contiguous KiB, so the swizzle is applied to the source
-// addresses: LDS unit p of an instruction fetches unit (p % 16) ^ (rr & 7) of row rr.
-constexpr int kGrpRows = 64;
-constexpr int kGrpCodeBytes = kGrpRows * 256;
-constexpr int kGrpLdsBytes = kGrpCodeBytes + kGrpRows * 16;
-
-struct GroupLds {
-  uint8_t b[2][kGrpLdsBytes];
+// Block order: MFMA q of super-chunk c takes blocks 16c + 4q .. 16c + 4q + 3 (lane group g takes
+// block 4q + g), not the one-tile kernels' 16c + 4g + q. The quarter's weight bytes of a row are
+// then one contiguous 64 B (half a cache line, whose other half the next quarter takes) instead
+// of four 16 B pieces spread over two lines, each line requested again by all four quarters.
+// The activations keep the AT layout: a quarter's operand is gathered from it in 256 B runs
+// (every run fetched once per item), and the scale bytes of blocks 4q + g, q = 0..3, are packed
+// into one register per lane at the first quarter of each super-chunk.
+constexpr int kGmT = 4;                        // row tiles per item
+constexpr int kGmWaves = 8;                    // column tiles per item
+constexpr int kGmRows = kGmWaves * 64;         // weight rows per item
+constexpr int kGmA = kGmT * 4096;              // A bytes per quarter: [tile][plane][piece][lane][16 B]
+constexpr int kGmW = kGmRows * 64;             // W bytes per quarter: [row][block][16 B]
+constexpr int kGmRing = 3;                     // quarters in LDS: the one read and two in flight
+struct GemmLds {
+  uint8_t q[kGmRing][kGmA + kGmW];             // quarter buffers
+  uint8_t sw[kGmRows * 16];                    // weight scales of a super-chunk: [row][16 B]
+  uint8_t sa[kGmT * 512];                      // activation scales of a super-chunk: [tile][512 B]
 };
 
-// Item `it` of this work-group: (group, part of four of its up to kGroupTiles tiles, column
-// tile). Returns 0 when there is none left, 2 for the empty part of a short group, 1 for an item.
-constexpr int kGrpParts = kGroupTiles / kWavesPerGroup;
-
-__device__ __forceinline__ int decode_group(const FwdArgs& a, int wave, int it, WorkItem& w)
-{
-  const int ng = *(cint_ptr)a.n_groups;
-  const int total = ng * kGrpParts * a.n_ct;
-  const int per_xcd = (total + 7) >> 3;
-  const int k = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
-  const int item = (int)(blockIdx.x & 7) * per_xcd + k;
-  if (k >= per_xcd || item >= total) return 0;
-  const int gp = item / a.n_ct;
-  w.ct = item - gp * a.n_ct;
-  w.ct0 = w.ct;
-  const int gi = gp / kGrpParts, part = gp - gi * kGrpParts;
-  const cint_ptr gg = (cint_ptr)(a.groups + gi);
-  w.expert = gg[0];
-  const int t0 = gg[1] + part * kWavesPerGroup, nt = gg[2] - part * kWavesPerGroup;
-  if (nt <= 0) return 2;
-  w.active = wave < nt;
-  w.tile = t0 + (w.active ? wave : 0);
-  const cint_ptr tt = (cint_ptr)(a.tiles + w.tile);
-  w.row0 = tt[1];
-  w.nrows = tt[2];
-  return 1;
-}
-
 template <int MODE>
-__device__ __forceinline__ void fwd_group_item(const FwdArgs& a, const WorkItem& w, int wave, int lane)
+__device__ __forceinline__ void fwd_gemm_item(const FwdArgs& a, int expert, int t0, int ntl, int fb, int wave,
+                                              int lane, GemmLds& lds)
 {
-  __shared__ GroupLds lds;
-  const int j = lane & 15, g = lane >> 4;
+  constexpr int T = kGmT;
+  const int g = lane >> 4;
   const int nb = a.K / kGroup;
   const int nsc = at_nchunks(a.K);
-  const uint8_t* const at_tile = a.a_tiles + (long long)w.tile * at_tile_bytes(a.K);
 
-  auto grp_row = [&](int grp) {
-    return MODE == kFwdGateUp ? w.ct * 32 + (grp & 1) * 16 : w.ct * kFwdColsPerTile + grp * 16;
-  };
-  auto grp_wp = [&](int grp) {
-    return (MODE == kFwdGateUp && grp >= 2 ? a.wp1 : a.wp0) + (long long)w.expert * a.wp_estride;
-  };
-  auto grp_ws = [&](int grp) {
-    return (MODE == kFwdGateUp && grp >= 2 ? a.ws1 : a.ws0) + (long long)w.expert * a.ws_estride;
-  };
-
-  // B(c) -> lds.b[buf]: instruction u of wave `wave` covers rows 4 (4 wave + u) .. +3; wave 0
-  // also copies the 64 rows' 16 scale bytes of the chunk
-  auto issue_b = [&](int c, int buf) {
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
+  WorkItem w[T];  // slots past the group's end repeat its last tile and are not stored
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int rr = (4 * wave + u) * 4 + (ln >> 4);
-      const int grp = rr >> 4;
-      const int n = min(grp_row(grp) + (rr & 15), a.R - 1);
-      const uint32_t off = (uint32_t)(n * (a.K / 2) + c * 256 + (((ln & 15) ^ (rr & 7)) << 4));
-      dma16(grp_wp(grp) + off, &lds.b[buf][(4 * wave + u) * 1024]);
-    }
-    if (wave == 0) {
-      const int grp = ln >> 4;
-      const int n = min(grp_row(grp) + (ln & 15), a.R - 1);
-      dma16(grp_ws(grp) + (uint32_t)(n * nb + c * 16), &lds.b[buf][kGrpCodeBytes]);
-    }
-  };
-  struct AChunk {
-    i32x4 v[16];
-    uint2 s;
-  };
-  auto load_a = [&](int c, AChunk& x) {
-    const uint8_t* p = at_tile + (long long)c * kAtChunkBytes + lane * 16;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int h = 0; h < 4; ++h) x.v[4 * q + h] = ldg16(p + q * 4096 + h * 1024);
-    x.s = *reinterpret_cast<const uint2*>(at_tile + (long long)c * kAtChunkBytes + kAtCodeBytes + lane * 8);
-  };
-
-  f32x4 acc[4];
-#pragma unroll
-  for (int grp = 0; grp < 4; ++grp) acc[grp] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float tw[4];
-  if (MODE == kFwdDown)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) tw[v] = a.row_w[w.row0 + min(4 * g + v, w.nrows - 1)];
-
-  auto step = [&](int c, AChunk& cur, AChunk& nxt) {
-    wait_vm0();
-    __syncthreads();
-    const uint8_t* lb = lds.b[c & 1];
-    i32x4 b[4][4];
-    uint32_t sb[4];
-#pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-      const int rr = grp * 16 + j;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        b[grp][q] = *reinterpret_cast<const i32x4*>(lb + (rr * 16 + ((g * 4 + q) ^ (rr & 7))) * 16);
-      sb[grp] = *reinterpret_cast<const uint32_t*>(lb + kGrpCodeBytes + rr * 16 + g * 4);
-    }
-    wait_lgkm0();
-    __builtin_amdgcn_sched_barrier(0);
-    if (c + 1 < nsc) {
-      issue_b(c + 1, (c + 1) & 1);
-      if (w.active) load_a(c + 1, nxt);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (w.active) {
-      sanitize(b, sb);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const i32x8 ah = cat8(cur.v[4 * q], cur.v[4 * q + 1]), al = cat8(cur.v[4 * q + 2], cur.v[4 * q + 3]);
-        if (q == 0) mfma_step<0>(acc, ah, al, b, sb, (int)cur.s.x, (int)cur.s.y);
-        if (q == 1) mfma_step<1>(acc, ah, al, b, sb, (int)cur.s.x, (int)cur.s.y);
-        if (q == 2) mfma_step<2>(acc, ah, al, b, sb, (int)cur.s.x, (int)cur.s.y);
-        if (q == 3) mfma_step<3>(acc, ah, al, b, sb, (int)cur.s.x, (int)cur.s.y);
-      }
-    }
-  };
-
-  AChunk a0, a1;
-  issue_b(0, 0);
-  if (w.active) load_a(0, a0);
-  for (int c = 0;;) {
-    step(c, a0, a1);
-    if (++c >= nsc) break;
-    step(c, a1, a0);
-    if (++c >= nsc) break;
+  for (int tt = 0; tt < T; ++tt) {
+    w[tt].tile = t0 + min(tt, ntl - 1);
+    const cint_ptr tl = (cint_ptr)(a.tiles + w[tt].tile);
+    w[tt].expert = expert;
+    w[tt].row0 = tl[1];
+    w[tt].nrows = tl[2];
+    w[tt].ct0 = fb * kGmWaves;
+    const int ct = fb * kGmWaves + wave;
+    w[tt].active = ct < a.n_ct;
+    w[tt].ct = w[tt].active ? ct : a.n_ct - 1;
   }
-  if (w.active) epilogue_direct<MODE>(a, w, lane, acc, tw);
-}
 
-template <int MODE>
-__global__ __launch_bounds__(256, 2) void fwd_group_kernel(FwdArgs a)
-{
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  WorkItem w;
-  bool busy = false;
-  for (int it = 0;; ++it) {
-    const int st = decode_group(a, wave, it, w);
-    if (st == 0) break;
-    if (st == 2) continue;
-    if (busy) __syncthreads();  // every wave is done with the previous item's LDS buffers
+  // weight row n of item row r (0..511): wave r / 64's column tile, column group cg = (r / 16) % 4
+  // (gate/up: groups 2, 3 are W3's rows); bases of the group's matrix
+  auto w_n = [&](int r) {
+    const int ct = min(fb * kGmWaves + (r >> 6), a.n_ct - 1), cg = (r >> 4) & 3, i = r & 15;
+    return MODE == kFwdGateUp ? min(ct * 32 + (cg & 1) * 16 + i, a.R - 1) : min(ct * kFwdColsPerTile + cg * 16 + i, a.R - 1);
+  };
+  auto w_base = [&](int cg) {
+    return (MODE == kFwdGateUp && cg >= 2 ? a.wp1 : a.wp0) + (long long)expert * a.wp_estride;
+  };
+  auto s_base = [&](int cg) {
+    return (MODE == kFwdGateUp && cg >= 2 ? a.ws1 : a.ws0) + (long long)expert * a.ws_estride;
+  };
+  // the copies of quarter q of super-chunk c into buffer buf, six per wave: blocks 4q .. 4q + 3
+  // of rows 64 wave .. + 63 of W (four instructions of 16 rows x 64 B) and the KiB units
+  // (plane wave % 2, pieces 0, 1) of tile wave / 2's operand, each gathered from four 256 B runs
+  // of the AT layout; at q = 0 also the super-chunk's weight scales of its 64 rows and half
+  // (wave % 2) of tile wave / 2's 512 B of activation scales
+  auto issue = [&](int c, int q, int buf) {
     int l = lane;
     asm volatile("" : "+v"(l));
-    fwd_group_item<MODE>(a, w, wave, l);
-    busy = true;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // instruction k: column group k of this wave's tile
+      const int r = wave * 64 + k * 16 + (l >> 2), b = l & 3;
+      dma16_async_s(w_base(k), (uint32_t)w_n(r) * (uint32_t)(a.K / 2) + (uint32_t)(c * 256 + (4 * q + b) * 16),
+                    &lds.q[buf][kGmA + (wave * 64 + k * 16) * 64]);
+    }
+    {
+      const int tt = wave >> 1;
+      const uint8_t* at = a.a_tiles + (long long)(t0 + min(tt, ntl - 1)) * at_tile_bytes(a.K) +
+                          (long long)c * kAtChunkBytes;
+      const int plane = wave & 1, g = l >> 4, i = l & 15;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        // lane (i, g) of piece k holds block 4q + 2k + g / 2, elements 16 (g % 2) .. + 15, which
+        // the AT layout keeps as logical block q of its MFMA 2k + g / 2: piece q / 2 of lane
+        // 16 (2 (q % 2) + g % 2) + i
+        const int src = ((((2 * k + (g >> 1)) * 2 + plane) * 2 + (q >> 1)) * 64 + 16 * (2 * (q & 1) + (g & 1)) + i) * 16;
+        dma16_async_s(at, (uint32_t)src, &lds.q[buf][tt * 4096 + (2 * plane + k) * 1024]);
+      }
+    }
+    if (q == 0) {  // two more copies: 8 in all
+      const int r = wave * 64 + l;
+      const uint8_t* ps = s_base((r >> 4) & 3) + (long long)w_n(r) * nb;
+      dma16_async(ps + c * 16, &lds.sw[wave * 64 * 16]);
+      const int tt = wave >> 1, h = wave & 1;
+      const uint8_t* at = a.a_tiles + (long long)(t0 + min(tt, ntl - 1)) * at_tile_bytes(a.K) +
+                          (long long)c * kAtChunkBytes + kAtCodeBytes + h * 256;
+      dma4_async(at + l * 4, &lds.sa[tt * 512 + h * 256]);
+    }
+  };
+
+  f32x4 acc[T][4];
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+    for (int cg = 0; cg < 4; ++cg) acc[tt][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float tw[T][4];
+  if (MODE == kFwdDown)
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tw[tt][v] = a.row_w[w[tt].row0 + min(4 * g + v, w[tt].nrows - 1)];
+
+  // One step per quarter s (super-chunk s / 4, MFMA q = s % 4): wait for its copies (the
+  // next quarter's stay in flight), barrier, request quarter s + 2 into the buffer step s - 1
+  // read, 32 MFMAs. At q = 0 the wave takes the super-chunk's scales into registers, which frees
+  // their single LDS copy for the next super-chunk's, requested two steps later. The scale dwords
+  // are shifted so that byte q is byte 0: the MFMAs' scale selectors stay constant and one copy
+  // of the step serves all four quarters.
+  const int ns = 4 * nsc;
+  issue(0, 0, 0);
+  if (ns > 1) issue(0, 1, 1);
+  uint32_t rw[4], ra[T][2];
+  for (int s = 0; s < ns; ++s) {
+    const int c = s >> 2, q = s & 3;
+    if (s + 1 >= ns) wait_vm0();
+    else if (((s + 1) & 3) == 0) wait_vm<8>();
+    else wait_vm<6>();
+    __syncthreads();
+    if (s + 2 < ns) issue((s + 2) >> 2, (s + 2) & 3, (s + 2) % kGmRing);
+    __builtin_amdgcn_sched_barrier(0);
+    // lane-derived LDS offsets are rebuilt here each step rather than held across the loop
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    const int jl = l & 15, gl = l >> 4;
+    if (q == 0) {  // byte q of each register: the scale of block 4q + g (g = this lane's group)
+      // byte g of x, y, z, w -> bytes 0..3: two byte permutes (selector 12 gives zero) and an or
+      const uint32_t lo = 0x0C0C0000u | ((4u + gl) << 8) | (uint32_t)gl, hi = (lo << 16) | 0x0C0Cu;
+      auto gather = [&](uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
+        return __builtin_amdgcn_perm(y, x, lo) | __builtin_amdgcn_perm(w, z, hi);
+      };
+#pragma unroll
+      for (int cg = 0; cg < 4; ++cg) {
+        const uint4 d = *reinterpret_cast<const uint4*>(&lds.sw[(wave * 64 + cg * 16 + jl) * 16]);
+        rw[cg] = gather(d.x, d.y, d.z, d.w);
+      }
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) {  // AT holds block 4qq + g's scales at lane 16qq + i, byte g
+        uint2 s2[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) s2[qq] = *reinterpret_cast<const uint2*>(&lds.sa[tt * 512 + (16 * qq + jl) * 8]);
+        ra[tt][0] = gather(s2[0].x, s2[1].x, s2[2].x, s2[3].x);
+        ra[tt][1] = gather(s2[0].y, s2[1].y, s2[2].y, s2[3].y);
+      }
+    }
+    const uint8_t* lq = lds.q[s % kGmRing];
+    uint32_t sb[4];
+    i32x4 b[4];
+#pragma unroll
+    for (int cg = 0; cg < 4; ++cg) {
+      const int r = wave * 64 + cg * 16 + jl;
+      sb[cg] = rw[cg] >> (8 * q);
+      b[cg] = *reinterpret_cast<const i32x4*>(lq + kGmA + (r * 4 + gl) * 16);
+      const bool dead = (sb[cg] & 0xFFu) >= 253u;  // zero block, scale 2^0
+      b[cg] = dead ? i32x4{0, 0, 0, 0} : b[cg];
+      sb[cg] = dead ? 127u : sb[cg];
+    }
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) {
+      const uint8_t* pa = lq + tt * 4096 + l * 16;
+      const i32x8 ah = cat8(*reinterpret_cast<const i32x4*>(pa), *reinterpret_cast<const i32x4*>(pa + 1024));
+      const i32x8 al = cat8(*reinterpret_cast<const i32x4*>(pa + 2048), *reinterpret_cast<const i32x4*>(pa + 3072));
+      const int sah = (int)(ra[tt][0] >> (8 * q)), sal = (int)(ra[tt][1] >> (8 * q));
+#pragma unroll
+      for (int cg = 0; cg < 4; ++cg) {
+        acc[tt][cg] = mfma_f8f4<0, 0>(ah, b[cg], acc[tt][cg], sah, (int)sb[cg]);
+        acc[tt][cg] = mfma_f8f4<0, 0>(al, b[cg], acc[tt][cg], sal, (int)sb[cg]);
+      }
+    }
+  }
+  wait_vm0();
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt)
+    if (tt < ntl && w[tt].active) epilogue_direct<MODE>(a, w[tt], lane, acc[tt], tw[tt]);
+}
+
+// Resident grid over the items (group, block of eight column tiles), feature blocks outermost,
+// dealt over the XCDs in contiguous runs: the work-groups on one XCD at a time take neighbouring
+// groups (mostly of one expert) at the same columns, so they share the weights through its L2.
+template <int MODE>
+__global__ __launch_bounds__(64 * kGmWaves, 1) void fwd_gemm_kernel(FwdArgs a)
+{
+  __shared__ GemmLds lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ng = *(cint_ptr)a.n_groups;
+  const int nfb = (a.n_ct + kGmWaves - 1) / kGmWaves;
+  const int total = ng * nfb;
+  const int per_xcd = (total + 7) >> 3;
+  for (int it = 0;; ++it) {
+    const int slot = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
+    const int item = (int)(blockIdx.x & 7) * per_xcd + slot;
+    if (slot >= per_xcd || item >= total) break;
+    const int fb = item / ng, gi = item - fb * ng;
+    const cint_ptr gg = (cint_ptr)(a.groups + gi);
+    if (it > 0) __syncthreads();  // every wave is done with the previous item's LDS
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    fwd_gemm_item<MODE>(a, gg[0], gg[1], gg[2], fb, wave, l, lds);
   }
 }
 
@@ -799,10 +841,10 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
 #undef MX_LAUNCH
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !split) return e;
-  dim3 ggrid((unsigned)resident_groups());
-  if (mode == kFwdGateUp) hipLaunchKernelGGL(fwd_group_kernel<kFwdGateUp>, ggrid, block, 0, s, b);
-  else if (mode == kFwdDown) hipLaunchKernelGGL(fwd_group_kernel<kFwdDown>, ggrid, block, 0, s, b);
-  else hipLaunchKernelGGL(fwd_group_kernel<kFwdPlain>, ggrid, block, 0, s, b);
+  dim3 mgrid((unsigned)(resident_groups() / 16 * 8)), mblock(64 * kGmWaves);  // one per CU, a multiple of 8
+  if (mode == kFwdGateUp) hipLaunchKernelGGL(fwd_gemm_kernel<kFwdGateUp>, mgrid, mblock, 0, s, b);
+  else if (mode == kFwdDown) hipLaunchKernelGGL(fwd_gemm_kernel<kFwdDown>, mgrid, mblock, 0, s, b);
+  else hipLaunchKernelGGL(fwd_gemm_kernel<kFwdPlain>, mgrid, mblock, 0, s, b);
   return hipGetLastError();
 }
 
