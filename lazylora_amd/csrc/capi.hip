@@ -233,7 +233,8 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   // h once per token in the XT layout (with a zero row N for the unused slots of a tile), which
   // the one-tile work-groups gather; the tiles of large buckets also in the AT layout, which the
   // grouped work-groups re-read for every column tile
-  MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, at<uint8_t>(ws, L.xt_x), s), "quantise h");
+  MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, at<int>(ws, L.meta), at<uint8_t>(ws, L.xt_x), s),
+         "quantise h");
   MX_TRY(mx::launch_quant_tiles(h, h_dtype == MXFP4_BF16, D, N, D, at<int4>(ws, L.tiles), at<int>(ws, L.meta),
                                 L.max_tiles, at<int>(ws, L.pair_token), 1, at<uint8_t>(ws, L.at_x), s),
          "quantise h tiles");

@@ -122,7 +122,8 @@ hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows
 // Rows 0 .. rows - 1 of x into the XT layout (xt_row_bytes(K) per row), followed by zero rows
 // up to xt_rows(rows): row `rows` is the all-zero row a tile's unused slots gather.
 inline long long xt_rows(int rows) { return ((long long)rows + 16) / 16 * 16; }
-hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, uint8_t* out, hipStream_t s);
+hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, const int* meta, uint8_t* out,
+                             hipStream_t s);
 hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int Kpad, uint16_t* hi,
                              uint16_t* lo, hipStream_t s);
 hipError_t launch_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R,

@@ -148,17 +148,42 @@ __device__ __forceinline__ int read_idx(const void* idx, int idx64, long long p)
   return idx64 ? (int)reinterpret_cast<const long long*>(idx)[p] : reinterpret_cast<const int*>(idx)[p];
 }
 
+// counter[e] += 1 for every lane with `valid` set; returns the lane's slot (the counter's old value
+// plus the lane's rank among the wave's lanes with the same e). The lanes of the first
+// kAggRounds distinct experts of the wave add with one atomic per expert (buckets shared by many
+// lanes of a wave, as when tokens come sorted by expert, would otherwise serialise on one
+// address); any lanes left take one atomic each.
+__device__ __forceinline__ int wave_bucket_add(int* counter, int e, bool valid)
+{
+  constexpr int kAggRounds = 2;
+  const int lane = (int)(threadIdx.x & 63);
+  uint64_t todo = __builtin_amdgcn_ballot_w64(valid);
+  int pos = -1;
+#pragma unroll
+  for (int r = 0; r < kAggRounds; ++r) {
+    if (todo == 0) break;
+    const int leader = __builtin_ctzll(todo);
+    const int el = __builtin_amdgcn_readlane(e, leader);
+    const bool mine = valid && e == el;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&counter[el], __popcll(m));
+    base = __builtin_amdgcn_readlane(base, leader);
+    if (mine) pos = base + __popcll(m & ((1ull << lane) - 1ull));
+    todo &= ~m;
+  }
+  if (valid && pos < 0) pos = atomicAdd(&counter[e], 1);
+  return pos;
+}
+
 __global__ __launch_bounds__(256) void route_count_kernel(const void* idx, int idx64, int P, int E, int* counts,
                                                           int* meta)
 {
   const int p = blockIdx.x * 256 + threadIdx.x;
-  if (p >= P) return;
-  const long long raw = idx64 ? reinterpret_cast<const long long*>(idx)[p] : reinterpret_cast<const int*>(idx)[p];
-  if (raw < 0 || raw >= E) {
-    atomicOr(&meta[1], 1);
-    return;
-  }
-  atomicAdd(&counts[(int)raw], 1);
+  const long long raw = p < P ? (idx64 ? reinterpret_cast<const long long*>(idx)[p] : reinterpret_cast<const int*>(idx)[p]) : 0;
+  const bool valid = p < P && raw >= 0 && raw < E;
+  if (p < P && !valid) atomicOr(&meta[1], 1);
+  wave_bucket_add(counts, valid ? (int)raw : 0, valid);
 }
 
 // Single work-group: exclusive scan of counts and of per-expert tile counts, tile list. An
@@ -228,13 +253,14 @@ __global__ __launch_bounds__(256) void route_place_kernel(const void* idx, int i
                                                           int* pair_of)
 {
   const int p = blockIdx.x * 256 + threadIdx.x;
+  const long long raw = p < P ? (idx64 ? reinterpret_cast<const long long*>(idx)[p] : reinterpret_cast<const int*>(idx)[p]) : 0;
+  const bool valid = p < P && raw >= 0 && raw < E;
+  const int pos = wave_bucket_add(cursor, valid ? (int)raw : 0, valid);
   if (p >= P) return;
-  const long long raw = idx64 ? reinterpret_cast<const long long*>(idx)[p] : reinterpret_cast<const int*>(idx)[p];
-  if (raw < 0 || raw >= E) {
+  if (!valid) {
     pair_of[p] = -1;
     return;
   }
-  const int pos = atomicAdd(&cursor[(int)raw], 1);
   pair_token[pos] = p / k;
   pair_w[pos] = w[p];
   pair_of[p] = pos;
@@ -287,10 +313,13 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(float* grad_h, float* 
 
 // The same quantisation into the XT layout: one work-group per (16 rows, super-chunk), rows
 // r0 .. r0 + 15 of x; rows at or past `rows` (at least the one that follows the last) get zeros,
-// the row a tile's unused slots read.
+// the row a tile's unused slots read. Only the one-tile work-groups read this layout: with the
+// routing's meta (non-null), a layer whose buckets are all large (groups, no small tiles) skips it.
 template <bool BF16>
-__global__ __launch_bounds__(256) void quant_rows_kernel(const void* x, long long ldx, int rows, int K, uint8_t* out)
+__global__ __launch_bounds__(256) void quant_rows_kernel(const void* x, long long ldx, int rows, int K,
+                                                         const int* meta, uint8_t* out)
 {
+  if (meta && meta[2] == 0 && meta[3] > 0) return;  // the whole grid
   __shared__ __attribute__((aligned(16))) uint8_t chunk[16 * kXtChunkBytes];
   const int nsc = at_nchunks(K);
   const int rg = (int)(blockIdx.x / nsc), c = (int)(blockIdx.x - (long long)rg * nsc);
@@ -359,13 +388,14 @@ hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows
   return hipGetLastError();
 }
 
-hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, uint8_t* out, hipStream_t s)
+hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, const int* meta, uint8_t* out,
+                             hipStream_t s)
 {
   const long long groups = (long long)xt_rows(rows) / 16 * at_nchunks(K);  // (16 rows, super-chunk)
   if (groups == 0) return hipSuccess;
   dim3 grid((unsigned)groups), block(256);
-  if (x_bf16) hipLaunchKernelGGL(quant_rows_kernel<true>, grid, block, 0, s, x, ldx, rows, K, out);
-  else hipLaunchKernelGGL(quant_rows_kernel<false>, grid, block, 0, s, x, ldx, rows, K, out);
+  if (x_bf16) hipLaunchKernelGGL(quant_rows_kernel<true>, grid, block, 0, s, x, ldx, rows, K, meta, out);
+  else hipLaunchKernelGGL(quant_rows_kernel<false>, grid, block, 0, s, x, ldx, rows, K, meta, out);
   return hipGetLastError();
 }
 

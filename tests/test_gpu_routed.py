@@ -118,14 +118,15 @@ def test_skewed_routing_large_buckets(k):
 
 @pytest.mark.parametrize("topk", [1, 2])
 def test_large_bucket_groups(k, topk):
-    """Buckets of 200, 65, 64, 49, 48, 17 and 1 rows: the experts with four or more 16-row tiles
-    take the grouped work-groups (groups of 4 tiles, ragged last group and last tile), the rest the
-    one-tile work-groups; K = 1024 and 512 keep both products on the path that splits them."""
-    case(f"large-bucket groups: E=8, D=1024, F=512, top-{topk}")
+    """Buckets of 200, 129, 65, 64, 49, 48, 17 and 1 rows: the experts with four or more 16-row
+    tiles take the grouped work-groups (groups of 4 tiles, ragged last groups down to one tile,
+    ragged last tile), the rest the one-tile work-groups; K = 1024 and 512 keep both products on
+    the path that splits them."""
+    case(f"large-bucket groups: E=9, D=1024, F=512, top-{topk}")
     rng = np.random.default_rng(18 + topk)
-    E, D, F = 8, 1024, 512
+    E, D, F = 9, 1024, 512
     ex = oracle.random_experts(rng, E, D, F, 118, 122)
-    sizes = [200, 65, 64, 49, 48, 17, 1, 0]
+    sizes = [200, 129, 65, 64, 49, 48, 17, 1, 0]
     first = np.concatenate([np.full(c, e) for e, c in enumerate(sizes)]).astype(np.int64)
     rng.shuffle(first)
     N = first.size
