@@ -13,7 +13,7 @@
  *   noted. Every call is asynchronous on `stream` (0 = the null stream).
  *
  * Alignment (checked; a violation returns MXFP4_EINVAL and launches nothing): packed weights
- * and scales 16 bytes (mxfp4_dequant takes any alignment); mxfp4_gemm's x 8 bytes; mxfp4_gemm_t's dy 4 bytes and y 16 bytes; the routed layer's
+ * and scales 16 bytes (mxfp4_dequant takes any alignment, mxfp4_dequant_bf16 a 4-byte aligned out); mxfp4_gemm's x 8 bytes; mxfp4_gemm_t's dy 4 bytes and y 16 bytes; the routed layer's
  * h 8 bytes (fp32) or 4 bytes (bf16), 16 bytes with LoRA, as are grad_out and the LoRA
  * factors then. Buffers from hipMalloc or torch satisfy all of these.
  *
@@ -70,6 +70,13 @@ int mxfp4_threads(void);
  * int K, int R) (mxfp4_gemm.c:142-150): out[R, K] fp32 = W, bit-exact. */
 int mxfp4_dequant(float *out, const uint8_t *packed, const uint8_t *scales, int K, int R,
                   hipStream_t stream);
+
+/* Replaces the bf16 result of _dequantize_mxfp4(weight_packed, weight_scale,
+ * out_dtype=None) (lazy_lora/streaming/expert_streamer.py:104-154, whose default output dtype
+ * is bfloat16): out[R, K] bf16 = W, the same values as mxfp4_dequant (each decoded value is
+ * exact in bf16), scale bytes >= 253 giving +-0. out 4-byte aligned. */
+int mxfp4_dequant_bf16(uint16_t *out, const uint8_t *packed, const uint8_t *scales, int K,
+                       int R, hipStream_t stream);
 
 /* Replaces void mxfp4_gemm(float *y, const float *x, const uint8_t *packed,
  * const uint8_t *scales, int M, int K, int R) (mxfp4_gemm.c:64-94):

@@ -367,7 +367,16 @@ int mxfp4_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int 
 {
   if (K <= 0 || R < 0 || K % 32) return fail(MXFP4_EINVAL, "dequant: K must be a positive multiple of 32%s");
   if (R > 0 && (!out || !packed || !scales)) return fail(MXFP4_EINVAL, "dequant: null pointer%s");
-  MX_TRY(mx::launch_dequant(out, packed, scales, K, R, stream), "dequant");
+  MX_TRY(mx::launch_dequant(out, 0, packed, scales, K, R, stream), "dequant");
+  return MXFP4_OK;
+}
+
+int mxfp4_dequant_bf16(uint16_t* out, const uint8_t* packed, const uint8_t* scales, int K, int R, hipStream_t stream)
+{
+  if (K <= 0 || R < 0 || K % 32) return fail(MXFP4_EINVAL, "dequant_bf16: K must be a positive multiple of 32%s");
+  if (R > 0 && (!out || !packed || !scales)) return fail(MXFP4_EINVAL, "dequant_bf16: null pointer%s");
+  if (R > 0 && ((uintptr_t)out & 3)) return fail(MXFP4_EINVAL, "dequant_bf16: out must be 4-byte aligned%s");
+  MX_TRY(mx::launch_dequant(out, 1, packed, scales, K, R, stream), "dequant_bf16");
   return MXFP4_OK;
 }
 

@@ -126,7 +126,7 @@ hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows,
                              hipStream_t s);
 hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int Kpad, uint16_t* hi,
                              uint16_t* lo, hipStream_t s);
-hipError_t launch_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R,
+hipError_t launch_dequant(void* out, int out_bf16, const uint8_t* packed, const uint8_t* scales, int K, int R,
                           hipStream_t s);
 // Routing: per-expert counts, scan, the tile list (tiles[t] = {expert, first pair row, rows, large}),
 // the small-bucket tile indices and the large-bucket groups ({expert, first tile, tiles, 0}),

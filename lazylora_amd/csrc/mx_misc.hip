@@ -91,11 +91,13 @@ __global__ __launch_bounds__(256) void split_bf16_kernel(const float* x, long lo
 }
 
 // ---------------------------------------------------------------- exact dequantisation
-// out[R, K] fp32 = decoded W (lazy_lora/native/mxfp4_gemm.c:142-150). The hardware fp4 -> bf16
-// conversion is exact for scale bytes 0..252 (bf16 widens to fp32 by a 16-bit shift); bytes
-// >= 253 give +-0 with the code's sign, as LUT[code] * 0.0f does.
-__global__ __launch_bounds__(256) void dequant_kernel(float* out, const uint8_t* packed, const uint8_t* scales,
-                                                      int K, int R)
+// out[R, K] = decoded W (lazy_lora/native/mxfp4_gemm.c:142-150), fp32 or bf16
+// (lazy_lora/streaming/expert_streamer.py:104-154, whose default output is bf16). The hardware
+// fp4 -> bf16 conversion is exact for scale bytes 0..252, and so is either output (bf16 widens to
+// fp32 by a 16-bit shift); bytes >= 253 give +-0 with the code's sign, as LUT[code] * 0.0f does.
+template <bool BF16>
+__global__ __launch_bounds__(256) void dequant_kernel(void* out, const uint8_t* packed, const uint8_t* scales, int K,
+                                                      int R)
 {
   const long long blk = (long long)blockIdx.x * 256 + threadIdx.x;  // one 32-element block
   const int nb = K / kGroup;
@@ -114,26 +116,35 @@ __global__ __launch_bounds__(256) void dequant_kernel(float* out, const uint8_t*
                  ((uint32_t)src[4 * d + 3] << 24);
   }
   const uint32_t s = scales[(long long)r * nb + b];
-  float* dst = out + (long long)r * K + b * kGroup;
+  const long long e0 = (long long)r * K + b * kGroup;  // first output element of the block
+  // the block's 32 values as 16 bf16 pairs (element 2n in the low half of pair n)
+  uint32_t pr[16];
   if (s >= 253u) {
 #pragma unroll
     for (int d = 0; d < 4; ++d)
 #pragma unroll
-      for (int n = 0; n < 8; ++n) dst[8 * d + n] = bits_f(((words[d] >> (4 * n)) & 8u) << 28);
-    return;
+      for (int n = 0; n < 4; ++n)  // the sign bits (bit 3) of codes 2n and 2n + 1 of word d
+        pr[4 * d + n] = (((words[d] >> (8 * n)) & 8u) << 12) | (((words[d] >> (8 * n + 4)) & 8u) << 28);
+  } else {
+    const float scale = bits_f(s << 23);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      pr[4 * d + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 0));
+      pr[4 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 1));
+      pr[4 * d + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 2));
+      pr[4 * d + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 3));
+    }
   }
-  const float scale = bits_f(s << 23);
+  if (BF16) {
+    uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(out) + e0);
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    uint32_t p[4];
-    p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 0));
-    p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 1));
-    p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 2));
-    p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(words[d], scale, 3));
+    for (int n = 0; n < 16; ++n) dst[n] = pr[n];
+  } else {
+    float* dst = static_cast<float*>(out) + e0;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      dst[8 * d + 2 * n] = bf16_lo(p[n]);
-      dst[8 * d + 2 * n + 1] = bf16_hi(p[n]);
+    for (int n = 0; n < 16; ++n) {
+      dst[2 * n] = bf16_lo(pr[n]);
+      dst[2 * n + 1] = bf16_hi(pr[n]);
     }
   }
 }
@@ -409,12 +420,14 @@ hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int
   return hipGetLastError();
 }
 
-hipError_t launch_dequant(float* out, const uint8_t* packed, const uint8_t* scales, int K, int R, hipStream_t s)
+hipError_t launch_dequant(void* out, int out_bf16, const uint8_t* packed, const uint8_t* scales, int K, int R,
+                          hipStream_t s)
 {
   const long long blocks = (long long)R * (K / kGroup);
   if (blocks == 0) return hipSuccess;
   dim3 grid((unsigned)((blocks + 255) / 256)), block(256);
-  hipLaunchKernelGGL(dequant_kernel, grid, block, 0, s, out, packed, scales, K, R);
+  if (out_bf16) hipLaunchKernelGGL(dequant_kernel<true>, grid, block, 0, s, out, packed, scales, K, R);
+  else hipLaunchKernelGGL(dequant_kernel<false>, grid, block, 0, s, out, packed, scales, K, R);
   return hipGetLastError();
 }
 

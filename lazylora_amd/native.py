@@ -58,6 +58,8 @@ def _load_library() -> ctypes.CDLL:
     lib.mxfp4_threads.argtypes = []
     lib.mxfp4_dequant.restype = ci
     lib.mxfp4_dequant.argtypes = [vp, vp, vp, ci, ci, vp]
+    lib.mxfp4_dequant_bf16.restype = ci
+    lib.mxfp4_dequant_bf16.argtypes = [vp, vp, vp, ci, ci, vp]
     lib.mxfp4_gemm_workspace_size.restype = sz
     lib.mxfp4_gemm_workspace_size.argtypes = [ci, ci, ci]
     lib.mxfp4_gemm.restype = ci
@@ -174,17 +176,25 @@ class MXFP4Kernel:
                                          ws.data_ptr(), nws, _stream(dev)), self.lib)
         return y if dy.is_cuda else y.cpu()
 
-    def dequant(self, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
-        """W[R, K] fp32 from the packed bytes, bit-exact (mxfp4_gemm.c:142-150)."""
+    def dequant(self, packed: torch.Tensor, scales: torch.Tensor, out_dtype=torch.float32) -> torch.Tensor:
+        """W[R, K] from the packed bytes, bit-exact (mxfp4_gemm.c:142-150): fp32 by default, as
+        the reference's; out_dtype=torch.bfloat16 decodes straight to bf16 (the same values, each
+        exact in bf16), any other floating dtype converts the fp32 result."""
         if packed.dim() != 2:
             raise ValueError(f"packed must be 2-D [R, K/2], got {tuple(packed.shape)}")
+        if not out_dtype.is_floating_point:
+            raise ValueError(f"out_dtype must be a floating dtype, got {out_dtype}")
         R, K = packed.shape[0], packed.shape[1] * 2
         _check_weight(packed, scales, R, K)
         dev = _device_for(packed)
         p, s = _u8(packed, dev, "packed"), _u8(scales, dev, "scales")
-        w = torch.empty((R, K), dtype=torch.float32, device=dev)
+        bf16 = out_dtype == torch.bfloat16
+        w = torch.empty((R, K), dtype=torch.bfloat16 if bf16 else torch.float32, device=dev)
         if R:
-            _check(self.lib.mxfp4_dequant(w.data_ptr(), p.data_ptr(), s.data_ptr(), K, R, _stream(dev)), self.lib)
+            fn = self.lib.mxfp4_dequant_bf16 if bf16 else self.lib.mxfp4_dequant
+            _check(fn(w.data_ptr(), p.data_ptr(), s.data_ptr(), K, R, _stream(dev)), self.lib)
+        if w.dtype != out_dtype:
+            w = w.to(out_dtype)
         return w if packed.is_cuda else w.cpu()
 
     def threads(self) -> int:

@@ -98,3 +98,40 @@ def host_layer_from(layer: ExpertLayer, pin: Optional[bool] = None) -> HostLayer
     for src, dst in zip(layer.tensors(), h.tensors):
         dst.copy_(src)
     return h
+
+
+def dequantize_mxfp4(weight_packed, weight_scale, group_size: int = 32, out_dtype=None):
+    """Widen one packed MXFP4 matrix on the device (_dequantize_mxfp4,
+    lazy_lora/streaming/expert_streamer.py:104-154): weight_packed [R, K/2] bytes (low nibble =
+    even element), weight_scale [R, K/32] E8M0 bytes (or [R], one byte per row), value =
+    e2m1(code) * 2^(scale - 127), a scale byte >= 253 giving +-0. Returns [R, K] in out_dtype,
+    bfloat16 when None as in the reference; bf16 and fp32 come straight from the device kernels,
+    other floating dtypes from the fp32 result. Torch tensors come back on their own device,
+    NumPy arrays as fp32 NumPy arrays (the reference's NumPy branch; there, unlike its torch
+    branch, only scale 255 is zeroed, where this zeroes >= 253 on both). Needs the MI355X
+    library: raises RuntimeError when it is unavailable."""
+    import numpy as np
+
+    from lazylora_amd.native import kernel
+
+    if group_size != 32:
+        raise ValueError(f"MXFP4 groups hold 32 elements, got group_size={group_size}")
+    k = kernel()
+    if k is None:
+        raise RuntimeError("dequantize_mxfp4 needs the MI355X MXFP4 library (kernel() is None)")
+    as_numpy = isinstance(weight_packed, np.ndarray)
+    p = torch.from_numpy(np.ascontiguousarray(weight_packed)) if as_numpy else weight_packed
+    s = torch.from_numpy(np.ascontiguousarray(weight_scale)) if isinstance(weight_scale, np.ndarray) else weight_scale
+    if p.dim() != 2:
+        raise ValueError(f"weight_packed must be 2-D [R, K/2], got {tuple(p.shape)}")
+    R, K = p.shape[0], p.shape[1] * 2
+    if s.dim() == 1:  # one scale per row
+        if s.shape[0] != R:
+            raise ValueError(f"a 1-D weight_scale needs one byte per row ({R}), got {s.shape[0]}")
+        s = s.reshape(R, 1).expand(R, K // 32)
+    dtype = torch.float32 if as_numpy else (out_dtype or torch.bfloat16)
+    w = k.dequant(p, s.contiguous(), out_dtype=dtype)
+    return w.numpy() if as_numpy else w
+
+
+_dequantize_mxfp4 = dequantize_mxfp4  # the reference's name, for callers that import it

@@ -45,6 +45,9 @@ def test_host_side_argument_errors(lib):
     dummy = vp(256)  # never dereferenced: every call below must fail its checks first
     assert lib.mxfp4_dequant(dummy, dummy, dummy, 33, 4, None) == -1
     assert b"multiple of 32" in lib.mxfp4_last_error()
+    assert lib.mxfp4_dequant_bf16(dummy, dummy, dummy, 33, 4, None) == -1
+    assert lib.mxfp4_dequant_bf16(None, dummy, dummy, 64, 4, None) == -1      # null output
+    assert lib.mxfp4_dequant_bf16(None, None, None, 64, 0, None) == 0         # R = 0: no-op
     assert lib.mxfp4_gemm(dummy, dummy, dummy, dummy, 4, 48, 4, None, 0, None) == -1
     assert lib.mxfp4_gemm(dummy, dummy, dummy, dummy, 4, 64, 4, None, 0, None) == -2
     assert lib.mxfp4_gemm_t(dummy, dummy, dummy, dummy, 4, 64, 4, None, 0, None) == -2
@@ -137,15 +140,17 @@ def test_no_device_gives_none(monkeypatch):
 
 
 def test_alignment_rejected_on_host(lib):
-    """Packed weights and scales need 16-byte alignment, gemm's x 8 bytes, gemm_t's dy 4 bytes
-    and the routed layer's h 8 bytes (fp32) / 4 bytes (bf16); violations return EINVAL before any
-    launch (include/lazylora_mxfp4.h)."""
+    """Packed weights and scales need 16-byte alignment, gemm's x 8 bytes, gemm_t's dy 4 bytes,
+    dequant_bf16's out 4 bytes and the routed layer's h 8 bytes (fp32) / 4 bytes (bf16);
+    violations return EINVAL before any launch (include/lazylora_mxfp4.h)."""
     vp = ctypes.c_void_p
     ok, odd8, odd4, odd1 = vp(4096), vp(4096 + 8), vp(4096 + 4), vp(4096 + 1)
     ws = vp(1 << 20)
     assert lib.mxfp4_gemm(ok, ok, ok, odd8, 4, 64, 4, ws, 1 << 30, None) == -1      # scales
     assert b"16-byte" in lib.mxfp4_last_error()
     assert lib.mxfp4_gemm(ok, odd4, ok, ok, 4, 64, 4, ws, 1 << 30, None) == -1      # x
+    assert lib.mxfp4_dequant_bf16(vp(4096 + 2), ok, ok, 64, 4, None) == -1         # bf16 out at 2 bytes
+    assert b"4-byte" in lib.mxfp4_last_error()
     assert lib.mxfp4_gemm_t(ok, ok, ok, odd8, 4, 64, 4, ws, 1 << 30, None) == -1    # scales
     assert lib.mxfp4_gemm_t(ok, odd1, ok, ok, 4, 64, 4, ws, 1 << 30, None) == -1    # dy
     wts = [ok] * 6

@@ -44,6 +44,46 @@ def test_dequant_expert_matrix_bit_exact(k, rng):
     assert np.array_equal(got.view(np.uint32), oracle.dequant(p, s).view(np.uint32))
 
 
+def test_dequant_bf16_all_pairs_bit_exact(k):
+    case("dequant bf16: all 65536 (byte, scale) pairs")
+    packed = np.repeat(np.arange(256, dtype=np.uint8), 16)[None, :].repeat(256, axis=0)
+    scales = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 256, axis=1)
+    got = k.dequant(cuda(packed), cuda(scales), out_dtype=torch.bfloat16)
+    assert got.dtype == torch.bfloat16 and got.shape == (256, 8192)
+    want32 = oracle.dequant(packed, scales)
+    assert not (want32.view(np.uint32) & 0xFFFF).any()  # every decoded value is exact in bf16
+    want = torch.from_numpy(want32).to(torch.bfloat16)  # the reference's .to(bfloat16)
+    assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16))
+
+
+def test_dequantize_mxfp4_mirror(k, rng):
+    """lazylora_amd.streaming.dequantize_mxfp4 against the reference's _dequantize_mxfp4 contract
+    (expert_streamer.py:104-154): bf16 by default, fp32 / fp16 on request, one scale per row,
+    NumPy and CPU inputs."""
+    case("dequantize_mxfp4: dtypes, per-row scales, NumPy and CPU inputs")
+    from lazylora_amd.streaming import _dequantize_mxfp4, dequantize_mxfp4
+    p, s = oracle.random_mx(rng, (96, 320), 0, 255)
+    want32 = oracle.dequant(p, s)
+    w = dequantize_mxfp4(cuda(p), cuda(s))
+    assert w.dtype == torch.bfloat16 and w.is_cuda
+    assert torch.equal(w.cpu().view(torch.int16), torch.from_numpy(want32).to(torch.bfloat16).view(torch.int16))
+    w32 = _dequantize_mxfp4(cuda(p), cuda(s), out_dtype=torch.float32)
+    assert np.array_equal(w32.cpu().numpy().view(np.uint32), want32.view(np.uint32))
+    w16 = dequantize_mxfp4(cuda(p), cuda(s), out_dtype=torch.float16)
+    assert w16.dtype == torch.float16 and torch.equal(w16.cpu(), torch.from_numpy(want32).to(torch.float16))
+    s1 = rng.integers(0, 256, 96).astype(np.uint8)  # one scale byte per row
+    want1 = oracle.dequant(p, np.repeat(s1[:, None], 320 // 32, axis=1))
+    w1 = dequantize_mxfp4(cuda(p), cuda(s1), out_dtype=torch.float32)
+    assert np.array_equal(w1.cpu().numpy().view(np.uint32), want1.view(np.uint32))
+    wn = dequantize_mxfp4(p, s)
+    assert isinstance(wn, np.ndarray) and wn.dtype == np.float32
+    assert np.array_equal(wn.view(np.uint32), want32.view(np.uint32))
+    wc = dequantize_mxfp4(torch.from_numpy(p), torch.from_numpy(s))
+    assert wc.device.type == "cpu" and wc.dtype == torch.bfloat16
+    with pytest.raises(ValueError):
+        dequantize_mxfp4(cuda(p), cuda(s), group_size=16)
+
+
 GEMM_SHAPES = [
     (1, 256, 128), (16, 256, 128), (64, 128, 256),                 # config-1 expert shapes
     (1, 7168, 2048), (4, 7168, 2048), (16, 7168, 2048),             # config-2 gate/up, M sweep
