@@ -47,11 +47,18 @@ def adapters_of(lo: oracle.LoRA, requires_grad=False):
     return tuple(mods)
 
 
-def run_case(k, E, D, F, N, topk, r, act, seed, h_bf16=False, scale_lo=119, scale_hi=123):
+def run_case(k, E, D, F, N, topk, r, act, seed, h_bf16=False, scale_lo=119, scale_hi=123, sizes=None):
+    """sizes: rows per expert, routed top-1 in shuffled order (N and topk are then ignored)."""
     rng = np.random.default_rng(seed)
     ex = oracle.random_experts(rng, E, D, F, scale_lo, scale_hi)
+    if sizes is not None:
+        first = np.concatenate([np.full(c, e) for e, c in enumerate(sizes)]).astype(np.int64)
+        rng.shuffle(first)
+        N = first.size
+        idx, w = first[:, None], rng.uniform(0.5, 1.5, (N, 1)).astype(np.float32)
     h = rng.standard_normal((N, D)).astype(np.float32)
-    idx, w = oracle.softmax_topk(rng.standard_normal((N, E)).astype(np.float32), topk)
+    if sizes is None:
+        idx, w = oracle.softmax_topk(rng.standard_normal((N, E)).astype(np.float32), topk)
     g = rng.standard_normal((N, D)).astype(np.float32)
     lo = oracle.random_lora(rng, D, F, r)
     L = layer_of(ex)
@@ -84,6 +91,15 @@ def test_config1_with_lora(k, act):
 def test_ranks_and_dtypes(k, r, h_bf16):
     case(f"16 experts 512x256, 96 tokens top-4, LoRA r={r}, bf16 h={h_bf16}")
     run_case(k, 16, 512, 256, 96, 4, r, "situ", seed=32 + r, h_bf16=h_bf16)
+
+
+@pytest.mark.parametrize("act", ["swiglu", "situ"])
+def test_large_buckets_with_lora(k, act):
+    """Buckets of 150, 70, 30 and 6 rows (10, 5, 2 and 1 tiles; K = 1024 and 512 keep both
+    products on the path that splits them): the first two take the grouped work-groups, whose
+    epilogues add the LoRA gate/up deltas and whose gradients feed the adapter gradients."""
+    case(f"large buckets + LoRA r=16 {act}")
+    run_case(k, 4, 1024, 512, 0, 1, 16, act, seed=47, scale_lo=118, scale_hi=122, sizes=[150, 70, 30, 6])
 
 
 def test_expert_shape_of_the_reference(k):
