@@ -16,9 +16,10 @@ repo's C restatement of the reference CPU path timed on a bounded sample of the 
 
     python bench.py [--steps 20] [--warmup 3] [--routing uniform|zipf] [--no-cpu] [--no-extra]
 
-The default run also times the Zipf-skewed routing of the same layer (key "zipf"), config 2 at
-M = 1 and M = 256 tokens per expert (key "config2") and a 12-layer sample of config 5's
-out-of-core sweep (key "config5_sample"), each in its own timed region after the headline's.
+The default run also times the Zipf-skewed routing of the same layer (key "zipf"), config 3's
+forward alone under both routings (key "config3_forward"), config 2 at M = 1 and M = 256 tokens
+per expert (key "config2") and a 12-layer sample of config 5's out-of-core sweep (key
+"config5_sample"), each in its own timed region after the headline's.
 """
 import argparse
 import json
@@ -377,6 +378,9 @@ def main():
                          "largest_bucket": int(counts.max()),
                          "weight_GBps": 2 * EXPERT_BYTES * nz / (ms_z * 1e-3) / 1e9,
                          "phases_ms": {n: round(v, 4) for n, v in ph_z.items()}}
+        # config 3: the same layer's forward alone, both routings
+        extra["config3_forward"] = {"uniform": time_forward(args, k, layer, H, I, W, ws, n_active),
+                                    "zipf": time_forward(args, k, layer, Hz, Iz, Wz, ws, nz)}
         del Hz, Iz, Wz, Gz
         # config 2 at its two ends, M = 1 (HBM-bound) and M = 256 (MFMA-bound)
         del ws
@@ -438,6 +442,29 @@ def main():
     }
     line.update(extra)
     print(json.dumps(line), flush=True)
+
+
+def time_forward(args, k, layer, H, I, W, ws, n_active):
+    """Config 3: the routed layer's forward alone (routing, quantised x,
+    gate/up + GLU, down, combine; nothing saved for a backward). A dict of ms per forward,
+    tokens/s and weight GB/s over args.steps timed calls after args.warmup."""
+    def fwd():
+        return k.routed_forward(H, I, W, layer, act=args.act, save_for_backward=False, workspace=ws)
+
+    for _ in range(args.warmup):
+        fwd()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        fwd()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    log(f"[bench] forward alone: {ms:.3f} ms ({n_active} active experts)")
+    return {"ms_per_forward": ms, "tokens_per_s": N / (ms * 1e-3), "active_experts": n_active,
+            "weight_GBps": EXPERT_BYTES * n_active / (ms * 1e-3) / 1e9}
 
 
 def time_layer(args, k, layer, H, I, W, G, ws, lora, n_active, calibrate=False):
