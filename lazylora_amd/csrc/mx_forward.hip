@@ -609,6 +609,7 @@ constexpr int kGmRows = kGmWaves * 64;         // weight rows per item
 constexpr int kGmA = kGmT * 4096;              // A bytes per quarter: [tile][plane][piece][lane][16 B]
 constexpr int kGmW = kGmRows * 64;             // W bytes per quarter: [row][block][16 B]
 constexpr int kGmRing = 3;                     // quarters in LDS: the one read and two in flight
+static_assert(kGmT >= kGroupTiles, "an item holds a whole group");
 struct GemmLds {
   uint8_t q[kGmRing][kGmA + kGmW];             // quarter buffers
   uint8_t sw[kGmRows * 16];                    // weight scales of a super-chunk: [row][16 B]
