@@ -167,7 +167,7 @@ struct LoraFactor {
 constexpr int kLoraMaxRank = 32;
 
 // out[row, s*r + j] = f_s.scale * sum_{k < K} src(row, koff_s + k) * f_s(j, k), segments s < nseg
-// (nseg <= 2), rows < rows; rows at or past *rows_dev (when given) get 0. K is a multiple of 16.
+// (nseg <= 2), rows < rows; rows at or past *rows_dev (when given) get 0. K is a multiple of 32.
 // `partial` holds lora_rowdot_partial_floats(rows, K, nseg, r) floats of scratch.
 size_t lora_rowdot_partial_floats(int rows, int K, int nseg, int r);
 hipError_t launch_lora_rowdot(const LoraMat& src, int rows, const int* rows_dev, int K, int r, int nseg,

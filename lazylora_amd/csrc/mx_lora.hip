@@ -63,22 +63,47 @@ MX_DEV f32x4 mfma4(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32
 
 // ---------------------------------------------------------------- row dots
 // Each wave takes one (16-row tile, segment, k-slice) and accumulates its 16 x r block of
-// partial sums on the matrix cores: per 16 k, lane (i, q) loads row i's k .. k+3 (k = 16 kb + 4q)
-// and the same four k of coefficient i (and 16 + i), then four MFMAs take one k each. The
-// k-slices are added in order by lora_rowdot_reduce_kernel.
+// partial sums on the matrix cores. Lane (i, q) loads KPL consecutive k of row i (KPL = 4 for
+// fp32 sources, 8 for bf16 ones, so that a load instruction reads whole 64-byte pieces of the
+// 16 rows) and the same k of coefficient i (and 16 + i); one MFMA per k of the lane, each
+// taking k-index q from every lane, covers the 4 KPL k of a load. The k-slices are added in
+// order by lora_rowdot_reduce_kernel.
 struct RowDotArgs {
   LoraMat src;
   int rows;
   const int* rows_dev;
-  int K, r, nseg, S, kb_per;
+  int K, r, nseg, S, kb_per;  // k-slices of kb_per 32-k units
   LoraFactor f[2];
   int koff[2];
   float* partial;  // [S][rows][nseg * r]
 };
 
+constexpr int kRowDotUnits = 1;  // 32-k units per step, all loads issued before the MFMAs
+
+// Elements (row, c .. c+7) of a bf16 or hi+lo source as fp32, from 16-byte loads; c is a multiple of 8.
+template <int KIND>
+MX_DEV void src8(const LoraMat& a, long long row, int c, f32x4& x0, f32x4& x1)
+{
+  const long long o = row * a.ld + c;
+  const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.p0) + o);
+  if (KIND == kLoraBF16) {
+    x0 = f32x4{bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y)};
+    x1 = f32x4{bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w)};
+  } else {
+    const uint4 l = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.p1) + o);
+    x0 = f32x4{bf16_lo(h.x) + bf16_lo(l.x), bf16_hi(h.x) + bf16_hi(l.x), bf16_lo(h.y) + bf16_lo(l.y),
+               bf16_hi(h.y) + bf16_hi(l.y)};
+    x1 = f32x4{bf16_lo(h.z) + bf16_lo(l.z), bf16_hi(h.z) + bf16_hi(l.z), bf16_lo(h.w) + bf16_lo(l.w),
+               bf16_hi(h.w) + bf16_hi(l.w)};
+  }
+}
+
 template <int KIND>
 __global__ __launch_bounds__(256) void lora_rowdot_kernel(RowDotArgs a)
 {
+  constexpr int KPL = (KIND == kLoraBF16 || KIND == kLoraHiLo) ? 8 : 4;
+  constexpr int NV = 8 / KPL;  // loads per lane per 32-k unit
+  constexpr int NC = KPL / 4;  // f32x4 per load
   const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
   const int tiles = (a.rows + 15) / 16;
   const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -93,29 +118,43 @@ __global__ __launch_bounds__(256) void lora_rowdot_kernel(RowDotArgs a)
   const LoraFactor f = a.f[sg];
   const int koff = a.koff[sg];
   const bool two = a.r > 16;
-  const int nkb = a.K / 16;
-  const int kb0 = ks * a.kb_per, kb1 = min(kb0 + a.kb_per, nkb);
+  const int nu = a.K / 32;
+  const int u0 = ks * a.kb_per, u1 = min(u0 + a.kb_per, nu);
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  // four blocks of 16 k per iteration, loads first
-  for (int kb = kb0; kb < kb1; kb += 4) {
-    f32x4 x[4], m0[4], m1[4];
+  for (int ub = u0; ub < u1; ub += kRowDotUnits) {
+    f32x4 x[kRowDotUnits][NV][NC], m0[kRowDotUnits][NV][NC], m1[kRowDotUnits][NV][NC];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int k = (kb + u) * 16 + 4 * q;
-      const bool in = kb + u < kb1;
-      x[u] = (rok && in) ? src4<KIND>(a.src, row, koff + k) : f32x4{0.f, 0.f, 0.f, 0.f};
-      m0[u] = in ? factor4(f, i, k, a.r) : f32x4{0.f, 0.f, 0.f, 0.f};
-      m1[u] = (in && two) ? factor4(f, 16 + i, k, a.r) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int uu = 0; uu < kRowDotUnits; ++uu) {
+      const bool in = ub + uu < u1;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+      for (int v = 0; v < NV; ++v) {
+        const int k = (ub + uu) * 32 + v * 4 * KPL + KPL * q;
+        if (KPL == 8) {
+          if (rok && in) src8<KIND>(a.src, row, koff + k, x[uu][v][0], x[uu][v][NC - 1]);
+          else x[uu][v][0] = x[uu][v][NC - 1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+          x[uu][v][0] = (rok && in) ? src4<KIND>(a.src, row, koff + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc0 = mfma4(x[u][c], m0[u][c], acc0);
-      if (two) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc1 = mfma4(x[u][c], m1[u][c], acc1);
+        for (int t = 0; t < NC; ++t) {
+          m0[uu][v][t] = in ? factor4(f, i, k + 4 * t, a.r) : f32x4{0.f, 0.f, 0.f, 0.f};
+          m1[uu][v][t] = (in && two) ? factor4(f, 16 + i, k + 4 * t, a.r) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
     }
+#pragma unroll
+    for (int uu = 0; uu < kRowDotUnits; ++uu)
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int t = 0; t < NC; ++t) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc0 = mfma4(x[uu][v][t][c], m0[uu][v][t][c], acc0);
+          if (two) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc1 = mfma4(x[uu][v][t][c], m1[uu][v][t][c], acc1);
+          }
+        }
   }
   const int m = a.nseg * a.r;
   float* out = a.partial + (long long)ks * a.rows * m + sg * a.r;
@@ -134,79 +173,115 @@ __global__ __launch_bounds__(256) void lora_rowdot_reduce_kernel(const float* pa
   const int m = nseg * r;
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (long long)rows * m) return;
+  // slices added in slice order; eight loads are issued ahead of their adds
+  const float* pp = partial + idx;
+  const long long step = (long long)rows * m;
   float s = 0.f;
-  for (int ks = 0; ks < S; ++ks) s += partial[(long long)ks * rows * m + idx];
+  int ks = 0;
+  for (; ks + 8 <= S; ks += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = pp[(ks + u) * step];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; ks < S; ++ks) s += pp[ks * step];
   out[idx] = ((int)(idx % m) < r ? scale0 : scale1) * s;
 }
 
-// k-slices of a row dot: about 4096 waves in all, at least 8 blocks of 16 k each.
+// k-slices of a row dot: about 4096 waves in all, at least 4 units of 32 k each.
 void rowdot_slices(int rows, int K, int nseg, int& S, int& kb_per)
 {
-  const int tiles = (rows + 15) / 16, nkb = K / 16;
+  const int tiles = (rows + 15) / 16, nu = K / 32;
   S = 4096 / max(1, tiles * nseg);
-  S = max(1, min(S, nkb / 8));
-  kb_per = (nkb + S - 1) / S;
-  S = max(1, (nkb + kb_per - 1) / kb_per);
+  S = max(1, min(S, nu / 4));
+  kb_per = (nu + S - 1) / S;
+  S = max(1, (nu + kb_per - 1) / kb_per);
 }
 
 // ---------------------------------------------------------------- expansions
-// One column per thread and 16 rows per work-group: the thread keeps its column of the factor
-// in registers and forms the rank-r dot with each row's coefficients (uniform across the
-// work-group, so they come through the scalar cache).
+// One column per thread and 16 or 32 rows per work-group, in chunks of 16: the thread loads its
+// column of each segment's factor into registers once for all of the work-group's rows, and the
+// work-group's coefficient rows are staged once in LDS and read back as broadcasts. Two chunks
+// per work-group (the factor read once per 32 output rows) only where that still leaves
+// kExpandMinBlocks work-groups: fewer, longer work-groups measured slower.
 struct ExpandArgs {
   const float* coef;
   int ldc, rows, r, nseg;
   LoraFactor f[2];
   int coff[2], col0[2], ncol[2];
+  int vec[2];  // k-major factor whose rows can be read as float4 (ld % 4 == 0, 16-byte aligned)
+  int chunks;  // 16-row chunks per work-group
   float* out;
   long long ldo;
   int Cout, accumulate;
 };
 
 constexpr int kExpandRows = 16;
+constexpr int kExpandChunks = 2;
+constexpr int kExpandMinBlocks = 768;
 
 __global__ __launch_bounds__(256) void lora_expand_kernel(ExpandArgs a)
 {
-  // The block's coefficient rows (16 rows x up to two segments x r) are the same for every
-  // thread: staged once in LDS and read back as broadcasts, rather than re-read from memory by
-  // every thread for every row.
-  __shared__ __attribute__((aligned(16))) float sc[kExpandRows][2][kLoraMaxRank];
+  __shared__ __attribute__((aligned(16))) float sc[kExpandChunks * kExpandRows][2][kLoraMaxRank];
   const int c = blockIdx.x * 256 + threadIdx.x;
-  const int t0 = blockIdx.y * kExpandRows;
-  const int nr = min(kExpandRows, a.rows - t0);
-  for (int i = threadIdx.x; i < kExpandRows * 2 * kLoraMaxRank; i += 256) {
+  const int span = a.chunks * kExpandRows;
+  const int t0 = blockIdx.y * span;
+  const int nr = min(span, a.rows - t0);
+  for (int i = threadIdx.x; i < span * 2 * kLoraMaxRank; i += 256) {
     const int u = i / (2 * kLoraMaxRank), sg = (i / kLoraMaxRank) & 1, j = i % kLoraMaxRank;
     sc[u][sg][j] = (u < nr && sg < a.nseg && j < a.r) ? a.coef[(long long)(t0 + u) * a.ldc + a.coff[sg] + j] : 0.f;
   }
   __syncthreads();
   if (c >= a.Cout) return;
-  float acc[kExpandRows];
+  float mc[2][kLoraMaxRank];
+  bool in[2];
 #pragma unroll
-  for (int u = 0; u < kExpandRows; ++u)
-    acc[u] = (a.accumulate && u < nr) ? a.out[(long long)(t0 + u) * a.ldo + c] : 0.f;
-  for (int sg = 0; sg < a.nseg; ++sg) {
+  for (int sg = 0; sg < 2; ++sg) {
     const int cc = c - a.col0[sg];
-    if (cc < 0 || cc >= a.ncol[sg]) continue;
-    const LoraFactor f = a.f[sg];
-    float mc[kLoraMaxRank];
-#pragma unroll
-    for (int j = 0; j < kLoraMaxRank; ++j) mc[j] = j < a.r ? factor_at(f, j, cc) : 0.f;
-#pragma unroll
-    for (int u = 0; u < kExpandRows; ++u) {
-      float s = 0.f;
+    in[sg] = sg < a.nseg && cc >= 0 && cc < a.ncol[sg];
+    const LoraFactor& f = a.f[sg];
+    if (in[sg] && a.vec[sg]) {
+      // row cc of a k-major factor: ceil(r / 4) float4s, which stay inside the row (r <= ld, ld % 4 == 0)
+      const f32x4* p = reinterpret_cast<const f32x4*>(f.m + (long long)cc * f.ld);
 #pragma unroll
       for (int j4 = 0; j4 < kLoraMaxRank / 4; ++j4) {
-        if (j4 * 4 < a.r) {  // uniform
-          const float4 cv = *reinterpret_cast<const float4*>(&sc[u][sg][j4 * 4]);
-          s += cv.x * mc[j4 * 4] + cv.y * mc[j4 * 4 + 1] + cv.z * mc[j4 * 4 + 2] + cv.w * mc[j4 * 4 + 3];
-        }
+        const f32x4 v = j4 * 4 < a.r ? p[j4] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) mc[sg][4 * j4 + t] = 4 * j4 + t < a.r ? v[t] : 0.f;
       }
-      acc[u] += f.scale * s;
+    } else {
+#pragma unroll
+      for (int j = 0; j < kLoraMaxRank; ++j) mc[sg][j] = (in[sg] && j < a.r) ? factor_at(f, j, cc) : 0.f;
     }
   }
+  for (int u0 = 0; u0 < nr; u0 += kExpandRows) {
+    float acc[kExpandRows];
 #pragma unroll
-  for (int u = 0; u < kExpandRows; ++u)
-    if (u < nr) a.out[(long long)(t0 + u) * a.ldo + c] = acc[u];
+    for (int u = 0; u < kExpandRows; ++u)
+      acc[u] = (a.accumulate && u0 + u < nr) ? a.out[(long long)(t0 + u0 + u) * a.ldo + c] : 0.f;
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+      if (!in[sg]) continue;
+      const float scale = a.f[sg].scale;
+#pragma unroll
+      for (int u = 0; u < kExpandRows; ++u) {
+        float s = 0.f;
+#pragma unroll
+        for (int j4 = 0; j4 < kLoraMaxRank / 4; ++j4) {
+          if (j4 * 4 < a.r) {  // uniform
+            const f32x4 cv = *reinterpret_cast<const f32x4*>(&sc[u0 + u][sg][j4 * 4]);
+            s += cv.x * mc[sg][j4 * 4] + cv.y * mc[sg][j4 * 4 + 1] + cv.z * mc[sg][j4 * 4 + 2] +
+                 cv.w * mc[sg][j4 * 4 + 3];
+          }
+        }
+        acc[u] += scale * s;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kExpandRows; ++u)
+      if (u0 + u < nr) a.out[(long long)(t0 + u0 + u) * a.ldo + c] = acc[u];
+  }
 }
 
 __global__ __launch_bounds__(256) void lora_slot_sum_kernel(const float* src, int m, const int* pair_of,
@@ -258,22 +333,20 @@ __global__ __launch_bounds__(256) void lora_outer_kernel(OuterArgs a)
   for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[jt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // four blocks of 4 rows per iteration: every load of the 16 rows is issued before the MFMAs
+  // four blocks of 4 rows per step: the rows' pair -> token lookups first, then every load of
+  // the step's 16 rows, then the MFMAs
   for (int qb = q0; qb < q1; qb += 4 * kOuterBlocks) {
-    bool ok[kOuterBlocks];
-    long long row[kOuterBlocks], crow[kOuterBlocks];
+    int row[kOuterBlocks], crow[kOuterBlocks];  // row < 0: no row (past the chunk, or a dropped pair)
     float wq[kOuterBlocks];
 #pragma unroll
     for (int u = 0; u < kOuterBlocks; ++u) {
       const int qq = qb + 4 * u + q;
-      ok[u] = qq < q1;
-      row[u] = qq;
+      const bool in = qq < q1;
+      row[u] = in ? qq : -1;
       crow[u] = qq;
       wq[u] = 1.0f;
-      if (a.pair_of && ok[u]) {
-        const int p = a.pair_of[qq];
-        ok[u] = p >= 0;
-        row[u] = p;
+      if (a.pair_of && in) {
+        row[u] = a.pair_of[qq];
         crow[u] = qq / a.k;
         if (a.topk_w) wq[u] = a.topk_w[qq];
       }
@@ -281,15 +354,15 @@ __global__ __launch_bounds__(256) void lora_outer_kernel(OuterArgs a)
     f32x4 x[kOuterBlocks];
 #pragma unroll
     for (int u = 0; u < kOuterBlocks; ++u)
-      x[u] = (ok[u] && cok) ? src4<KIND>(a.src, row[u], a.c_off + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      x[u] = (row[u] >= 0 && cok) ? src4<KIND>(a.src, row[u], a.c_off + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     float cf[kOuterBlocks][JT];
 #pragma unroll
     for (int u = 0; u < kOuterBlocks; ++u) {
-      const float* cr = a.coef + crow[u] * a.ldc + a.coff;
+      const float* cr = a.coef + (long long)crow[u] * a.ldc + a.coff;
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) {
         const int j = jt * 16 + i;
-        cf[u][jt] = (ok[u] && j < a.m) ? wq[u] * cr[j] : 0.f;
+        cf[u][jt] = (row[u] >= 0 && j < a.m) ? wq[u] * cr[j] : 0.f;
       }
     }
 #pragma unroll
@@ -324,6 +397,18 @@ __global__ __launch_bounds__(256) void lora_outer_reduce_kernel(const float* par
   const long long step = (long long)m * C;
   float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f;
   int rs = 0;
+  for (; rs + 16 <= RS; rs += 16) {  // the same sums, sixteen loads issued ahead of their adds
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = pp[(rs + u) * step];
+#pragma unroll
+    for (int u = 0; u < 16; u += 4) {
+      q0 += v[u];
+      q1 += v[u + 1];
+      q2 += v[u + 2];
+      q3 += v[u + 3];
+    }
+  }
   for (; rs + 4 <= RS; rs += 4) {
     q0 += pp[(rs + 0) * step];
     q1 += pp[(rs + 1) * step];
@@ -373,7 +458,7 @@ hipError_t launch_lora_rowdot(const LoraMat& src, int rows, const int* rows_dev,
                               const LoraFactor* f, const int* koff, float* partial, float* out, hipStream_t s)
 {
   if (rows <= 0) return hipSuccess;
-  if (r > kLoraMaxRank || nseg < 1 || nseg > 2 || K % 16) return hipErrorInvalidValue;
+  if (r > kLoraMaxRank || nseg < 1 || nseg > 2 || K % 32) return hipErrorInvalidValue;
   RowDotArgs a = {};
   a.src = src; a.rows = rows; a.rows_dev = rows_dev; a.K = K; a.r = r; a.nseg = nseg; a.partial = partial;
   rowdot_slices(rows, K, nseg, a.S, a.kb_per);
@@ -410,8 +495,14 @@ hipError_t launch_lora_expand(const float* coef, int ldc, int rows, int r, int n
     a.col0[i] = col0[i];
     a.ncol[i] = ncol[i];
   }
+  for (int i = 0; i < nseg; ++i)
+    a.vec[i] = f[i].kmajor && f[i].ld % 4 == 0 && ((uintptr_t)f[i].m & 15) == 0;
   a.out = out; a.ldo = ldo; a.Cout = Cout; a.accumulate = accumulate;
-  dim3 grid((unsigned)((Cout + 255) / 256), (unsigned)((rows + kExpandRows - 1) / kExpandRows)), block(256);
+  const int col_blocks = (Cout + 255) / 256, row_tiles = (rows + kExpandRows - 1) / kExpandRows;
+  a.chunks = kExpandChunks;
+  while (a.chunks > 1 && (long long)col_blocks * ((row_tiles + a.chunks - 1) / a.chunks) < kExpandMinBlocks)
+    a.chunks /= 2;
+  dim3 grid((unsigned)col_blocks, (unsigned)((row_tiles + a.chunks - 1) / a.chunks)), block(256);
   hipLaunchKernelGGL(lora_expand_kernel, grid, block, 0, s, a);
   return hipGetLastError();
 }
