@@ -7,7 +7,11 @@ w1/w3 [2048, 7168] and w2 [7168, 2048] in MXFP4 (uniform e2m1 codes, E8M0 scales
 renormalised softmax weights, upstream gradient ~N(0,1) fp32. One step = the routed forward
 (saving gate/up for the backward) + the manual backward (dX through the transposed experts,
 GLU derivative, routing-weight gradient). Weights and inputs are resident in HBM before the
-timed region starts; nothing is skipped inside it.
+timed region starts; nothing is skipped inside it. Before the timed regions the layer also gets
+its forward-layout copy of the expert codes (ExpertLayer.prepare_forward_layout: the same bytes
+in the order the small-bucket forward work-groups load them, built once, as a serving process
+would at load time; `config.weight_layout` reports its size and build time;
+--no-forward-layout reads the checkpoint layout only).
 
 Prints one JSON line. `value` is MoE-layer fwd+bwd tokens/s; `roofline` is the dominant
 kernel's algorithmic weight bytes per launch over its mean duration, measured with HIP events
@@ -82,6 +86,20 @@ def make_layer(seed: int):
 
     return ExpertLayer(codes(E, F, D // 2), scales(E, F, D // 32), codes(E, F, D // 2), scales(E, F, D // 32),
                        codes(E, D, F // 2), scales(E, D, F // 32))
+
+
+def forward_layout(args, layer) -> dict:
+    """Builds the layer's forward-layout copy of the expert codes (a one-time load step, outside
+    every timed region) unless --no-forward-layout; returns what the JSON line reports of it."""
+    if args.no_forward_layout:
+        return {"forward_layout": False}
+    torch.cuda.synchronize()
+    t0 = time.time()
+    extra = layer.prepare_forward_layout()
+    torch.cuda.synchronize()
+    ms = (time.time() - t0) * 1e3
+    log(f"[bench] forward layout: {extra / 1e9:.2f} GB more in HBM, built in {ms:.1f} ms")
+    return {"forward_layout": True, "forward_layout_bytes": extra, "forward_layout_build_ms": round(ms, 1)}
 
 
 def make_inputs(seed: int, routing: str):
@@ -170,6 +188,7 @@ def expert_sweep(args, k, Ms):
     scales = lambda *sh: torch.randint(117, 122, sh, dtype=torch.uint8, device="cuda", generator=gen)
     layer = ExpertLayer(codes(copies, F, D // 2), scales(copies, F, D // 32), codes(copies, F, D // 2),
                         scales(copies, F, D // 32), codes(copies, D, F // 2), scales(copies, D, F // 32))
+    forward_layout(args, layer)
     sweep = []
     for M in Ms:
         n = copies * M
@@ -328,6 +347,8 @@ def main():
     ap.add_argument("--ring", type=int, default=2, help="stream: distinct pinned host layers cycled through")
     ap.add_argument("--lora-rank", type=int, default=0,
                     help="rank of the layer's gate/up/down LoRA adapters (0: off, the BASELINE configs)")
+    ap.add_argument("--no-forward-layout", action="store_true",
+                    help="read only the checkpoint layout (no forward-layout copy of the expert codes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (reference kernel for rocprof byte counters)")
     args = ap.parse_args()
@@ -351,6 +372,7 @@ def main():
         return
     t_setup = time.time()
     layer = make_layer(0)
+    layout = forward_layout(args, layer)
     H, I, W, G = make_inputs(1, args.routing)
     n_active = int(torch.unique(I).numel())
     ws = torch.empty(k.moe_workspace_bytes(N, TOPK, E, D, F), dtype=torch.uint8, device="cuda")
@@ -430,6 +452,7 @@ def main():
             "arithmetic": "MXFP4 weights x two-term e4m3 activations (fwd, fp4-native scaled MFMA) / exact bf16 "
                           "decode x two-term bf16 gradients (bwd, bf16 MFMA), fp32 accumulate",
             "weight_bytes_per_step": step_bytes,
+            "weight_layout": layout,
         },
         "weight_GBps": step_gbs,
         "weight_frac_of_hbm_peak": step_gbs / PEAK_HBM_GBS,

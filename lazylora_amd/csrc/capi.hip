@@ -211,6 +211,20 @@ int check_lora(const float* const* lora, const float* scaling, int rank, Lora& l
   return MXFP4_OK;
 }
 
+// Forward-layout copies {W1, W3, W2} (null array or entries: that product reads the checkpoint
+// layout). An entry needs its matrix's K (D for W1 and W3, F for W2) to be a multiple of 512.
+int check_forward_layout(const uint8_t* const* fl, int D, int F)
+{
+  if (!fl) return MXFP4_OK;
+  for (int i = 0; i < 3; ++i) {
+    if (!fl[i]) continue;
+    if ((i < 2 ? D : F) % 512) return fail(MXFP4_EINVAL, "moe: a forward layout needs its K to be a multiple of 512%s");
+    if (!aligned16(fl[i])) return fail(MXFP4_EINVAL, "moe: forward layouts must be 16-byte aligned%s");
+  }
+  if (!fl[0] != !fl[1]) return fail(MXFP4_EINVAL, "moe: give the forward layouts of W1 and W3 together%s");
+  return MXFP4_OK;
+}
+
 mx::LoraMat mat_f32(const void* p, long long ld) { return mx::LoraMat{mx::kLoraF32, p, nullptr, ld, 0, 0}; }
 mx::LoraFactor jmajor(const float* m, long long ld, float scale) { return mx::LoraFactor{m, ld, 0, scale}; }
 mx::LoraFactor kmajor(const float* m, long long ld, float scale) { return mx::LoraFactor{m, ld, 1, scale}; }
@@ -220,8 +234,8 @@ mx::LoraFactor kmajor(const float* m, long long ld, float scale) { return mx::Lo
 // epilogue), v = A_down act per pair and V = sum over a token's slots of w * v; gate|up are
 // then always saved, since v and the backward read them.
 int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const float* w, int N, int k,
-              const uint8_t* const* wts, int E, int D, int F, int act_kind, bool save, const Lora& lo, void* ws,
-              const MoeLayout& L, hipStream_t s)
+              const uint8_t* const* wts, const uint8_t* const* fl, int E, int D, int F, int act_kind, bool save,
+              const Lora& lo, void* ws, const MoeLayout& L, hipStream_t s)
 {
   const long long P = (long long)N * k;
   MX_TRY(mx::launch_route(idx, idx_dtype == MXFP4_I64, w, N, k, E, at<int>(ws, L.counts), at<int>(ws, L.offsets),
@@ -256,6 +270,10 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   a.n_ct = F / 32;
   a.q_tiles = at<uint8_t>(ws, L.at_act);
   set_buckets(a, ws, L);
+  if (fl && fl[0] && fl[1]) {
+    a.fl0 = fl[0]; a.fl1 = fl[1];
+    a.fl_estride = mx::forward_layout_bytes(F, D);
+  }
   a.save = (save || lo.r) ? at<float>(ws, L.saved) : nullptr;
   a.act_kind = act_kind;
   const int r = lo.r;
@@ -453,14 +471,37 @@ size_t mxfp4_moe_workspace_size(int N, int k, int E, int D, int F)
   return moe_layout(N, k, E, D, F).end;
 }
 
-int mxfp4_moe_forward_lora(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
-                           const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s,
-                           const uint8_t* w3p, const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, int E,
-                           int D, int F, int act_kind, const float* const* lora, const float* lora_scaling,
-                           int lora_rank, int flags, void* workspace, size_t workspace_bytes, hipStream_t stream)
+size_t mxfp4_forward_layout_bytes(int E, int R, int K)
+{
+  if (E <= 0 || R <= 0 || K <= 0 || K % 512) return 0;
+  return (size_t)E * (size_t)mx::forward_layout_bytes(R, K);
+}
+
+int mxfp4_forward_layout(uint8_t* dst, const uint8_t* packed, int E, int R, int K, hipStream_t stream)
+{
+  if (E < 0 || R < 0 || K <= 0 || K % 512)
+    return fail(MXFP4_EINVAL, "forward_layout: K must be a positive multiple of 512%s");
+  if (E == 0 || R == 0) return MXFP4_OK;
+  if (!dst || !packed) return fail(MXFP4_EINVAL, "forward_layout: null pointer%s");
+  if (!aligned16(dst) || !aligned16(packed))
+    return fail(MXFP4_EINVAL, "forward_layout: dst and packed must be 16-byte aligned%s");
+  const uintptr_t d0 = (uintptr_t)dst, d1 = d0 + mxfp4_forward_layout_bytes(E, R, K);
+  const uintptr_t p0 = (uintptr_t)packed, p1 = p0 + (size_t)E * R * (K / 2);
+  if (d0 < p1 && p0 < d1) return fail(MXFP4_EINVAL, "forward_layout: dst overlaps packed%s");
+  MX_TRY(mx::launch_forward_layout(packed, dst, E, R, K, stream), "forward_layout");
+  return MXFP4_OK;
+}
+
+int mxfp4_moe_forward_fl(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
+                         const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p,
+                         const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, const uint8_t* const* fwd_layout,
+                         int E, int D, int F, int act_kind, const float* const* lora, const float* lora_scaling,
+                         int lora_rank, int flags, void* workspace, size_t workspace_bytes, hipStream_t stream)
 {
   const uint8_t* wts[6] = {w1p, w1s, w3p, w3s, w2p, w2s};
   int rc = check_moe_args(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind);
+  if (rc) return rc;
+  rc = check_forward_layout(fwd_layout, D, F);
   if (rc) return rc;
   Lora lo;
   rc = check_lora(lora, lora_scaling, lora_rank, lo);
@@ -471,11 +512,15 @@ int mxfp4_moe_forward_lora(float* out, const void* h, int h_dtype, const void* t
   if (!workspace || workspace_bytes < L.end) return fail(MXFP4_EWORKSPACE, "moe_forward: workspace too small%s");
   if (N == 0) return MXFP4_OK;
   MX_TRY(g_timer.begin(stream), "phase timer");
-  rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, (flags & MXFP4_MOE_SAVE) != 0,
-                 lo, workspace, L, stream);
+  rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, fwd_layout, E, D, F, act_kind,
+                 (flags & MXFP4_MOE_SAVE) != 0, lo, workspace, L, stream);
   if (rc) return rc;
   mx::FwdArgs a = {};
   a.wp0 = w2p; a.ws0 = w2s;
+  if (fwd_layout && fwd_layout[2]) {
+    a.fl0 = fwd_layout[2];
+    a.fl_estride = mx::forward_layout_bytes(D, F);
+  }
   a.wp_estride = (long long)F * D / 2;
   a.ws_estride = (long long)F * D / 32;
   a.R = D; a.K = F;
@@ -501,6 +546,17 @@ int mxfp4_moe_forward_lora(float* out, const void* h, int h_dtype, const void* t
   return MXFP4_OK;
 }
 
+int mxfp4_moe_forward_lora(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
+                           const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s,
+                           const uint8_t* w3p, const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, int E,
+                           int D, int F, int act_kind, const float* const* lora, const float* lora_scaling,
+                           int lora_rank, int flags, void* workspace, size_t workspace_bytes, hipStream_t stream)
+{
+  return mxfp4_moe_forward_fl(out, h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, w1p, w1s, w3p, w3s, w2p, w2s,
+                              nullptr, E, D, F, act_kind, lora, lora_scaling, lora_rank, flags, workspace,
+                              workspace_bytes, stream);
+}
+
 int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
                       const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p,
                       const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, int E, int D, int F, int act_kind,
@@ -510,16 +566,18 @@ int mxfp4_moe_forward(float* out, const void* h, int h_dtype, const void* topk_i
                                 D, F, act_kind, nullptr, nullptr, 0, flags, workspace, workspace_bytes, stream);
 }
 
-int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out, const void* h, int h_dtype,
-                            const void* topk_idx, int idx_dtype, const float* topk_w, int N, int k,
-                            const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p, const uint8_t* w3s,
-                            const uint8_t* w2p, const uint8_t* w2s, int E, int D, int F, int act_kind,
-                            const float* const* lora, const float* lora_scaling, int lora_rank,
-                            float* const* lora_grads, int flags, void* workspace, size_t workspace_bytes,
-                            hipStream_t stream)
+int mxfp4_moe_backward_fl(float* grad_h, float* grad_w, const float* grad_out, const void* h, int h_dtype,
+                          const void* topk_idx, int idx_dtype, const float* topk_w, int N, int k, const uint8_t* w1p,
+                          const uint8_t* w1s, const uint8_t* w3p, const uint8_t* w3s, const uint8_t* w2p,
+                          const uint8_t* w2s, const uint8_t* const* fwd_layout, int E, int D, int F, int act_kind,
+                          const float* const* lora, const float* lora_scaling, int lora_rank,
+                          float* const* lora_grads, int flags, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream)
 {
   const uint8_t* wts[6] = {w1p, w1s, w3p, w3s, w2p, w2s};
   int rc = check_moe_args(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind);
+  if (rc) return rc;
+  rc = check_forward_layout(fwd_layout, D, F);
   if (rc) return rc;
   Lora lo;
   rc = check_lora(lora, lora_scaling, lora_rank, lo);
@@ -544,8 +602,8 @@ int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out,
   }
   MX_TRY(g_timer.begin(stream), "phase timer");
   if (!(flags & MXFP4_MOE_REUSE_FORWARD)) {
-    rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind, true, lo, workspace, L,
-                   stream);
+    rc = moe_front(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, fwd_layout, E, D, F, act_kind, true, lo,
+                   workspace, L, stream);
     if (rc) return rc;
   }
   // grad_out -> bf16 hi + lo, the A operand of the W2 transposed product
@@ -657,6 +715,19 @@ int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out,
     MX_PHASE("lora_grads", stream);
   }
   return MXFP4_OK;
+}
+
+int mxfp4_moe_backward_lora(float* grad_h, float* grad_w, const float* grad_out, const void* h, int h_dtype,
+                            const void* topk_idx, int idx_dtype, const float* topk_w, int N, int k,
+                            const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p, const uint8_t* w3s,
+                            const uint8_t* w2p, const uint8_t* w2s, int E, int D, int F, int act_kind,
+                            const float* const* lora, const float* lora_scaling, int lora_rank,
+                            float* const* lora_grads, int flags, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream)
+{
+  return mxfp4_moe_backward_fl(grad_h, grad_w, grad_out, h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, w1p, w1s,
+                               w3p, w3s, w2p, w2s, nullptr, E, D, F, act_kind, lora, lora_scaling, lora_rank,
+                               lora_grads, flags, workspace, workspace_bytes, stream);
 }
 
 int mxfp4_moe_backward(float* grad_h, float* grad_w, const float* grad_out, const void* h, int h_dtype,

@@ -350,9 +350,11 @@ __device__ __forceinline__ void epilogue_direct(const FwdArgs& a, const WorkItem
 
 
 // One work item: the 16 x 64 tile (w.tile, w.ct) over all of K, then its epilogue.
-template <int MODE, bool FAST>
+// FL: the weights come from the forward layout (fl0 / fl1), one 1 KiB block per load instruction
+template <int MODE, bool FAST, bool FL>
 __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, int wave, int lane)
 {
+  static_assert(FAST || !FL, "the forward layout is read by the fast path only");
   __shared__ FwdLds lds;  // used by the fast path only
   const int j = lane & 15, g = lane >> 4;
   const int nb = a.K / kGroup;
@@ -436,21 +438,39 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
     // weights of chunk c through one buffer resource per column group: a fixed per-lane offset
     // + 256 c (uniform) + 16 q (immediate). A chunk past the last is requested from an empty
     // resource: zeros, no memory traffic, and the same count of loads in vmcnt.
+    // Forward layout: the column group's 16 rows are row group rg, whose chunk c is the 4 KiB at
+    // (rg * nsc + c) * 4096 and holds MFMA q's operand at q * 1024, lane l's 16 B at l * 16: the
+    // same bytes, each load instruction one contiguous 1 KiB.
     rsrc_t wr[4], wr_none[4];
     uint32_t woff[4];
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
-      const uint8_t* base = grp_wp(grp);
-      wr[grp] = make_rsrc(base, (uint32_t)a.R * (uint32_t)(a.K / 2));
-      wr_none[grp] = make_rsrc(base, 0);
-      woff[grp] = (uint32_t)(wrow[grp] - base) + boff[grp];
+      if constexpr (FL) {
+        // the resource starts at the row group, so the lane offset is the same for all four
+        const int rg = min(grp_row(grp), a.R - 1) / 16;
+        const uint8_t* base = (MODE == kFwdGateUp && grp >= 2 ? a.fl1 : a.fl0) + (long long)w.expert * a.fl_estride +
+                              (long long)rg * nsc * 4096;
+        wr[grp] = make_rsrc(base, (uint32_t)((a.R + 15) / 16 - rg) * (uint32_t)nsc * 4096u);
+        wr_none[grp] = make_rsrc(base, 0);
+        woff[grp] = (uint32_t)lane * 16u;
+      } else {
+        const uint8_t* base = grp_wp(grp);
+        wr[grp] = make_rsrc(base, (uint32_t)a.R * (uint32_t)(a.K / 2));
+        wr_none[grp] = make_rsrc(base, 0);
+        woff[grp] = (uint32_t)(wrow[grp] - base) + boff[grp];
+      }
     }
     auto load_b_buf = [&](int c, i32x4 (&b)[4][4]) {
       const bool live = c < nsc;  // uniform
 #pragma unroll
       for (int grp = 0; grp < 4; ++grp)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b[grp][q] = buf16(live ? wr[grp] : wr_none[grp], woff[grp] + 16 * q, (uint32_t)c * 256);
+        for (int q = 0; q < 4; ++q) {
+          if constexpr (FL)
+            b[grp][q] = buf16(live ? wr[grp] : wr_none[grp], woff[grp] + 1024 * q, (uint32_t)c * 4096);
+          else
+            b[grp][q] = buf16(live ? wr[grp] : wr_none[grp], woff[grp] + 16 * q, (uint32_t)c * 256);
+        }
     };
 
     // Two chunks of weights in flight: a buffer is refilled with chunk c + 2 as soon as chunk
@@ -569,7 +589,7 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
   if (w.active) epilogue_direct<MODE>(a, w, lane, acc, tw);
 }
 
-template <int MODE, bool FAST>
+template <int MODE, bool FAST, bool FL>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
 {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -582,7 +602,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
     // recompute lane-derived addresses per item instead of holding them across items
     int l = lane;
     asm volatile("" : "+v"(l));
-    fwd_item<MODE, FAST>(a, w, wave, l);
+    fwd_item<MODE, FAST, FL>(a, w, wave, l);
   }
 }
 
@@ -830,14 +850,22 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
     b.small_tiles = nullptr;
     b.groups = nullptr;
   }
+  // the one-tile work-groups read the forward layout when every matrix of the product has one
+  // (and its byte count fits a buffer resource, as for the checkpoint layout)
+  const bool fl = fast && mode != kFwdPlain && a.fl0 && (mode != kFwdGateUp || a.fl1) &&
+                  forward_layout_bytes(a.R, a.K) < (1LL << 32);
   dim3 grid((unsigned)blocks), block(64 * kWavesPerGroup);
-#define MX_LAUNCH(M, F) hipLaunchKernelGGL((fwd_kernel<M, F>), grid, block, 0, s, b)
+#define MX_LAUNCH(M, F, L) hipLaunchKernelGGL((fwd_kernel<M, F, L>), grid, block, 0, s, b)
   if (mode == kFwdPlain) {
-    if (fast) MX_LAUNCH(kFwdPlain, true); else MX_LAUNCH(kFwdPlain, false);
+    if (fast) MX_LAUNCH(kFwdPlain, true, false); else MX_LAUNCH(kFwdPlain, false, false);
   } else if (mode == kFwdGateUp) {
-    if (fast) MX_LAUNCH(kFwdGateUp, true); else MX_LAUNCH(kFwdGateUp, false);
+    if (fl) MX_LAUNCH(kFwdGateUp, true, true);
+    else if (fast) MX_LAUNCH(kFwdGateUp, true, false);
+    else MX_LAUNCH(kFwdGateUp, false, false);
   } else {
-    if (fast) MX_LAUNCH(kFwdDown, true); else MX_LAUNCH(kFwdDown, false);
+    if (fl) MX_LAUNCH(kFwdDown, true, true);
+    else if (fast) MX_LAUNCH(kFwdDown, true, false);
+    else MX_LAUNCH(kFwdDown, false, false);
   }
 #undef MX_LAUNCH
   hipError_t e = hipGetLastError();
@@ -846,6 +874,48 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   if (mode == kFwdGateUp) hipLaunchKernelGGL(fwd_gemm_kernel<kFwdGateUp>, mgrid, mblock, 0, s, b);
   else if (mode == kFwdDown) hipLaunchKernelGGL(fwd_gemm_kernel<kFwdDown>, mgrid, mblock, 0, s, b);
   else hipLaunchKernelGGL(fwd_gemm_kernel<kFwdPlain>, mgrid, mblock, 0, s, b);
+  return hipGetLastError();
+}
+
+long long forward_layout_bytes(int R, int K)
+{
+  return (long long)((R + 15) / 16) * (K / kChunk) * 4096;
+}
+
+namespace {
+
+// One thread per 16-byte piece of the forward layout: piece l of operand block q of super-chunk
+// c of row group rg (at byte ((rg * nsc + c) * 4 + q) * 1024 + l * 16 of the expert's layout)
+// is MX block 4 (l / 16) + q of that super-chunk of row 16 rg + l % 16, the 16 bytes lane l of
+// the one-tile kernels reads for MFMA q; rows past R repeat row R - 1, as those kernels' loads do.
+__global__ __launch_bounds__(256) void forward_layout_kernel(const uint8_t* packed, uint8_t* out, int R, int K,
+                                                             long long per_expert, long long total)
+{
+  const long long p = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (p >= total) return;
+  const int nsc = K / kChunk;
+  const long long e = p / per_expert;
+  long long r = p - e * per_expert;
+  const int l = (int)(r & 63);
+  r >>= 6;
+  const int q = (int)(r & 3);
+  r >>= 2;
+  const int rg = (int)(r / nsc), c = (int)(r - (long long)rg * nsc);
+  const int row = min(rg * 16 + (l & 15), R - 1);
+  const uint8_t* src = packed + (e * R + row) * (long long)(K / 2) + c * 256 + (4 * (l >> 4) + q) * 16;
+  *reinterpret_cast<i32x4*>(out + p * 16) = *reinterpret_cast<const i32x4*>(src);
+}
+
+}  // namespace
+
+hipError_t launch_forward_layout(const uint8_t* packed, uint8_t* out, int E, int R, int K, hipStream_t s)
+{
+  if (E <= 0 || R <= 0) return hipSuccess;
+  if (K <= 0 || K % kChunk) return hipErrorInvalidValue;
+  const long long per_expert = forward_layout_bytes(R, K) / 16;
+  const long long total = per_expert * E;
+  hipLaunchKernelGGL(forward_layout_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, packed, out, R,
+                     K, per_expert, total);
   return hipGetLastError();
 }
 

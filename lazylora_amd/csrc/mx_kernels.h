@@ -54,7 +54,19 @@ struct FwdArgs {
   const int* n_small;
   const int4* groups;
   const int* n_groups;
+  // Forward layout (launch_forward_layout) of W (W1 for kFwdGateUp) and W3, or null: the
+  // one-tile work-groups then load whole 1 KiB operand blocks; everything else reads wp* / ws*.
+  const uint8_t* fl0;
+  const uint8_t* fl1;
+  long long fl_estride;  // bytes between experts in fl*
 };
+
+// Forward layout of E stacked packed [R, K] matrices (K a multiple of 512), per expert
+// forward_layout_bytes(R, K) bytes: the 4 KiB at (rg * K / 512 + c) * 4096 hold super-chunk c of
+// the 16 rows 16 rg .., MFMA q's operand block at q * 1024, lane l's 16 bytes (MX block
+// 4 (l / 16) + q of row 16 rg + l % 16) at l * 16; rows past R repeat row R - 1.
+long long forward_layout_bytes(int R, int K);
+hipError_t launch_forward_layout(const uint8_t* packed, uint8_t* out, int E, int R, int K, hipStream_t s);
 
 // ---------------------------------------------------------------- transposed products
 enum BwdMode : int {

@@ -12,6 +12,7 @@ as six stacked, expert-major tensors and every routed-layer call reads experts b
 
 Roles follow the reference: w1 = gate, w3 = up, w2 = down (expert_streamer.py:229-246).
 """
+import ctypes
 from typing import Iterable, Optional, Sequence
 
 import torch
@@ -42,6 +43,7 @@ class ExpertLayer:
         self.E, self.D, self.F = E, D, F
         (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s) = [
             _aligned16(t.to(self.device, non_blocking=True).contiguous()) for t in tensors]
+        self._fl = None  # forward-layout copies (W1, W3, W2; None where K is not a multiple of 512)
 
     @classmethod
     def empty(cls, E: int, D: int, F: int, device=None) -> "ExpertLayer":
@@ -92,6 +94,32 @@ class ExpertLayer:
                 dst[eid].copy_(src, non_blocking=True)
             stacked.append(dst)
         return cls(*stacked, device=device)
+
+    def prepare_forward_layout(self) -> int:
+        """Builds the forward-layout copies of W1, W3 (when D is a multiple of 512) and W2 (when F
+        is), which the routed forward's small-bucket work-groups then read with whole 1 KiB loads
+        (mxfp4_forward_layout; results are bit-identical). Each copy holds as many bytes as the
+        packed codes it copies; returns the bytes added. The copies reflect the weights as they
+        are now: rebuild them after writing new weights (loader.upload drops them)."""
+        from lazylora_amd.native import kernel
+
+        k = kernel()
+        if k is None:
+            raise RuntimeError("the forward layout needs the native library on a GPU")
+        w13 = (k.forward_layout(self.w1p), k.forward_layout(self.w3p)) if self.D % 512 == 0 else (None, None)
+        w2 = k.forward_layout(self.w2p) if self.F % 512 == 0 else None
+        self._fl = (w13[0], w13[1], w2)
+        return sum(t.numel() for t in self._fl if t is not None)
+
+    def drop_forward_layout(self) -> None:
+        """Forgets the forward-layout copies (the routed calls then read the checkpoint layout)."""
+        self._fl = None
+
+    def forward_layout_pointers(self):
+        """Host array of the three forward-layout device pointers for mxfp4_moe_*_fl, or None."""
+        if self._fl is None:
+            return None
+        return (ctypes.c_void_p * 3)(*[t.data_ptr() if t is not None else None for t in self._fl])
 
     def pointers(self):
         return (self.w1p.data_ptr(), self.w1s.data_ptr(), self.w3p.data_ptr(), self.w3s.data_ptr(),

@@ -84,6 +84,16 @@ def _load_library() -> ctypes.CDLL:
     lib.mxfp4_moe_backward_lora.restype = ci
     lib.mxfp4_moe_backward_lora.argtypes = [vp, vp, vp, vp, ci, vp, ci, vp, ci, ci, vp, vp, vp, vp, vp, vp,
                                             ci, ci, ci, ci, vp, vp, ci, vp, ci, vp, sz, vp]
+    lib.mxfp4_moe_forward_fl.restype = ci
+    lib.mxfp4_moe_forward_fl.argtypes = [vp, vp, ci, vp, ci, vp, ci, ci, vp, vp, vp, vp, vp, vp, vp,
+                                         ci, ci, ci, ci, vp, vp, ci, ci, vp, sz, vp]
+    lib.mxfp4_moe_backward_fl.restype = ci
+    lib.mxfp4_moe_backward_fl.argtypes = [vp, vp, vp, vp, ci, vp, ci, vp, ci, ci, vp, vp, vp, vp, vp, vp, vp,
+                                          ci, ci, ci, ci, vp, vp, ci, vp, ci, vp, sz, vp]
+    lib.mxfp4_forward_layout_bytes.restype = sz
+    lib.mxfp4_forward_layout_bytes.argtypes = [ci, ci, ci]
+    lib.mxfp4_forward_layout.restype = ci
+    lib.mxfp4_forward_layout.argtypes = [vp, vp, ci, ci, ci, vp]
     lib.mxfp4_moe_route_status.restype = ci
     lib.mxfp4_moe_route_status.argtypes = [vp, vp, vp]
     lib.mxfp4_router_topk.restype = ci
@@ -201,6 +211,25 @@ class MXFP4Kernel:
         """Parallel width of the device (compute units), the analogue of mxfp4_threads()."""
         return int(self.lib.mxfp4_threads())
 
+    def forward_layout(self, packed: torch.Tensor) -> torch.Tensor:
+        """The forward layout (mxfp4_forward_layout) of stacked packed matrices [E, R, K/2] uint8
+        in HBM, K a multiple of 512: a new flat uint8 tensor on the same device. No counterpart
+        in the reference; ExpertLayer.prepare_forward_layout keeps these for a resident layer."""
+        if packed.dtype != torch.uint8 or packed.dim() != 3 or not packed.is_cuda:
+            raise ValueError("packed must be a CUDA uint8 tensor [E, R, K/2]")
+        E, R, Kh = packed.shape
+        K = 2 * Kh
+        if K % 512:
+            raise ValueError(f"the forward layout needs K to be a multiple of 512, got K={K}")
+        src = packed.contiguous()
+        if src.data_ptr() % 16:
+            src = src.clone()
+        n = int(self.lib.mxfp4_forward_layout_bytes(E, R, K))
+        out = torch.empty(max(n, 16), dtype=torch.uint8, device=packed.device)
+        _check(self.lib.mxfp4_forward_layout(out.data_ptr(), src.data_ptr(), E, R, K, _stream(packed.device)),
+               self.lib)
+        return out
+
     # -- routed layer ------------------------------------------------------------------------
     def routed_forward(self, h: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                        experts, act="swiglu", save_for_backward: bool = False,
@@ -216,11 +245,11 @@ class MXFP4Kernel:
         call = _RoutedCall(self.lib, h, topk_indices, topk_weights, experts, act, workspace)
         lo = _LoraCall(lora, call.dev, call.D, call.F)
         out = torch.empty((call.N, call.D), dtype=torch.float32, device=call.dev)
-        _check(self.lib.mxfp4_moe_forward_lora(
+        _check(self.lib.mxfp4_moe_forward_fl(
             out.data_ptr(), call.h.data_ptr(), call.h_dtype, call.idx.data_ptr(), call.idx_dtype,
-            call.w.data_ptr(), call.N, call.k, *experts.pointers(), experts.E, call.D, call.F, call.act,
-            lo.ptrs, lo.scaling, lo.r, MOE_SAVE if save_for_backward else 0, call.ws.data_ptr(), call.nws,
-            _stream(call.dev)), self.lib)
+            call.w.data_ptr(), call.N, call.k, *experts.pointers(), experts.forward_layout_pointers(), experts.E,
+            call.D, call.F, call.act, lo.ptrs, lo.scaling, lo.r, MOE_SAVE if save_for_backward else 0,
+            call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
         return out
 
     def routed_backward(self, h: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
@@ -246,10 +275,10 @@ class MXFP4Kernel:
         grad_w = torch.empty((call.N, call.k), dtype=torch.float32, device=call.dev)
         grads = [torch.empty_like(t) for t in lo.tensors]
         gptrs = (ctypes.c_void_p * 6)(*[t.data_ptr() for t in grads]) if lo.r else None
-        _check(self.lib.mxfp4_moe_backward_lora(
+        _check(self.lib.mxfp4_moe_backward_fl(
             grad_h.data_ptr(), grad_w.data_ptr(), g.data_ptr(), call.h.data_ptr(), call.h_dtype,
             call.idx.data_ptr(), call.idx_dtype, call.w.data_ptr(), call.N, call.k, *experts.pointers(),
-            experts.E, call.D, call.F, call.act, lo.ptrs, lo.scaling, lo.r, gptrs,
+            experts.forward_layout_pointers(), experts.E, call.D, call.F, call.act, lo.ptrs, lo.scaling, lo.r, gptrs,
             MOE_REUSE_FORWARD if reuse_forward else 0, call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
         if lo.r:
             return grad_h, grad_w, tuple(grads)

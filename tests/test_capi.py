@@ -67,6 +67,39 @@ def test_host_side_argument_errors(lib):
     assert lib.mxfp4_router_topk_backward(dummy, dummy, dummy, dummy, 4, 8, 9, 1.0, 1, None) == -1
 
 
+def test_forward_layout_host_checks(lib):
+    vp = ctypes.c_void_p
+    dummy = vp(256)  # never dereferenced: every call below fails (or finishes) before a launch
+    # 2 experts x 3 row groups (R = 40: the last group holds 8 rows) x 2 super-chunks x 4 KiB
+    assert lib.mxfp4_forward_layout_bytes(2, 40, 1024) == 2 * 3 * 2 * 4096
+    assert lib.mxfp4_forward_layout_bytes(2, 40, 1056) == 0  # K not a multiple of 512
+    assert lib.mxfp4_forward_layout(dummy, dummy, 2, 40, 1056, None) == -1
+    assert b"multiple of 512" in lib.mxfp4_last_error()
+    assert lib.mxfp4_forward_layout(None, dummy, 2, 40, 1024, None) == -1     # null output
+    assert lib.mxfp4_forward_layout(vp(264), dummy, 2, 40, 1024, None) == -1  # unaligned output
+    assert lib.mxfp4_forward_layout(dummy, vp(256 + 4096), 2, 40, 1024, None) == -1  # overlapping
+    assert b"overlaps" in lib.mxfp4_last_error()
+    assert lib.mxfp4_forward_layout(None, None, 0, 40, 1024, None) == 0       # E = 0: no-op
+    # the routed calls with forward layouts {W1, W3, W2}: D = 1024, F = 544
+    args = [dummy, dummy, 0, dummy, 3, dummy, 4, 2] + [dummy] * 6
+    tail = [8, 1024, 544, 0, None, None, 0, 0, dummy, 1 << 40, None]
+    fl_w2 = (vp * 3)(None, None, 256)      # W2's K = F = 544 is not a multiple of 512
+    assert lib.mxfp4_moe_forward_fl(*args, fl_w2, *tail) == -1
+    assert b"multiple of 512" in lib.mxfp4_last_error()
+    fl_w1 = (vp * 3)(256, None, None)      # W1 without W3
+    assert lib.mxfp4_moe_forward_fl(*args, fl_w1, *tail) == -1
+    assert b"together" in lib.mxfp4_last_error()
+    fl_odd = (vp * 3)(256, 264, None)      # unaligned
+    assert lib.mxfp4_moe_forward_fl(*args, fl_odd, *tail) == -1
+    btail = [8, 1024, 544, 0, None, None, 0, None, 0, dummy, 1 << 40, None]
+    assert lib.mxfp4_moe_backward_fl(dummy, dummy, dummy, dummy, 0, dummy, 3, dummy, 4, 2, *([dummy] * 6),
+                                     fl_w1, *btail) == -1
+    # without tokens the forward has nothing to do: valid layouts and no launch
+    ok = (vp * 3)(256, 512, None)
+    tail0 = [8, 1024, 544, 0, None, None, 0, 0, dummy, 1 << 40, None]
+    assert lib.mxfp4_moe_forward_fl(dummy, dummy, 0, dummy, 3, dummy, 0, 2, *([dummy] * 6), ok, *tail0) == 0
+
+
 def test_python_api_validation(lib):
     from lazylora_amd import native
     k = native.MXFP4Kernel(lib)  # the shape checks run before any device is needed
