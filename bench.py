@@ -9,7 +9,7 @@ renormalised softmax weights, upstream gradient ~N(0,1) fp32. One step = the rou
 GLU derivative, routing-weight gradient). Weights and inputs are resident in HBM before the
 timed region starts; nothing is skipped inside it. Before the timed regions the layer also gets
 its forward-layout copy of the expert codes (ExpertLayer.prepare_forward_layout: the same bytes
-in the order the small-bucket forward work-groups load them, built once, as a serving process
+in the order the forward work-groups load them, built once, as a serving process
 would at load time; `config.weight_layout` reports its size and build time;
 --no-forward-layout reads the checkpoint layout only).
 

@@ -166,8 +166,9 @@ int mxfp4_moe_backward_lora(float *grad_h, float *grad_w, const float *grad_out,
  * callers that keep a layer resident in HBM over many steps. For E stacked packed [R, K]
  * matrices (K a multiple of 512) mxfp4_forward_layout writes mxfp4_forward_layout_bytes(E, R, K)
  * bytes: per expert, 16-row group and 512-element super-chunk, the 4 KiB of codes that the
- * small-bucket forward work-groups read, in the order their load instructions consume them (each
- * instruction then reads 1 KiB contiguous instead of 16-byte pieces of 16 rows). Scales are not
+ * one-tile forward work-groups read, in the order their load instructions consume them (each
+ * instruction then reads 1 KiB contiguous instead of 16-byte pieces of 16 rows; the large-bucket
+ * work-groups' copies read four 256-byte runs instead of 16 rows' 64-byte runs). Scales are not
  * copied. The copy must be rebuilt whenever the weights change. dst and packed: 16-byte aligned,
  * not overlapping. */
 size_t mxfp4_forward_layout_bytes(int E, int R, int K);
@@ -178,8 +179,8 @@ int mxfp4_forward_layout(uint8_t *dst, const uint8_t *packed, int E, int R, int 
  * a host array of 3 device pointers {W1, W3, W2}, the mxfp4_forward_layout of w1p, w3p, w2p (W1
  * and W3 both or neither; NULL entries, or a NULL array, read the checkpoint layout). An entry
  * needs its K (D for W1 and W3, F for W2) to be a multiple of 512. Results are bit-identical to
- * the calls without forward layouts; w1p, w3p, w2p are still read (large buckets and the
- * transposed products use them). */
+ * the calls without forward layouts; w1p, w3p, w2p are still read (the transposed products use
+ * them). */
 int mxfp4_moe_forward_fl(float *out, const void *h, int h_dtype, const void *topk_idx,
                          int idx_dtype, const float *topk_w, int N, int k, const uint8_t *w1p,
                          const uint8_t *w1s, const uint8_t *w3p, const uint8_t *w3s,

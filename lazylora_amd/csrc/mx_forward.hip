@@ -636,7 +636,9 @@ struct GemmLds {
   uint8_t sa[kGmT * 512];                      // activation scales of a super-chunk: [tile][512 B]
 };
 
-template <int MODE>
+// FL: weight codes from the forward layout (fl0 / fl1): the same bytes land in the same LDS
+// places, each copy instruction reading four 256-byte runs instead of 16 rows' 64-byte runs
+template <int MODE, bool FL>
 __device__ __forceinline__ void fwd_gemm_item(const FwdArgs& a, int expert, int t0, int ntl, int fb, int wave,
                                               int lane, GemmLds& lds)
 {
@@ -682,8 +684,19 @@ __device__ __forceinline__ void fwd_gemm_item(const FwdArgs& a, int expert, int 
 #pragma unroll
     for (int k = 0; k < 4; ++k) {  // instruction k: column group k of this wave's tile
       const int r = wave * 64 + k * 16 + (l >> 2), b = l & 3;
-      dma16_async_s(w_base(k), (uint32_t)w_n(r) * (uint32_t)(a.K / 2) + (uint32_t)(c * 256 + (4 * q + b) * 16),
-                    &lds.q[buf][kGmA + (wave * 64 + k * 16) * 64]);
+      if constexpr (FL) {
+        // row l / 4 of the group's 16 (row group rg of the layout), block 4q + b: piece b of its
+        // super-chunk c, lane 16 q + l / 4
+        const int ct = min(fb * kGmWaves + wave, a.n_ct - 1);
+        const int row0 = MODE == kFwdGateUp ? ct * 32 + (k & 1) * 16 : ct * kFwdColsPerTile + k * 16;
+        const uint32_t rg = (uint32_t)(min(row0, a.R - 1) / 16);
+        const uint8_t* base = (MODE == kFwdGateUp && k >= 2 ? a.fl1 : a.fl0) + (long long)expert * a.fl_estride;
+        dma16_async_s(base, (rg * (uint32_t)nsc + (uint32_t)c) * 4096u + (uint32_t)(b * 1024 + (16 * q + (l >> 2)) * 16),
+                      &lds.q[buf][kGmA + (wave * 64 + k * 16) * 64]);
+      } else {
+        dma16_async_s(w_base(k), (uint32_t)w_n(r) * (uint32_t)(a.K / 2) + (uint32_t)(c * 256 + (4 * q + b) * 16),
+                      &lds.q[buf][kGmA + (wave * 64 + k * 16) * 64]);
+      }
     }
     {
       const int tt = wave >> 1;
@@ -798,7 +811,7 @@ __device__ __forceinline__ void fwd_gemm_item(const FwdArgs& a, int expert, int 
 // Resident grid over the items (group, block of eight column tiles), feature blocks outermost,
 // dealt over the XCDs in contiguous runs: the work-groups on one XCD at a time take neighbouring
 // groups (mostly of one expert) at the same columns, so they share the weights through its L2.
-template <int MODE>
+template <int MODE, bool FL>
 __global__ __launch_bounds__(64 * kGmWaves, 1) void fwd_gemm_kernel(FwdArgs a)
 {
   __shared__ GemmLds lds;
@@ -817,7 +830,7 @@ __global__ __launch_bounds__(64 * kGmWaves, 1) void fwd_gemm_kernel(FwdArgs a)
     if (it > 0) __syncthreads();  // every wave is done with the previous item's LDS
     int l = lane;
     asm volatile("" : "+v"(l));
-    fwd_gemm_item<MODE>(a, gg[0], gg[1], gg[2], fb, wave, l, lds);
+    fwd_gemm_item<MODE, FL>(a, gg[0], gg[1], gg[2], fb, wave, l, lds);
   }
 }
 
@@ -850,7 +863,7 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
     b.small_tiles = nullptr;
     b.groups = nullptr;
   }
-  // the one-tile work-groups read the forward layout when every matrix of the product has one
+  // both work-group shapes read the forward layout when every matrix of the product has one
   // (and its byte count fits a buffer resource, as for the checkpoint layout)
   const bool fl = fast && mode != kFwdPlain && a.fl0 && (mode != kFwdGateUp || a.fl1) &&
                   forward_layout_bytes(a.R, a.K) < (1LL << 32);
@@ -871,9 +884,15 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !split) return e;
   dim3 mgrid((unsigned)(resident_groups() / 16 * 8)), mblock(64 * kGmWaves);  // one per CU, a multiple of 8
-  if (mode == kFwdGateUp) hipLaunchKernelGGL(fwd_gemm_kernel<kFwdGateUp>, mgrid, mblock, 0, s, b);
-  else if (mode == kFwdDown) hipLaunchKernelGGL(fwd_gemm_kernel<kFwdDown>, mgrid, mblock, 0, s, b);
-  else hipLaunchKernelGGL(fwd_gemm_kernel<kFwdPlain>, mgrid, mblock, 0, s, b);
+  if (mode == kFwdGateUp) {
+    if (fl) hipLaunchKernelGGL((fwd_gemm_kernel<kFwdGateUp, true>), mgrid, mblock, 0, s, b);
+    else hipLaunchKernelGGL((fwd_gemm_kernel<kFwdGateUp, false>), mgrid, mblock, 0, s, b);
+  } else if (mode == kFwdDown) {
+    if (fl) hipLaunchKernelGGL((fwd_gemm_kernel<kFwdDown, true>), mgrid, mblock, 0, s, b);
+    else hipLaunchKernelGGL((fwd_gemm_kernel<kFwdDown, false>), mgrid, mblock, 0, s, b);
+  } else {
+    hipLaunchKernelGGL((fwd_gemm_kernel<kFwdPlain, false>), mgrid, mblock, 0, s, b);
+  }
   return hipGetLastError();
 }
 

@@ -55,7 +55,8 @@ struct FwdArgs {
   const int4* groups;
   const int* n_groups;
   // Forward layout (launch_forward_layout) of W (W1 for kFwdGateUp) and W3, or null: the
-  // one-tile work-groups then load whole 1 KiB operand blocks; everything else reads wp* / ws*.
+  // fast path's work-groups then read their weight codes from it in whole lines (the scales,
+  // and the general path, always come from wp* / ws*).
   const uint8_t* fl0;
   const uint8_t* fl1;
   long long fl_estride;  // bytes between experts in fl*

@@ -108,9 +108,9 @@ def test_routed_layer_small_buckets(k, act):
 
 
 def test_routed_layer_large_buckets_and_lora(k):
-    """Buckets of 150, 70, 30 and 6 rows: the large ones take the GEMM-shaped work-groups (which
-    read the checkpoint layout), the small ones the one-tile work-groups (the forward layout);
-    LoRA deltas join both epilogues."""
+    """Buckets of 150, 70, 30 and 6 rows: the large ones take the GEMM-shaped work-groups, the
+    small ones the one-tile work-groups, both reading the forward layout (each its own way); LoRA
+    deltas join both epilogues."""
     case("routed layer with/without forward layout, large buckets + LoRA r=8")
     rng = np.random.default_rng(62)
     L = layer_of(oracle.random_experts(rng, 4, 1024, 512, 118, 122))
