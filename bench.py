@@ -20,7 +20,8 @@ repo's C restatement of the reference CPU path timed on a bounded sample of the 
 
     python bench.py [--steps 20] [--warmup 3] [--routing uniform|zipf] [--no-cpu] [--no-extra]
 
-The default run also times the Zipf-skewed routing of the same layer (key "zipf"), config 3's
+The default run also times the same step reading only the checkpoint layout (key
+"checkpoint_layout_only"), the Zipf-skewed routing of the same layer (key "zipf"), config 3's
 forward alone under both routings (key "config3_forward"), config 2 at M = 1 and M = 256 tokens
 per expert (key "config2") and a 12-layer sample of config 5's out-of-core sweep (key
 "config5_sample"), each in its own timed region after the headline's.
@@ -389,6 +390,12 @@ def main():
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
 
     extra = {}
+    if not args.no_extra and layout.get("forward_layout"):
+        # the same step reading only the checkpoint layout, for comparison (then the copy is rebuilt)
+        layer.drop_forward_layout()
+        ms_ck, _ = time_layer(args, k, layer, H, I, W, G, ws, lora, n_active)
+        extra["checkpoint_layout_only"] = {"ms_per_step": ms_ck, "tokens_per_s": N / (ms_ck * 1e-3)}
+        layer.prepare_forward_layout()
     if not args.no_extra and args.routing == "uniform" and not args.lora_rank:
         # the skewed variant of configs 3/4 ([3]) on the same layer
         Hz, Iz, Wz, Gz = make_inputs(1, "zipf")
