@@ -129,6 +129,16 @@ def test_only_gate_up_laid_out(k):
     both_ways(k, L, *inputs(rng, 64, 1024, 6, 2))
 
 
+def test_only_down_laid_out(k):
+    """D = 544 is not a multiple of 512: W1|W3 have no forward layout, W2 (K = F = 1024) has one."""
+    case("routed layer, forward layout for W2 only (D = 544)")
+    rng = np.random.default_rng(67)
+    L = layer_of(oracle.random_experts(rng, 6, 544, 1024, 119, 123))
+    L.prepare_forward_layout()
+    assert L._fl[0] is None and L._fl[1] is None and L._fl[2] is not None
+    both_ways(k, L, *inputs(rng, 64, 544, 6, 2))
+
+
 def test_upload_drops_a_stale_layout(k):
     from lazylora_amd.loader import upload
     from lazylora_amd.streaming import host_layer_from
