@@ -250,7 +250,8 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, at<int>(ws, L.meta), at<uint8_t>(ws, L.xt_x), s),
          "quantise h");
   MX_TRY(mx::launch_quant_tiles(h, h_dtype == MXFP4_BF16, D, N, D, at<int4>(ws, L.tiles), at<int>(ws, L.meta),
-                                L.max_tiles, at<int>(ws, L.pair_token), 1, at<uint8_t>(ws, L.at_x), s),
+                                L.max_tiles, at<int>(ws, L.pair_token), 1, at<uint8_t>(ws, L.xt_x),
+                                at<int>(ws, L.meta), at<uint8_t>(ws, L.at_x), s),
          "quantise h tiles");
   MX_PHASE("quant_h", s);
   if (F % mx::kChunk) {  // padding blocks of the act buffer are read by the down product
@@ -326,7 +327,8 @@ int gemm_into(float* y, const float* x, const uint8_t* packed, const uint8_t* sc
               uint8_t* tiles_dev, hipStream_t stream)
 {
   const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
-  MX_TRY(mx::launch_quant_tiles(x, 0, K, M, K, nullptr, nullptr, tiles, nullptr, 0, tiles_dev, stream),
+  MX_TRY(mx::launch_quant_tiles(x, 0, K, M, K, nullptr, nullptr, tiles, nullptr, 0, nullptr, nullptr, tiles_dev,
+                                stream),
          "gemm: quantise x");
   mx::FwdArgs a = {};
   a.wp0 = packed; a.ws0 = scales;

@@ -129,9 +129,12 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
 // with tiles == null the tiles are dense: tile t holds rows 16t.. of `rows`. Unused slots get
 // zeros. max_tiles bounds the grid; the live tile count is read from n_tiles on the device.
 // large_only: only the tiles of large buckets (tiles[t].w != 0); the others are left untouched.
+// xt (with meta and row_map): the XT rows of x written by launch_quant_rows on the same stream;
+// when that call wrote them (meta says some bucket is small) the tiles are copied from them
+// instead of quantising x again (the same bytes).
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
-                              const int* n_tiles, int max_tiles, const int* row_map, int large_only, uint8_t* out,
-                              hipStream_t s);
+                              const int* n_tiles, int max_tiles, const int* row_map, int large_only, const uint8_t* xt,
+                              const int* meta, uint8_t* out, hipStream_t s);
 // Rows 0 .. rows - 1 of x into the XT layout (xt_row_bytes(K) per row), followed by zero rows
 // up to xt_rows(rows): row `rows` is the all-zero row a tile's unused slots gather.
 inline long long xt_rows(int rows) { return ((long long)rows + 16) / 16 * 16; }

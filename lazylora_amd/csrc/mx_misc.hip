@@ -15,7 +15,8 @@ namespace {
 template <bool BF16>
 __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long long ldx, int rows, int K,
                                                           const int4* tiles, const int* n_tiles, const int* row_map,
-                                                          int large_only, uint8_t* out)
+                                                          int large_only, const uint8_t* xt, const int* meta,
+                                                          uint8_t* out)
 {
   __shared__ __attribute__((aligned(16))) uint8_t chunk[kAtChunkBytes];
   const int nsc = at_nchunks(K);
@@ -33,9 +34,30 @@ __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long lo
     row0 = t * kFwdRowsPerTile;
     nrows = min(kFwdRowsPerTile, rows - row0);
   }
+  const long long cbase = (long long)c * kAtChunkBytes;  // at_*_off are tile-relative
+  if (xt && !(meta[2] == 0 && meta[3] > 0)) {
+    // The token-major rows are written (quant_rows_kernel runs before this kernel and quantises
+    // each token's row with the same blocks, so they hold the same codes): tile unit u, lane
+    // 16g + i is piece (u, g) of the row of slot i's token (the zero row `rows` for unused
+    // slots), and lane 16g + i's scale dword of a plane is that row's dword (plane, g).
+    uint8_t* dst = out + (long long)t * at_tile_bytes(K) + cbase;
+    const long long rb = xt_row_bytes(K);
+    for (int p = threadIdx.x; p < 1024; p += 256) {
+      const int u = p >> 6, l = p & 63, ii = l & 15, g = l >> 4;
+      const long long tok = ii < nrows ? row_map[row0 + ii] : rows;
+      *reinterpret_cast<i32x4*>(dst + u * 1024 + l * 16) =
+          *reinterpret_cast<const i32x4*>(xt + tok * rb + (long long)c * kXtChunkBytes + (u * 4 + g) * 16);
+    }
+    if (threadIdx.x < 128) {
+      const int l = threadIdx.x >> 1, plane = threadIdx.x & 1, ii = l & 15, g = l >> 4;
+      const long long tok = ii < nrows ? row_map[row0 + ii] : rows;
+      *reinterpret_cast<uint32_t*>(dst + kAtCodeBytes + l * 8 + plane * 4) = *reinterpret_cast<const uint32_t*>(
+          xt + tok * rb + (long long)c * kXtChunkBytes + kXtCodeBytes + (plane * 4 + g) * 4);
+    }
+    return;
+  }
   const bool valid = i < nrows;
   const long long src = valid ? (row_map ? row_map[row0 + i] : row0 + i) : 0;
-  const long long cbase = (long long)c * kAtChunkBytes;  // at_*_off are tile-relative
   // all 16 blocks' loads are issued before the first is quantised
   float v0[kChunkBlocks], v1[kChunkBlocks];
 #pragma unroll
@@ -386,16 +408,19 @@ __global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, long long n_word
 }  // namespace
 
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
-                              const int* n_tiles, int max_tiles, const int* row_map, int large_only, uint8_t* out,
-                              hipStream_t s)
+                              const int* n_tiles, int max_tiles, const int* row_map, int large_only, const uint8_t* xt,
+                              const int* meta, uint8_t* out, hipStream_t s)
 {
   const long long groups = (long long)max_tiles * at_nchunks(K);  // (tile, super-chunk) work-groups
   if (groups == 0) return hipSuccess;
+  if (xt && (!meta || !row_map || !tiles)) return hipErrorInvalidValue;
   dim3 grid((unsigned)groups), block(256);
   if (x_bf16)
-    hipLaunchKernelGGL(quant_tiles_kernel<true>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, large_only, out);
+    hipLaunchKernelGGL(quant_tiles_kernel<true>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map,
+                       large_only, xt, meta, out);
   else
-    hipLaunchKernelGGL(quant_tiles_kernel<false>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map, large_only, out);
+    hipLaunchKernelGGL(quant_tiles_kernel<false>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map,
+                       large_only, xt, meta, out);
   return hipGetLastError();
 }
 

@@ -150,6 +150,30 @@ def test_large_bucket_groups(k, topk):
     assert_close(gw.cpu().numpy(), gw64, "groups grad_w")
 
 
+@pytest.mark.parametrize("h_bf16", [False, True])
+def test_large_bucket_tiles_copied_from_token_rows(k, h_bf16):
+    """With some small buckets the token-major rows of x are written, and the large buckets'
+    activation tiles are copied from them; with only large buckets the tiles are quantised from x.
+    Both must hold the same bytes: the tokens of two large experts, routed top-1 together with
+    small buckets and then alone, get bit-identical outputs (each depends only on its own row)."""
+    case(f"large-bucket tiles from token rows vs from x, bf16 h={h_bf16}")
+    rng = np.random.default_rng(71)
+    ex = oracle.random_experts(rng, 4, 1024, 512, 118, 122)
+    L = layer_of(ex)
+    first = np.concatenate([np.full(c, e) for e, c in enumerate([150, 70, 30, 6])]).astype(np.int64)
+    rng.shuffle(first)
+    N = first.size
+    h = torch.from_numpy(rng.standard_normal((N, 1024)).astype(np.float32)).cuda()
+    if h_bf16:
+        h = h.bfloat16()
+    w = torch.from_numpy(rng.uniform(0.5, 1.5, (N, 1)).astype(np.float32)).cuda()
+    idx = torch.from_numpy(first[:, None]).cuda()
+    out_mixed = k.routed_forward(h, idx, w, L)
+    large = torch.from_numpy(np.nonzero(first < 2)[0]).cuda()
+    out_large = k.routed_forward(h[large].contiguous(), idx[large].contiguous(), w[large].contiguous(), L)
+    assert torch.equal(out_mixed[large], out_large)
+
+
 @pytest.mark.parametrize("D,F", [(640, 384), (1024, 352)])
 def test_large_bucket_ragged_columns(k, D, F):
     """Large buckets with output widths that leave the grouped transposed products partial
