@@ -13,6 +13,7 @@ as six stacked, expert-major tensors and every routed-layer call reads experts b
 Roles follow the reference: w1 = gate, w3 = up, w2 = down (expert_streamer.py:229-246).
 """
 import ctypes
+import warnings
 from typing import Iterable, Optional, Sequence
 
 import torch
@@ -109,15 +110,28 @@ class ExpertLayer:
         w13 = (k.forward_layout(self.w1p), k.forward_layout(self.w3p)) if self.D % 512 == 0 else (None, None)
         w2 = k.forward_layout(self.w2p) if self.F % 512 == 0 else None
         self._fl = (w13[0], w13[1], w2)
+        self._fl_versions = self._code_versions()
         return sum(t.numel() for t in self._fl if t is not None)
 
     def drop_forward_layout(self) -> None:
         """Forgets the forward-layout copies (the routed calls then read the checkpoint layout)."""
         self._fl = None
 
+    def _code_versions(self):
+        # torch counts in-place writes per tensor (a write through a view counts for its base)
+        return (self.w1p._version, self.w3p._version, self.w2p._version, self.w1p.data_ptr(),
+                self.w3p.data_ptr(), self.w2p.data_ptr())
+
     def forward_layout_pointers(self):
-        """Host array of the three forward-layout device pointers for mxfp4_moe_*_fl, or None."""
+        """Host array of the three forward-layout device pointers for mxfp4_moe_*_fl, or None.
+        Copies made before an in-place write to the codes (or a rebinding of the tensors) are
+        stale: they are dropped, with a warning, and the call reads the checkpoint layout."""
         if self._fl is None:
+            return None
+        if self._code_versions() != self._fl_versions:
+            warnings.warn("expert codes changed after prepare_forward_layout(): the forward-layout copy is dropped "
+                          "(call prepare_forward_layout() again to rebuild it)", RuntimeWarning, stacklevel=3)
+            self._fl = None
             return None
         return (ctypes.c_void_p * 3)(*[t.data_ptr() if t is not None else None for t in self._fl])
 

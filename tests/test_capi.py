@@ -233,3 +233,25 @@ def test_from_bundles_places_streamed_experts_by_id():
     unpacked = SimpleNamespace(packed=False, gate_packed=None)
     with pytest.raises(ValueError):
         ExpertLayer.from_bundles([unpacked], device="cpu")
+
+
+def test_forward_layout_dropped_after_inplace_write():
+    """A forward-layout copy made before an in-place write to the codes is stale: the layer drops
+    it (with a warning) instead of handing its pointers to the routed calls."""
+    import warnings
+    from lazylora_amd.experts import ExpertLayer
+    E, D, F = 2, 512, 512
+    z = lambda *shape: torch.zeros(shape, dtype=torch.uint8)
+    L = ExpertLayer(z(E, F, D // 2), z(E, F, D // 32), z(E, F, D // 2), z(E, F, D // 32), z(E, D, F // 2),
+                    z(E, D, F // 32), device=torch.device("cpu"))
+    assert L.forward_layout_pointers() is None
+    L._fl = (z(16), z(16), None)  # stand-ins for the copies prepare_forward_layout makes on a GPU
+    L._fl_versions = L._code_versions()
+    assert L.forward_layout_pointers() is not None
+    L.w2p[1].fill_(3)  # through a view
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        assert L.forward_layout_pointers() is None
+    assert any(issubclass(w.category, RuntimeWarning) for w in caught)
+    assert L._fl is None
+

@@ -152,6 +152,13 @@ def test_upload_drops_a_stale_layout(k):
     torch.cuda.synchronize()
     assert L.forward_layout_pointers() is None
     assert torch.equal(k.routed_forward(H, I, W, L), k.routed_forward(H, I, W, other))
+    # an in-place write by any other route: the stale copy is dropped before the call reads it
+    L.prepare_forward_layout()
+    L.w1p.copy_(layer_of(oracle.random_experts(rng, 4, 512, 512, 119, 123)).w1p)
+    with pytest.warns(RuntimeWarning):
+        out = k.routed_forward(H, I, W, L)
+    L.drop_forward_layout()
+    assert torch.equal(out, k.routed_forward(H, I, W, L))
 
 
 @pytest.mark.parametrize("zipf", [False, True])
