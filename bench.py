@@ -24,7 +24,8 @@ The default run also times the same step reading only the checkpoint layout (key
 "checkpoint_layout_only"), the Zipf-skewed routing of the same layer (key "zipf"), config 3's
 forward alone under both routings (key "config3_forward"), config 2 at M = 1 and M = 256 tokens
 per expert (key "config2") and a 12-layer sample of config 5's out-of-core sweep (key
-"config5_sample"), each in its own timed region after the headline's.
+"config5_sample", with the same sweep under Zipf routing copying only the selected experts),
+each in its own timed region after the headline's.
 """
 import argparse
 import json
@@ -249,26 +250,38 @@ def expert_main(args, k):
     print(json.dumps(line), flush=True)
 
 
-def stream_sweep(args, k, layers, ring, routing):
-    """Config 5: an out-of-core sweep of `layers` routed-expert layers of the config-3 shape, each
-    copied from pinned host memory (a ring of `ring` distinct layers, as 93 x 20.96 GB cannot be
-    pinned) into one of two HBM slots on a copy stream while the compute stream runs the layer
-    forward for 1024 tokens on the previous slot. Returns the sweep's timings."""
-    from lazylora_amd.streaming import LayerStreamer, host_layer_from
-    t_setup = time.time()
+def stream_hosts(ring):
+    """`ring` distinct config-3 layers in pinned host memory (93 x 20.96 GB cannot be pinned)."""
+    from lazylora_amd.streaming import host_layer_from
     hosts = []
     for r in range(ring):
         layer = make_layer(r)
         hosts.append(host_layer_from(layer, pin=True))
         del layer
         torch.cuda.empty_cache()
+    return hosts
+
+
+def stream_sweep(args, k, layers, ring, routing, hosts=None, active_only=False):
+    """Config 5: an out-of-core sweep of `layers` routed-expert layers of the config-3 shape, each
+    copied from pinned host memory (a ring of `ring` distinct layers) into one of two HBM slots on
+    a copy stream while the compute stream runs the layer forward for 1024 tokens on the previous
+    slot. active_only: copy only the experts the routing selects (as the reference's streamer
+    loads only the active experts); with uniform routing that is every expert. Returns the
+    sweep's timings."""
+    from lazylora_amd.streaming import LayerStreamer
+    t_setup = time.time()
+    if hosts is None:
+        hosts = stream_hosts(ring)
     H, I, W, _ = make_inputs(1, routing)
+    active = torch.unique(I).tolist() if active_only else None
+    ids = (lambda n: [active] * n) if active_only else (lambda n: None)
     ws = torch.empty(k.moe_workspace_bytes(N, TOPK, E, D, F), dtype=torch.uint8, device="cuda")
     streamer = LayerStreamer(E, D, F, slots=2, timing=True)
     log(f"[bench] stream: {ring} pinned host layers of {hosts[0].nbytes / 1e9:.2f} GB, setup "
         f"{time.time() - t_setup:.1f}s")
     # one warm sweep of a few layers (first-touch of the slots and the workspace)
-    for _, layer in streamer.stream(hosts[i % ring] for i in range(min(3, layers))):
+    for _, layer in streamer.stream((hosts[i % ring] for i in range(min(3, layers))), ids(min(3, layers))):
         k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
     torch.cuda.synchronize()
     streamer.copy_events.clear()
@@ -276,7 +289,7 @@ def stream_sweep(args, k, layers, ring, routing):
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for i, layer in streamer.stream(hosts[i % ring] for i in range(layers)):
+    for i, layer in streamer.stream((hosts[i % ring] for i in range(layers)), ids(layers)):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
@@ -291,15 +304,15 @@ def stream_sweep(args, k, layers, ring, routing):
     copy_ms, copy_bytes = streamer.copy_stats()
     t_copy = copy_ms / 1e3
     hidden = max(0.0, min(1.0, (t_copy + t_comp - t_total) / t_comp)) if t_comp > 0 else 0.0
-    del hosts, streamer, ws
+    del streamer, ws
     torch.cuda.empty_cache()
     return {"total_s": t_total, "compute_s": t_comp, "copy_s": t_copy, "copy_bytes": copy_bytes,
-            "hidden_compute_fraction": hidden}
+            "hidden_compute_fraction": hidden, "experts_copied": len(active) if active_only else E}
 
 
 def stream_main(args, k):
     """Config 5 as the bench line (`--workload stream`): the full sweep of args.layers layers."""
-    r = stream_sweep(args, k, args.layers, args.ring, args.routing)
+    r = stream_sweep(args, k, args.layers, args.ring, args.routing, active_only=args.active_only)
     t_total, t_comp, t_copy, copy_bytes, hidden = (r["total_s"], r["compute_s"], r["copy_s"], r["copy_bytes"],
                                                    r["hidden_compute_fraction"])
     h2d = copy_bytes / t_copy / 1e9
@@ -319,7 +332,7 @@ def stream_main(args, k):
         "config": {"workload": f"config 5: {args.layers} routed-expert layers (config-3 shape, 20.96 GB each) "
                                f"streamed from a ring of {args.ring} pinned host layers into 2 HBM slots, layer "
                                f"forward for {N} tokens x {D}, top-{TOPK}",
-                   "routing": args.routing, "act": args.act},
+                   "routing": args.routing, "act": args.act, "experts_copied_per_layer": r["experts_copied"]},
         "h2d_GBps": h2d,
         "h2d_bytes_per_layer": copy_bytes / args.layers,
         "copy_s": t_copy,
@@ -346,6 +359,8 @@ def main():
                          "expert: config 2, the single-expert block swept over token counts")
     ap.add_argument("--layers", type=int, default=93, help="stream: layers per sweep (Kimi K3 has 93 MoE layers)")
     ap.add_argument("--ring", type=int, default=2, help="stream: distinct pinned host layers cycled through")
+    ap.add_argument("--active-only", action="store_true",
+                    help="stream: copy only the experts the routing selects (every expert under uniform routing)")
     ap.add_argument("--lora-rank", type=int, default=0,
                     help="rank of the layer's gate/up/down LoRA adapters (0: off, the BASELINE configs)")
     ap.add_argument("--no-forward-layout", action="store_true",
@@ -423,7 +438,8 @@ def main():
         # config 5 on a sample of its sweep: 12 of the 93 layers streamed
         # from pinned host memory; the full sweep is `--workload stream`
         n5 = 12
-        r5 = stream_sweep(args, k, n5, 2, args.routing)
+        hosts = stream_hosts(2)
+        r5 = stream_sweep(args, k, n5, 2, args.routing, hosts=hosts)
         per_layer = r5["total_s"] / n5
         extra["config5_sample"] = {
             "layers_streamed": n5, "s_per_layer": per_layer,
@@ -432,6 +448,15 @@ def main():
             "hidden_compute_fraction": r5["hidden_compute_fraction"],
             "note": "a 93-layer sweep costs 93 x s_per_layer (the sweep is H2D-bound, so the per-layer time "
                     "does not depend on the layer count)"}
+        # the same sweep under the Zipf-skewed routing, copying only the experts it selects
+        r5z = stream_sweep(args, k, n5, 2, "zipf", hosts=hosts, active_only=True)
+        per_layer_z = r5z["total_s"] / n5
+        extra["config5_sample"]["zipf_active_experts_only"] = {
+            "experts_copied": r5z["experts_copied"], "s_per_layer": per_layer_z,
+            "tokens_per_s_93_layers": N / (93 * per_layer_z),
+            "h2d_GBps": r5z["copy_bytes"] / r5z["copy_s"] / 1e9,
+            "hidden_compute_fraction": r5z["hidden_compute_fraction"]}
+        del hosts
 
     cpu = None
     if not args.no_cpu:
