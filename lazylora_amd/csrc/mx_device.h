@@ -212,6 +212,11 @@ MX_DEV i32x4 buf16(rsrc_t r, uint32_t voff, uint32_t soff)
 }
 // 16 bytes, streaming (non-temporal, as ldg16_nt)
 MX_DEV i32x4 buf16_nt(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2); }
+// Streaming (nt) load with a scalar offset: for bytes each read exactly once, by whole lines.
+MX_DEV i32x4 buf16_nt(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2);
+}
 MX_DEV uint8_t buf8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0); }
 
 // f(integral_constant<int, i>) for i = 0 .. N-1
@@ -250,6 +255,16 @@ MX_DEV void dma16_async_s(const void* base, uint32_t voff, void* lds)
   const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)b), bhi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
   const uint64_t bs = ((uint64_t)bhi << 32) | blo;
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "s"(m0) : "memory");
+}
+// dma16_async_s with the streaming (nt) hint, for bytes each copied exactly once, by whole lines.
+MX_DEV void dma16_async_s_nt(const void* base, uint32_t voff, void* lds)
+{
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)b), bhi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint64_t bs = ((uint64_t)bhi << 32) | blo;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(bs), "s"(m0) : "memory");
 }
 // The 4-byte form (global_load_lds_dword): lane l's 4 bytes land at lds + 4 l.
 MX_DEV void dma4_async(const void* src, void* lds)

@@ -466,8 +466,8 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       for (int grp = 0; grp < 4; ++grp)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if constexpr (FL)
-            b[grp][q] = buf16(live ? wr[grp] : wr_none[grp], woff[grp] + 1024 * q, (uint32_t)c * 4096);
+          if constexpr (FL)  // each line read once, whole, by one instruction: streaming hint
+            b[grp][q] = buf16_nt(live ? wr[grp] : wr_none[grp], woff[grp] + 1024 * q, (uint32_t)c * 4096);
           else
             b[grp][q] = buf16(live ? wr[grp] : wr_none[grp], woff[grp] + 16 * q, (uint32_t)c * 256);
         }
@@ -691,8 +691,8 @@ __device__ __forceinline__ void fwd_gemm_item(const FwdArgs& a, int expert, int 
         const int row0 = MODE == kFwdGateUp ? ct * 32 + (k & 1) * 16 : ct * kFwdColsPerTile + k * 16;
         const uint32_t rg = (uint32_t)(min(row0, a.R - 1) / 16);
         const uint8_t* base = (MODE == kFwdGateUp && k >= 2 ? a.fl1 : a.fl0) + (long long)expert * a.fl_estride;
-        dma16_async_s(base, (rg * (uint32_t)nsc + (uint32_t)c) * 4096u + (uint32_t)(b * 1024 + (16 * q + (l >> 2)) * 16),
-                      &lds.q[buf][kGmA + (wave * 64 + k * 16) * 64]);
+        dma16_async_s_nt(base, (rg * (uint32_t)nsc + (uint32_t)c) * 4096u + (uint32_t)(b * 1024 + (16 * q + (l >> 2)) * 16),
+                         &lds.q[buf][kGmA + (wave * 64 + k * 16) * 64]);
       } else {
         dma16_async_s(w_base(k), (uint32_t)w_n(r) * (uint32_t)(a.K / 2) + (uint32_t)(c * 256 + (4 * q + b) * 16),
                       &lds.q[buf][kGmA + (wave * 64 + k * 16) * 64]);
