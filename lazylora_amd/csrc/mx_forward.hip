@@ -10,6 +10,9 @@
 // 4 column groups of 16 weight rows:
 //   B: 64 contiguous bytes of weight row n = 4 MX blocks 16c+4g+q (q = 0..3), one dword of
 //      scales. MFMA q consumes block 16c+4g+q from lane group g, so op_sel q picks its scale.
+//      With a forward layout (launch_forward_layout) the same 16-byte pieces come from a copy
+//      that holds each MFMA's operand as one contiguous KiB: whole lines per load instruction,
+//      each read once, with the streaming hint.
 //   A: the two-term activations of the tile in the AT layout: for each (q, plane, piece) one
 //      contiguous KiB, and one 8-byte scale pair per lane.
 // Weights are consumed as stored: the MFMA applies the E8M0 scales and the e2m1 codes itself.
