@@ -301,20 +301,39 @@ __global__ __launch_bounds__(256) void route_place_kernel(const void* idx, int i
 
 // ---------------------------------------------------------------- combines
 // out[t, :] = sum over the token's slots, in slot order, of the pair rows (already weighted).
+// sum over a token's slots, in slot order, of 4 columns of its pairs' rows (p < 0: no row).
+// Up to 8 slots the row loads are all issued before the adds; each row is read once (streaming).
+MX_DEV float4 slot_sum4(const float* rows, long long ld, const int* slots, int k, int d)
+{
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (k <= 8) {
+    int p[8];
+    f32x4 v[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) p[s] = s < k ? slots[s] : -1;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      v[s] = p[s] >= 0 ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rows + (long long)p[s] * ld + d))
+                       : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (p[s] >= 0) acc += v[s];  // a skipped slot adds nothing (not even +0, which would turn -0 into +0)
+  } else {
+    for (int s = 0; s < k; ++s) {
+      const int q = slots[s];
+      if (q >= 0) acc += *reinterpret_cast<const f32x4*>(rows + (long long)q * ld + d);
+    }
+  }
+  return make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(float* out, const float* ypair, long long ldy,
                                                       const int* pair_of, int N, int k, int D)
 {
   const int t = blockIdx.y;
   const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (t >= N || d >= D) return;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s = 0; s < k; ++s) {
-    const int p = pair_of[t * k + s];
-    if (p < 0) continue;
-    const float4 v = *reinterpret_cast<const float4*>(ypair + (long long)p * ldy + d);
-    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-  }
-  *reinterpret_cast<float4*>(out + (long long)t * D + d) = acc;
+  *reinterpret_cast<float4*>(out + (long long)t * D + d) = slot_sum4(ypair, ldy, pair_of + (long long)t * k, k, d);
 }
 
 __global__ __launch_bounds__(256) void combine_bwd_kernel(float* grad_h, float* grad_w, const float* dxpair,
@@ -334,14 +353,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(float* grad_h, float* 
     }
   }
   if (d >= D) return;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s = 0; s < k; ++s) {
-    const int p = pair_of[t * k + s];
-    if (p < 0) continue;
-    const float4 v = *reinterpret_cast<const float4*>(dxpair + (long long)p * ldy + d);
-    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-  }
-  *reinterpret_cast<float4*>(grad_h + (long long)t * D + d) = acc;
+  *reinterpret_cast<float4*>(grad_h + (long long)t * D + d) = slot_sum4(dxpair, ldy, pair_of + (long long)t * k, k, d);
 }
 
 // The same quantisation into the XT layout: one work-group per (16 rows, super-chunk), rows
