@@ -43,6 +43,34 @@ MX_DEV f32x4 src4(const LoraMat& a, long long row, int c)
                bf16_hi(h.y) + bf16_hi(l.y)};
 }
 
+// Streaming (nt) loads of the same elements, for the outer-product reductions, whose load
+// instructions each read their lines whole and exactly once.
+template <typename V>
+MX_DEV V ldnt(const V* p) { return __builtin_nontemporal_load(p); }
+
+template <int KIND>
+MX_DEV f32x4 src4_nt(const LoraMat& a, long long row, int c)
+{
+  if (KIND == kLoraF32) return ldnt(reinterpret_cast<const f32x4*>(static_cast<const float*>(a.p0) + row * a.ld + c));
+  if (KIND == kLoraBF16) {
+    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+    const u32x2v v = ldnt(reinterpret_cast<const u32x2v*>(static_cast<const uint16_t*>(a.p0) + row * a.ld + c));
+    return f32x4{bf16_lo(v[0]), bf16_hi(v[0]), bf16_lo(v[1]), bf16_hi(v[1])};
+  }
+  if (KIND == kLoraGLU) {
+    const float* r = static_cast<const float*>(a.p0) + row * a.ld;
+    const f32x4 g = ldnt(reinterpret_cast<const f32x4*>(r + c)), u = ldnt(reinterpret_cast<const f32x4*>(r + a.F + c));
+    return f32x4{glu_fwd(g[0], u[0], a.act_kind), glu_fwd(g[1], u[1], a.act_kind), glu_fwd(g[2], u[2], a.act_kind),
+                 glu_fwd(g[3], u[3], a.act_kind)};
+  }
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  const long long o = row * a.ld + c;
+  const u32x2v h = ldnt(reinterpret_cast<const u32x2v*>(static_cast<const uint16_t*>(a.p0) + o));
+  const u32x2v l = ldnt(reinterpret_cast<const u32x2v*>(static_cast<const uint16_t*>(a.p1) + o));
+  return f32x4{bf16_lo(h[0]) + bf16_lo(l[0]), bf16_hi(h[0]) + bf16_hi(l[0]), bf16_lo(h[1]) + bf16_lo(l[1]),
+               bf16_hi(h[1]) + bf16_hi(l[1])};
+}
+
 MX_DEV float factor_at(const LoraFactor& f, int j, int k)
 {
   return f.kmajor ? f.m[(long long)k * f.ld + j] : f.m[(long long)j * f.ld + k];
@@ -354,7 +382,7 @@ __global__ __launch_bounds__(256) void lora_outer_kernel(OuterArgs a)
     f32x4 x[kOuterBlocks];
 #pragma unroll
     for (int u = 0; u < kOuterBlocks; ++u)
-      x[u] = (row[u] >= 0 && cok) ? src4<KIND>(a.src, row[u], a.c_off + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      x[u] = (row[u] >= 0 && cok) ? src4_nt<KIND>(a.src, row[u], a.c_off + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     float cf[kOuterBlocks][JT];
 #pragma unroll
     for (int u = 0; u < kOuterBlocks; ++u) {
