@@ -118,6 +118,16 @@ def test_routed_layer_large_buckets_and_lora(k):
     both_ways(k, L, *inputs(rng, 0, 1024, 4, 1, sizes=[150, 70, 30, 6]), lora=lora)
 
 
+def test_reference_expert_shape_with_lora(k):
+    """Experts of the BASELINE shape (W1/W3 2048 x 7168, W2 7168 x 2048: 14 and 4 super-chunks
+    per row) with rank-16 adapters, with and without the forward layout."""
+    case("8 experts 2048x7168, 40 tokens top-2, LoRA r=16, with/without forward layout")
+    rng = np.random.default_rng(68)
+    L = layer_of(oracle.random_experts(rng, 8, 7168, 2048, 117, 121))
+    lora = adapters(oracle.random_lora(rng, 7168, 2048, 16))
+    both_ways(k, L, *inputs(rng, 40, 7168, 8, 2), act="situ", lora=lora)
+
+
 def test_only_gate_up_laid_out(k):
     """F = 544 is not a multiple of 512: W2 has no forward layout and the down product reads the
     checkpoint layout, W1|W3 (K = D = 1024) read theirs."""
