@@ -245,14 +245,20 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
          "route");
   MX_PHASE("route", s);
   // h once per token in the XT layout (with a zero row N for the unused slots of a tile), which
-  // the one-tile work-groups gather; the tiles of large buckets also in the AT layout, which the
-  // grouped work-groups re-read for every column tile
-  MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, at<int>(ws, L.meta), at<uint8_t>(ws, L.xt_x), s),
+  // the one-tile work-groups gather; when the gate/up product splits its buckets, the tiles of
+  // large buckets also in the AT layout, which the grouped work-groups re-read for every column
+  // tile, and the XT rows are skipped when no bucket is small (the routing's meta says so on
+  // the device). Without the split every tile reads the XT rows, so they are always written.
+  const bool gu_split = mx::fwd_bucket_split(F, D);
+  MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, gu_split ? at<int>(ws, L.meta) : nullptr,
+                               at<uint8_t>(ws, L.xt_x), s),
          "quantise h");
-  MX_TRY(mx::launch_quant_tiles(h, h_dtype == MXFP4_BF16, D, N, D, at<int4>(ws, L.tiles), at<int>(ws, L.meta),
-                                L.max_tiles, at<int>(ws, L.pair_token), 1, at<uint8_t>(ws, L.xt_x),
-                                at<int>(ws, L.meta), at<uint8_t>(ws, L.at_x), s),
-         "quantise h tiles");
+  if (gu_split) {
+    MX_TRY(mx::launch_quant_tiles(h, h_dtype == MXFP4_BF16, D, N, D, at<int4>(ws, L.tiles), at<int>(ws, L.meta),
+                                  L.max_tiles, at<int>(ws, L.pair_token), 1, at<uint8_t>(ws, L.xt_x),
+                                  at<int>(ws, L.meta), at<uint8_t>(ws, L.at_x), s),
+           "quantise h tiles");
+  }
   MX_PHASE("quant_h", s);
   if (F % mx::kChunk) {  // padding blocks of the act buffer are read by the down product
     MX_TRY(mx::launch_zero(at<void>(ws, L.at_act), at_bytes(L.max_tiles, F), s), "zero act");

@@ -848,7 +848,13 @@ int resident_groups()
   return max(8, (2 * cus) / 8 * 8);
 }
 
+// The fast path addresses a weight matrix through one buffer resource (32-bit byte counts and
+// offsets); larger matrices, and K not a multiple of 512, take the general path.
+bool fast_path(int R, int K) { return K > 0 && (K % kChunk) == 0 && (long long)R * (K / 2) < (1LL << 32); }
+
 }  // namespace
+
+bool fwd_bucket_split(int R, int K) { return fast_path(R, K); }
 
 hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
 {
@@ -856,11 +862,9 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   const long long total = (long long)max_tiles * n_cg;
   if (total <= 0) return hipSuccess;
   const long long blocks = std::min<long long>((total + 7) / 8 * 8, resident_groups());
-  // the fast path addresses a weight matrix through one buffer resource (32-bit byte counts and
-  // offsets); larger matrices take the general path
-  const bool fast = (a.K % kChunk) == 0 && (long long)a.R * (a.K / 2) < (1LL << 32);
+  const bool fast = fast_path(a.R, a.K);
   // the bucket split needs the tile list and the fast path; otherwise every tile takes fwd_kernel
-  const bool split = fast && a.tiles && a.small_tiles && a.groups;
+  const bool split = fwd_bucket_split(a.R, a.K) && a.tiles && a.small_tiles && a.groups;
   FwdArgs b = a;
   if (!split) {
     b.small_tiles = nullptr;

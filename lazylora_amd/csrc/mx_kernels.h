@@ -120,6 +120,11 @@ constexpr int kGroupMinTiles = 4;  // experts with at least this many tiles take
 constexpr int kFwdColsPerTile = 64;  // kFwdPlain / kFwdDown; kFwdGateUp covers 32 features
 constexpr int kBwdColsPerTile = 256;  // output columns of one transposed-product wave
 
+// Whether launch_fwd splits a routed product over W [R, K] into small-bucket and large-bucket
+// work-groups: the large-bucket shape needs the fast path (K a multiple of 512, one buffer
+// resource addressing the whole matrix). Without the split every tile takes the one-tile
+// work-groups, whose gate/up product reads the token-major (XT) rows of x for every tile.
+bool fwd_bucket_split(int R, int K);
 hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
 

@@ -99,9 +99,16 @@ class ExpertLayer:
     def prepare_forward_layout(self) -> int:
         """Builds the forward-layout copies of W1, W3 (when D is a multiple of 512) and W2 (when F
         is), which the routed forward's small-bucket work-groups then read with whole 1 KiB loads
-        (mxfp4_forward_layout; results are bit-identical). Each copy holds as many bytes as the
-        packed codes it copies; returns the bytes added. The copies reflect the weights as they
-        are now: rebuild them after writing new weights (loader.upload drops them)."""
+        (mxfp4_forward_layout; results are bit-identical). Each copy holds the packed codes it
+        copies with the rows padded to a multiple of 16 (ceil(R / 16) * 16 * K / 2 bytes per
+        expert: the same size when R is a multiple of 16); returns the bytes added.
+
+        The copies reflect the weights as they are now. An in-place torch write to the codes
+        (or rebinding the tensors) is detected before the next routed call, which then drops
+        the copy with a warning; loader.upload drops it too. Writes the version counters do not
+        see (through `.data`, ctypes or hipMemcpy, or by another C caller) are not detected:
+        call drop_forward_layout() or prepare_forward_layout() after them, or the forward reads
+        the old codes."""
         from lazylora_amd.native import kernel
 
         k = kernel()

@@ -22,12 +22,15 @@ import torch
 
 from lazylora_amd.experts import ExpertLayer
 from lazylora_amd.native import kernel
+from lazylora_amd.streaming import BundleStager, compact_ids
 
 
 def _native():
     k = kernel()
     if k is None:
-        raise RuntimeError("LAZYLORA_NO_NATIVE=1: the MI355X routed-expert path is disabled")
+        raise RuntimeError("the MI355X routed-expert path is unavailable: LAZYLORA_NO_NATIVE=1 is set, or the "
+                           "native library failed to load, or no HIP device is visible (set "
+                           "LAZYLORA_NATIVE_STRICT=1 to see the underlying error)")
     return k
 
 
@@ -112,9 +115,31 @@ class RoutedExpertsFunction(torch.autograd.Function):
 def layer_from_stream(expert_streamer, layer_idx, active_experts, num_experts=None, device=None) -> ExpertLayer:
     """The active experts of one layer, supplied by the reference's streamer as packed
     ExpertWeightBundles (DynamicExpertStreamer.stream_experts, expert_streamer.py:315-369, in disk
-    order), placed by expert id in an HBM ExpertLayer."""
+    order), placed by expert id in an HBM ExpertLayer of num_experts experts (absent experts
+    hold zero codes). StreamedRoutedExpertsFunction uses the compact form, stream_compact."""
     pairs = list(expert_streamer.stream_experts(layer_idx, active_experts))
     return ExpertLayer.from_bundles(pairs, device=device, num_experts=num_experts)
+
+
+_stagers = {}
+
+
+def _stager(device) -> BundleStager:
+    dev = torch.device(device)
+    if dev not in _stagers:
+        _stagers[dev] = BundleStager(dev)
+    return _stagers[dev]
+
+
+def stream_compact(expert_streamer, layer_idx, active_experts, topk_indices, device):
+    """(layer, ids on the layer): the bundles of `active_experts`, consumed from the streamer's
+    generator as it yields them and staged into a compact HBM layer of only those experts
+    (BundleStager), and topk_indices mapped onto it; routed ids outside the active set map to -1
+    and are skipped by the routed call, as the reference's sweep over the streamed experts never
+    visits them (lazy_trainer.py:806-880)."""
+    active = list(active_experts)
+    layer, ids = _stager(device).stage(expert_streamer.stream_experts(layer_idx, active), len(active))
+    return layer, compact_ids(topk_indices, ids, device)
 
 
 class StreamedRoutedExpertsFunction(torch.autograd.Function):
@@ -124,21 +149,26 @@ class StreamedRoutedExpertsFunction(torch.autograd.Function):
     As in the reference, the experts are streamed once in forward (skipped when `cached` holds
     the routed sum) and once more in backward, and nothing expert-sized stays alive between the
     two: each pass takes the packed bundles of `trainer.expert_streamer.stream_experts(layer_idx,
-    active_experts)` into HBM and runs the whole layer in one call. The activation is SiTU-GLU and
-    `bundle` is the layer's LoRALayerBundle (its gate/up/down adapters), as in
-    _routed_experts_forward/_backward (lazy_trainer.py:806-880); the adapters' gradients are
-    accumulated into them with accumulate_grad. The streamer must hand over packed bundles
-    (keep_packed, which holds whenever kernel() is not None)."""
+    active_experts)` as the generator yields them, stages them through pinned buffers into a
+    compact HBM layer of only those experts on a copy stream (the DMA of one expert overlaps the
+    next bundle's arrival), and runs the whole layer in one call. Tokens' choices outside the
+    active set contribute nothing (no expert term, no adapter term, zero grad_w), as in the
+    reference's sweep. The activation is SiTU-GLU and `bundle` is the layer's LoRALayerBundle
+    (its gate/up/down adapters), as in _routed_experts_forward/_backward
+    (lazy_trainer.py:806-880); the adapters' gradients are accumulated into them with
+    accumulate_grad. The streamer must hand over packed bundles (keep_packed, which holds
+    whenever kernel() is not None)."""
 
     @staticmethod
     def forward(ctx, h_latent, topk_weights, topk_indices, trainer, layer_idx, bundle, active_experts, cached=None):
         if cached is not None:
             out = cached.to(torch.float32)
+        elif len(active_experts) == 0:  # nothing streamed: the reference's sweep adds nothing
+            out = torch.zeros(h_latent.shape, dtype=torch.float32, device=h_latent.device)
         else:
-            layer = layer_from_stream(trainer.expert_streamer, layer_idx, active_experts,
-                                      num_experts=_num_experts(trainer, topk_indices, active_experts),
-                                      device=h_latent.device if h_latent.is_cuda else None)
-            out = routed_experts_forward(h_latent, topk_indices, topk_weights, layer, act="situ", lora=_lora(bundle))
+            dev = _device(h_latent)
+            layer, idx = stream_compact(trainer.expert_streamer, layer_idx, active_experts, topk_indices, dev)
+            out = routed_experts_forward(h_latent, idx, topk_weights, layer, act="situ", lora=_lora(bundle))
             del layer
             out = out.to(h_latent.device)
         ctx.save_for_backward(h_latent, topk_weights, topk_indices)
@@ -148,12 +178,17 @@ class StreamedRoutedExpertsFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         h_latent, topk_weights, topk_indices = ctx.saved_tensors
-        layer = layer_from_stream(ctx.trainer.expert_streamer, ctx.layer_idx, ctx.active_experts,
-                                  num_experts=_num_experts(ctx.trainer, topk_indices, ctx.active_experts),
-                                  device=h_latent.device if h_latent.is_cuda else None)
-        grad_h, grad_w = routed_experts_backward(h_latent, topk_indices, topk_weights, layer, grad_out,
+        if len(ctx.active_experts) == 0:
+            return (torch.zeros_like(h_latent), torch.zeros_like(topk_weights), None, None, None, None, None, None)
+        dev = _device(h_latent)
+        layer, idx = stream_compact(ctx.trainer.expert_streamer, ctx.layer_idx, ctx.active_experts, topk_indices, dev)
+        grad_h, grad_w = routed_experts_backward(h_latent, idx, topk_weights, layer, grad_out,
                                                  act="situ", lora=_lora(ctx.bundle))
         return (grad_h.to(h_latent.device), grad_w.to(topk_weights.device), None, None, None, None, None, None)
+
+
+def _device(h_latent):
+    return h_latent.device if h_latent.is_cuda else torch.device("cuda", torch.cuda.current_device())
 
 
 def _lora(bundle):
@@ -164,14 +199,3 @@ def _lora(bundle):
     if any(getattr(m, "r", 1) == 0 or getattr(m, "lora_A", None) is None for m in mods):
         return None
     return bundle
-
-
-def _num_experts(trainer, topk_indices, active_experts) -> int:
-    """Experts of the layer: the trainer's configured count when it has one, else enough for every
-    routed id (ids are validated against it by the routed call)."""
-    cfg = getattr(getattr(trainer, "config", None), "model", None)
-    n = getattr(cfg, "n_routed_experts", None) or getattr(cfg, "num_experts", None)
-    if n:
-        return int(n)
-    hi = int(topk_indices.max()) if topk_indices.numel() else 0
-    return max([hi] + [int(e) for e in active_experts]) + 1

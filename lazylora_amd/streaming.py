@@ -14,6 +14,7 @@ host never blocks except to throttle when all slots are in flight.
 from collections import deque
 from typing import Iterable, Iterator, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from lazylora_amd.experts import ExpertLayer
@@ -90,6 +91,117 @@ class LayerStreamer:
         torch.cuda.synchronize(self.device)
         ms = sum(a.elapsed_time(b) for a, b, _ in self.copy_events)
         return ms, sum(n for _, _, n in self.copy_events)
+
+
+_BUNDLE_ATTRS = ("gate_packed", "gate_scale", "up_packed", "up_scale", "down_packed", "down_scale")
+
+
+class BundleStager:
+    """Packed ExpertWeightBundles, as the reference's streamer yields them (CPU tensors, one
+    expert at a time, expert_streamer.py:27-50, :315-369), into a compact HBM layer that holds
+    only the experts streamed.
+
+    Each bundle is copied into one of `slots` pinned host buffers and from there to HBM by an
+    asynchronous copy on a dedicated copy stream (default priority), so the DMA of expert i runs
+    while expert i + 1 is taken from the generator and copied into the next buffer; the host
+    waits only before refilling a buffer whose DMA is still running. Bundles already in pinned
+    memory skip the staging copy; bundles already on the device are copied device to device.
+    The pinned buffers are kept between calls (they are sized for one expert)."""
+
+    def __init__(self, device=None, slots: int = 4):
+        if slots < 2:
+            raise ValueError("staging needs at least two pinned buffers")
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.slots = slots
+        self.copy_stream = torch.cuda.Stream(device=self.device)
+        self._buf: List[torch.Tensor] = []
+        self._done = [torch.cuda.Event() for _ in range(slots)]
+        self._used = [False] * slots
+        self._shapes: Optional[Tuple[Tuple[int, ...], ...]] = None
+        self.bytes_copied = 0
+
+    def _buffers(self, shapes) -> None:
+        if self._shapes == shapes:
+            return
+        for s in range(self.slots):  # buffers of another geometry: wait for their last copies
+            if self._used[s]:
+                self._done[s].synchronize()
+        total = sum(int(np.prod(s)) for s in shapes)
+        self._buf = [torch.empty(total, dtype=torch.uint8, pin_memory=True) for _ in range(self.slots)]
+        self._used = [False] * self.slots
+        self._shapes = shapes
+
+    def stage(self, pairs: Iterable, capacity: int) -> Tuple[ExpertLayer, List[int]]:
+        """(layer, ids): expert j of the returned layer is the bundle of expert id ids[j], in the
+        order the (expert_id, bundle) pairs came. `capacity` bounds the number of pairs (the
+        length of the active set). The current stream waits for the copies before it uses the
+        layer; the call returns once the last DMA is queued."""
+        it = iter(pairs)
+        first = next(it, None)
+        if first is None:
+            raise ValueError("the streamer yielded no experts")
+        b0 = first[1]
+        shapes = tuple(tuple(getattr(b0, a).shape) for a in _BUNDLE_ATTRS)
+        (F, Dh), (_, Dg), (_, _), (_, _), (D, Fh), (_, Fg) = shapes
+        if Dh * 2 != D or Fh * 2 != F or Dg * 32 != D or Fg * 32 != F:
+            raise ValueError(f"bundle shapes {shapes} are not a packed MXFP4 expert")
+        self._buffers(shapes)
+        layer = ExpertLayer.empty(max(1, capacity), D, F, self.device)
+        dst = layer.tensors()
+        compute = torch.cuda.current_stream(self.device)
+        cs = self.copy_stream
+        cs.wait_stream(compute)  # the layer's memory may have been in use on the compute stream
+        ids: List[int] = []
+        sizes = [int(np.prod(s)) for s in shapes]
+        offs = np.concatenate([[0], np.cumsum(sizes)]).tolist()
+
+        def put(j, eid, b):
+            if j >= capacity:
+                raise ValueError(f"the streamer yielded more than the {capacity} experts asked for")
+            srcs = []
+            for a, shp in zip(_BUNDLE_ATTRS, shapes):
+                t = getattr(b, a)
+                if t is None or tuple(t.shape) != shp or t.dtype != torch.uint8:
+                    raise ValueError(f"expert {eid}: {a} must be uint8 {shp}, got "
+                                     f"{None if t is None else (t.dtype, tuple(t.shape))}")
+                srcs.append(t)
+            slot = j % self.slots
+            staged = all(t.is_cuda or t.is_pinned() for t in srcs)
+            if not staged:
+                if self._used[slot]:
+                    self._done[slot].synchronize()  # its previous DMA has read the buffer
+                buf = self._buf[slot]
+                for t, o0, o1 in zip(srcs, offs[:-1], offs[1:]):
+                    buf[o0:o1].copy_(t.reshape(-1))
+                srcs = [buf[o0:o1] for o0, o1 in zip(offs[:-1], offs[1:])]
+            with torch.cuda.stream(cs):
+                for d, t in zip(dst, srcs):
+                    d[j].view(-1).copy_(t.reshape(-1), non_blocking=True)
+            if not staged:
+                self._done[slot].record(cs)
+                self._used[slot] = True
+            ids.append(int(eid))
+            self.bytes_copied += offs[-1]
+
+        put(0, first[0], b0)
+        for j, (eid, b) in enumerate(it, start=1):
+            put(j, eid, b)
+        if len(set(ids)) != len(ids) or min(ids) < 0:
+            raise ValueError("expert ids must be distinct and non-negative")
+        compute.wait_stream(cs)
+        return layer, ids
+
+
+def compact_ids(topk_indices: torch.Tensor, ids: Sequence[int], device) -> torch.Tensor:
+    """topk_indices mapped onto a compact layer holding experts `ids` (expert ids[j] at j), on
+    `device`: an id not among them becomes -1, which the routed call skips, as the reference's
+    sweep over the streamed experts never visits it (lazy_trainer.py:806-834)."""
+    n_map = max(ids) + 1
+    emap = torch.full((n_map,), -1, dtype=torch.int64, device=device)
+    emap[torch.tensor(ids, dtype=torch.int64, device=device)] = torch.arange(len(ids), device=device)
+    idx = topk_indices.to(device, non_blocking=True).long()
+    inside = (idx >= 0) & (idx < n_map)
+    return torch.where(inside, emap[idx.clamp(0, n_map - 1)], torch.full_like(idx, -1)).contiguous()
 
 
 def host_layer_from(layer: ExpertLayer, pin: Optional[bool] = None) -> HostLayer:

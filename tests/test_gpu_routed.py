@@ -200,6 +200,37 @@ def test_large_bucket_ragged_columns(k, D, F):
     assert_close(gw.cpu().numpy(), gw64, "ragged grad_w")
 
 
+@pytest.mark.parametrize("D,F", [(640, 512), (1024, 352)])
+def test_only_large_buckets_unsplit_product(k, D, F):
+    """Every bucket large (at least 49 rows) while a product cannot split its buckets (its K is
+    not a multiple of 512: D = 640 for gate/up, F = 352 for down): every tile then takes the
+    one-tile work-groups, so x's token-major rows must still be written. Run twice on one reused
+    workspace, the second time on other tokens, so stale rows of the first call would show."""
+    case(f"only large buckets, unsplit product: E=4, D={D}, F={F}, top-1, reused workspace")
+    rng = np.random.default_rng(D * 7 + F)
+    E = 4
+    ex = oracle.random_experts(rng, E, D, F, 118, 122)
+    L = layer_of(ex)
+    ws = None
+    for call, sizes in enumerate(([150, 70, 64, 49], [64, 49, 130, 52])):
+        idx = np.concatenate([np.full(c, e) for e, c in enumerate(sizes)]).astype(np.int64)
+        rng.shuffle(idx)
+        N = idx.size
+        idx = idx[:, None]
+        w = rng.uniform(0.5, 1.5, (N, 1)).astype(np.float32)
+        h = rng.standard_normal((N, D)).astype(np.float32)
+        g = rng.standard_normal((N, D)).astype(np.float32)
+        if ws is None:
+            ws = torch.empty(k.moe_workspace_bytes(340, 1, E, D, F), dtype=torch.uint8, device="cuda")
+        H, I, W, G = (torch.from_numpy(a).cuda() for a in (h, idx, w, g))
+        assert_close(k.routed_forward(H, I, W, L, workspace=ws).cpu().numpy(), oracle.routed_forward(h, idx, w, ex),
+                     f"large-only fwd call {call}")
+        gh, gw = k.routed_backward(H, I, W, L, G, workspace=ws)
+        gh64, gw64 = oracle.routed_backward(h, idx, w, ex, g)
+        assert_close(gh.cpu().numpy(), gh64, f"large-only grad_h call {call}")
+        assert_close(gw.cpu().numpy(), gw64, f"large-only grad_w call {call}")
+
+
 def test_input_dtypes(k):
     """bf16 h gives the fp32 result of the same (bf16-representable) values; int32 ids = int64."""
     case("bf16 h, int32 topk ids")
@@ -353,6 +384,62 @@ def test_streamed_node_with_reference_signature(k):
     got = [t for m in (bundle.gate_lora, bundle.up_lora, bundle.down_lora) for t in m.grads[0]]
     for n, (a, b) in enumerate(zip(got, want[2])):
         assert_close(a.numpy(), b, f"streamed node LoRA grad {n}")
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+def test_streamed_node_ids_outside_active_set(k, pinned):
+    """Routed ids that the active set leaves out get nothing, as in the reference's sweep over the
+    streamed experts (lazy_trainer.py:806-880): no expert term and no adapter term in the output
+    (equal to the oracle with those slots' weights zeroed), zero grad_w on those slots, and the
+    adapter gradients of the streamed experts only. Bundles in pageable or pinned host memory;
+    more bundles than staging buffers, so the buffers are reused within a pass."""
+    case(f"streamed node, ids outside the active set, pinned bundles={pinned}")
+    from types import SimpleNamespace
+    from lazylora_amd.routed import StreamedRoutedExpertsFunction
+    rng = np.random.default_rng(28)
+    E, D, F, N, topk, r = 16, 512, 256, 64, 2, 4
+    ex = oracle.random_experts(rng, E, D, F, 119, 123)
+    idx, w = routing(rng, N, E, topk)
+    routed = sorted(set(idx.ravel().tolist()))
+    dropped = routed[::3]
+    active = [e for e in routed if e not in dropped]
+    streamer = _Streamer(ex, list(rng.permutation(E)))
+    if pinned:
+        for b in streamer.bundles.values():
+            for a in ("gate_packed", "gate_scale", "up_packed", "up_scale", "down_packed", "down_scale"):
+                setattr(b, a, getattr(b, a).pin_memory())
+    trainer = SimpleNamespace(expert_streamer=streamer)
+
+    def adapter(n_in, n_out):
+        A = torch.from_numpy((0.05 * rng.standard_normal((r, n_in))).astype(np.float32))
+        B = torch.from_numpy((0.05 * rng.standard_normal((n_out, r))).astype(np.float32))
+        mod = SimpleNamespace(lora_A=A, lora_B=B, scaling=2.0, r=r, dropout_rate=0.0, grads=[])
+        mod.accumulate_grad = lambda gA, gB, m=mod: m.grads.append((gA.cpu(), gB.cpu()))
+        return mod
+
+    bundle = SimpleNamespace(gate_lora=adapter(D, F), up_lora=adapter(D, F), down_lora=adapter(F, D))
+    f64 = [t.numpy().astype(np.float64) for m in (bundle.gate_lora, bundle.up_lora, bundle.down_lora)
+           for t in (m.lora_A, m.lora_B)]
+    lo = oracle.LoRA(*f64, gate_s=2.0, up_s=2.0, down_s=2.0)
+    h_np = rng.standard_normal((N, D)).astype(np.float32)
+    g_np = rng.standard_normal((N, D)).astype(np.float32)
+    keep = np.isin(idx, active)
+    assert (~keep).any() and keep.any()
+    w_kept = np.where(keep, w, 0).astype(np.float32)
+    h = torch.from_numpy(h_np).cuda().requires_grad_()
+    W = torch.from_numpy(w).cuda().requires_grad_()
+    out = StreamedRoutedExpertsFunction.apply(h, W, torch.from_numpy(idx).cuda(), trainer, 0, bundle, active, None)
+    assert_close(out.detach().cpu().numpy(), oracle.routed_forward(h_np, idx, w_kept, ex, "situ", lora=lo),
+                 "streamed node fwd, dropped ids")
+    out.backward(torch.from_numpy(g_np).cuda())
+    want = oracle.routed_backward(h_np, idx, w_kept, ex, g_np, "situ", lora=lo)
+    assert_close(h.grad.cpu().numpy(), want[0], "streamed node grad_h, dropped ids")
+    gw = W.grad.cpu().numpy()
+    assert np.all(gw[~keep] == 0)
+    assert_close(gw[keep], want[1][keep], "streamed node grad_w, dropped ids")
+    got = [t for m in (bundle.gate_lora, bundle.up_lora, bundle.down_lora) for t in m.grads[0]]
+    for n, (a, b) in enumerate(zip(got, want[2])):
+        assert_close(a.numpy(), b, f"streamed node LoRA grad {n}, dropped ids")
 
 
 def test_many_slots_per_token(k):
