@@ -23,9 +23,12 @@ repo's C restatement of the reference CPU path timed on a bounded sample of the 
 The default run also times the same step reading only the checkpoint layout (key
 "checkpoint_layout_only"), the Zipf-skewed routing of the same layer (key "zipf"), config 3's
 forward alone under both routings (key "config3_forward"), config 2 at M = 1 and M = 256 tokens
-per expert (key "config2") and a 12-layer sample of config 5's out-of-core sweep (key
-"config5_sample", with the same sweep under Zipf routing copying only the selected experts),
-each in its own timed region after the headline's.
+per expert (key "config2"), a 12-layer sample of config 5's out-of-core sweep (key
+"config5_sample", with the same sweep under Zipf routing copying only the selected experts) and
+the reference-signature streamed node fed by a streamer of pageable ExpertWeightBundle-shaped
+objects (key "streamed_node"), each in its own timed region after the headline's. The CPU
+baseline runs on both routings (key "cpu_baseline_zipf" for the Zipf layer, where the
+reference's rows > 48 branch runs).
 """
 import argparse
 import json
@@ -117,17 +120,38 @@ def make_inputs(seed: int, routing: str):
     return torch.from_numpy(h).cuda(), idx.contiguous(), w.contiguous(), torch.from_numpy(g).cuda()
 
 
-def _cpu_model() -> str:
+def _cpu_info() -> dict:
+    """Host CPU model, sockets, logical CPUs and the vector extensions the C path uses, from
+    /proc/cpuinfo."""
+    info = {"model": "unknown", "sockets": None, "logical_cpus": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0))}
+    sockets, flags = set(), set()
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name" and info["model"] == "unknown":
+                info["model"] = val
+            elif key == "physical id":
+                sockets.add(val)
+            elif key in ("cpu family", "model", "stepping") and f"cpu_{key.replace(' ', '_')}" not in info:
+                info[f"cpu_{key.replace(' ', '_')}"] = val
+            elif key == "flags" and not flags:
+                flags = set(val.split())
     except OSError:
         pass
-    return "unknown"
+    info["sockets"] = len(sockets) or None
+    info["vector_flags"] = sorted(f for f in flags if f in ("avx2", "fma", "avx512f", "avx512bw", "avx512_bf16"))
+    return info
 
 
-def cpu_baseline(layer, H, I, W, G, budget_s: float, act: str):
+def cpu_host_layer(layer):
+    """The layer's packed tensors on the host as the CPU leg's ExpertSet (copied once)."""
+    import oracle
+    return oracle.ExpertSet(*[t.cpu().numpy() for t in layer.tensors()])
+
+
+def cpu_baseline(ex, H, I, W, G, budget_s: float, act: str):
     """The reference trainer's CPU path over the whole layer (every active expert, every token):
     oracle/reference_path.py composes it as lazy_trainer.py:746-880 does, the fused C products
     (oracle/mxfp4_oracle.c, the reference's schedule and flags) for buckets of at most 48 rows and
@@ -139,7 +163,6 @@ def cpu_baseline(layer, H, I, W, G, budget_s: float, act: str):
     lib = oracle.oracle_lib()
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    ex = oracle.ExpertSet(*[t.cpu().numpy() for t in layer.tensors()])
     h, idx, w, g = H.cpu().numpy(), I.cpu().numpy(), W.cpu().numpy(), G.cpu().numpy()
     times = []
     while len(times) < 3:
@@ -152,11 +175,12 @@ def cpu_baseline(layer, H, I, W, G, budget_s: float, act: str):
             break
     t = float(np.median(times))
     counts = np.bincount(idx.ravel(), minlength=E)
-    big = int((counts > reference_path.FUSED_MAX_ROWS).sum())
+    big = counts > reference_path.FUSED_MAX_ROWS
     return {"value": N / t, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"the whole layer ({int((counts > 0).sum())} active experts, {big} of them above 48 rows, "
-                      f"every token), fwd+bwd, median of {len(times)} run(s): {[round(x, 2) for x in times]} s",
-            "cpu_model": _cpu_model(), "threads": {"openmp": lib.threads(), "torch": torch.get_num_threads()},
+            "sample": f"the whole layer ({int((counts > 0).sum())} active experts, {int(big.sum())} of them above 48 "
+                      f"rows, every token), fwd+bwd, median of {len(times)} run(s): {[round(x, 2) for x in times]} s",
+            "experts_above_48_rows": int(big.sum()), "pairs_in_experts_above_48_rows": int(counts[big].sum()),
+            "cpu": _cpu_info(), "threads": {"openmp": lib.threads(), "torch": torch.get_num_threads()},
             "compile_flags": "gcc -O3 -mavx2 -mfma -fopenmp (oracle/Makefile; the reference's build.sh flags)",
             "path": "reference composition: fused C products for buckets <= 48 rows, C dequant + torch CPU "
                     "sgemm above (lazy_trainer.py:746-880)"}
@@ -343,6 +367,62 @@ def stream_main(args, k):
     print(json.dumps(line), flush=True)
 
 
+def streamed_node_sample(args, k, layer, H, I, W, G, reps: int = 3):
+    """The reference-signature node (routed.StreamedRoutedExpertsFunction, lazy_trainer.py:45-77)
+    fed by a streamer that yields ExpertWeightBundle-shaped objects of pageable host tensors, as
+    the reference's DynamicExpertStreamer does (expert_streamer.py:27-50, :315-369), in a seeded
+    'disk' order: the active experts of the given routing, each pass staging them through pinned
+    buffers into a compact HBM layer. Reports the staging rate alone (generator to layer ready)
+    and the node's forward and forward + backward (two streaming passes) per layer."""
+    from types import SimpleNamespace
+    from lazylora_amd.routed import StreamedRoutedExpertsFunction, _stager
+    active = torch.unique(I).tolist()
+    order = {e: i for i, e in enumerate(np.random.default_rng(5).permutation(active).tolist())}
+    names = ("gate_packed", "gate_scale", "up_packed", "up_scale", "down_packed", "down_scale")
+    bundles = {e: SimpleNamespace(expert_idx=e, packed=True,
+                                  **{n: t[e].cpu() for n, t in zip(names, layer.tensors())}) for e in active}
+
+    class Streamer:
+        def stream_experts(self, layer_idx, ids):
+            for e in sorted(ids, key=order.__getitem__):
+                yield e, bundles[e]
+
+    streamer = Streamer()
+    trainer = SimpleNamespace(expert_streamer=streamer)
+    nbytes = len(active) * EXPERT_BYTES
+    stager = _stager(H.device)
+    stager.stage(streamer.stream_experts(0, active), len(active))  # warm: pinned buffers, allocator
+    torch.cuda.synchronize()
+    stage_s = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        stager.stage(streamer.stream_experts(0, active), len(active))
+        torch.cuda.synchronize()
+        stage_s.append(time.perf_counter() - t0)
+    fwd_s, step_s = [], []
+    for _ in range(reps):
+        h = H.detach().requires_grad_()
+        w = W.detach().requires_grad_()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = StreamedRoutedExpertsFunction.apply(h, w, I, trainer, 0, None, active, None)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        out.backward(G)
+        torch.cuda.synchronize()
+        fwd_s.append(t1 - t0)
+        step_s.append(time.perf_counter() - t0)
+    t_stage = float(np.median(stage_s))
+    log(f"[bench] streamed node: {len(active)} experts ({nbytes / 1e9:.2f} GB) staged in {t_stage * 1e3:.1f} ms "
+        f"({nbytes / t_stage / 1e9:.1f} GB/s), forward {np.median(fwd_s) * 1e3:.1f} ms, "
+        f"fwd+bwd {np.median(step_s) * 1e3:.1f} ms")
+    del bundles
+    return {"experts_streamed": len(active), "bytes_per_pass": nbytes,
+            "staging_s": t_stage, "staging_GBps": nbytes / t_stage / 1e9,
+            "forward_s": float(np.median(fwd_s)), "forward_backward_s": float(np.median(step_s)),
+            "source": "pageable host tensors (ExpertWeightBundle-shaped), pinned staging, copy stream"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -405,6 +485,7 @@ def main():
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
 
     extra = {}
+    zipf_inputs = None
     if not args.no_extra and layout.get("forward_layout"):
         # the same step reading only the checkpoint layout, for comparison (then the copy is rebuilt)
         layer.drop_forward_layout()
@@ -425,7 +506,9 @@ def main():
         # config 3: the same layer's forward alone, both routings
         extra["config3_forward"] = {"uniform": time_forward(args, k, layer, H, I, W, ws, n_active),
                                     "zipf": time_forward(args, k, layer, Hz, Iz, Wz, ws, nz)}
-        del Hz, Iz, Wz, Gz
+        # the reference-signature streamed node on the Zipf routing's active experts
+        extra["streamed_node"] = streamed_node_sample(args, k, layer, Hz, Iz, Wz, Gz)
+        zipf_inputs = (Hz, Iz, Wz, Gz)
         # config 2 at its two ends, M = 1 (HBM-bound) and M = 256 (MFMA-bound)
         del ws
         torch.cuda.empty_cache()
@@ -457,12 +540,23 @@ def main():
             "h2d_GBps": r5z["copy_bytes"] / r5z["copy_s"] / 1e9,
             "hidden_compute_fraction": r5z["hidden_compute_fraction"]}
         del hosts
+        ls = extra["config5_sample"]["zipf_active_experts_only"]["h2d_GBps"]
+        extra["streamed_node"]["layer_streamer_GBps_same_experts"] = ls
+        extra["streamed_node"]["staging_vs_layer_streamer"] = extra["streamed_node"]["staging_GBps"] / ls
 
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline (the reference composition on the C restatement + torch CPU) ...")
-        cpu = cpu_baseline(layer, H, I, W, G, args.cpu_seconds, args.act)
+        ex = cpu_host_layer(layer)
+        cpu = cpu_baseline(ex, H, I, W, G, args.cpu_seconds, args.act)
         log(f"[bench] CPU baseline {cpu['value']:.2f} tokens/s on {cpu['cores']} threads")
+        if zipf_inputs is not None:  # the Zipf layer, where the reference's > 48-row branch runs
+            cz = cpu_baseline(ex, *zipf_inputs, args.cpu_seconds, args.act)
+            log(f"[bench] CPU baseline, Zipf routing: {cz['value']:.2f} tokens/s")
+            extra["cpu_baseline_zipf"] = cz
+            if "zipf" in extra:
+                extra["zipf"]["vs_cpu_baseline_zipf"] = extra["zipf"]["tokens_per_s"] / cz["value"]
+        del ex
 
     line = {
         "metric": METRIC,
