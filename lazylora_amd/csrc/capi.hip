@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "../../include/lazylora_mxfp4.h"
 #include "mx_device.h"
@@ -100,7 +101,7 @@ long long pad32(long long v) { return (v + 31) / 32 * 32; }
 // Routed-layer workspace: one layout for forward and backward so the backward can reuse
 // what the forward left behind.
 struct MoeLayout {
-  size_t meta, counts, offsets, cursor, tiles, small_tiles, groups, pair_token, pair_w, pair_of;
+  size_t meta, counts, offsets, cursor, tiles, small_tiles, groups, wgroups, pair_token, pair_w, pair_of;
   size_t at_x, xt_x, at_act;
   size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part;
   size_t l_u, l_delta, l_v, l_vsum, l_q, l_rq, l_dh, l_dsum, l_part;  // LoRA (rank <= kLoraMaxRank)
@@ -122,6 +123,7 @@ MoeLayout moe_layout(int N, int k, int E, int D, int F)
   L.tiles = o; o = align_up(o + sizeof(int4) * (size_t)L.max_tiles);
   L.small_tiles = o; o = align_up(o + sizeof(int) * (size_t)L.max_tiles);
   L.groups = o; o = align_up(o + sizeof(int4) * (size_t)L.max_tiles);
+  L.wgroups = o; o = align_up(o + sizeof(int4) * (size_t)L.max_tiles);
   L.pair_token = o; o = align_up(o + sizeof(int) * (size_t)P);
   L.pair_w = o; o = align_up(o + sizeof(float) * (size_t)P);
   L.pair_of = o; o = align_up(o + sizeof(int) * (size_t)P);
@@ -186,6 +188,10 @@ void set_buckets(Args& a, void* ws, const MoeLayout& L)
   a.n_small = at<int>(ws, L.meta) + 2;
   a.groups = at<int4>(ws, L.groups);
   a.n_groups = at<int>(ws, L.meta) + 3;
+  if constexpr (std::is_same<Args, mx::FwdArgs>::value) {
+    a.wgroups = at<int4>(ws, L.wgroups);
+    a.n_wgroups = at<int>(ws, L.meta) + 4;
+  }
 }
 
 // The layer's LoRA adapters, shared by all its experts (lazy_trainer.py:130-134).
@@ -240,7 +246,7 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   const long long P = (long long)N * k;
   MX_TRY(mx::launch_route(idx, idx_dtype == MXFP4_I64, w, N, k, E, at<int>(ws, L.counts), at<int>(ws, L.offsets),
                           at<int>(ws, L.cursor), at<int4>(ws, L.tiles), at<int>(ws, L.small_tiles),
-                          at<int4>(ws, L.groups), at<int>(ws, L.meta), at<int>(ws, L.pair_token),
+                          at<int4>(ws, L.groups), at<int4>(ws, L.wgroups), at<int>(ws, L.meta), at<int>(ws, L.pair_token),
                           at<float>(ws, L.pair_w), at<int>(ws, L.pair_of), s),
          "route");
   MX_PHASE("route", s);
@@ -281,6 +287,7 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
     a.fl0 = fl[0]; a.fl1 = fl[1];
     a.fl_estride = mx::forward_layout_bytes(F, D);
   }
+  a.wcounter = at<int>(ws, L.meta) + 8;
   a.save = (save || lo.r) ? at<float>(ws, L.saved) : nullptr;
   a.act_kind = act_kind;
   const int r = lo.r;
@@ -538,6 +545,7 @@ int mxfp4_moe_forward_fl(float* out, const void* h, int h_dtype, const void* top
   a.y = at<float>(workspace, L.ypair); a.ldy = D;
   a.row_w = at<float>(workspace, L.pair_w);
   set_buckets(a, workspace, L);
+  a.wcounter = at<int>(workspace, L.meta) + 10;
   MX_TRY(mx::launch_fwd(a, mx::kFwdDown, L.max_tiles, stream), "moe_forward: down product");
   MX_PHASE("fwd_down", stream);
   MX_TRY(mx::launch_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D, stream),

@@ -290,6 +290,25 @@ MX_DEV void wait_vm()
 MX_DEV void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 MX_DEV void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Work queue of a resident grid. counter[0] hands out items in order (one atomic per work-group
+// and item); counter[1] counts the work-groups that have found the queue empty, and the last of
+// them resets both to zero, so the next launch on the same counters starts from item 0 without
+// a clearing launch. Every work-group of the grid must call queue_leave once, after its loop.
+MX_DEV int queue_next(int* counter, int* s_item)
+{
+  __syncthreads();  // every wave is done with the previous item (and with *s_item)
+  if (threadIdx.x == 0) *s_item = atomicAdd(counter, 1);
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(*s_item);
+}
+MX_DEV void queue_leave(int* counter)
+{
+  if (threadIdx.x == 0 && atomicAdd(counter + 1, 1) == (int)gridDim.x - 1) {
+    atomicExch(counter, 0);
+    atomicExch(counter + 1, 0);
+  }
+}
+
 // bf16 helpers (round to nearest even, as v_cvt_pk_bf16_f32 does)
 MX_DEV uint32_t pack_bf16(float a, float b)
 {

@@ -837,6 +837,242 @@ __global__ __launch_bounds__(64 * kGmWaves, 1) void fwd_gemm_kernel(FwdArgs a)
   }
 }
 
+// ---------------------------------------------------------------- large buckets, forward layout
+// With a forward layout the large buckets take wider items: one wide group (up to
+// kWideGroupTiles = 8 row tiles, 128 rows) x eight column tiles (512 weight rows, 64 per wave of
+// an eight-wave work-group that holds the CU alone). Each wave loads its own weight operands
+// straight into registers, one contiguous KiB per MFMA operand block of the forward layout
+// (two quarters in flight); only the activations go through LDS, one quarter (8 tiles x 4 KiB,
+// copied from the AT layout as it lies) at a time, double-buffered. Per quarter a wave issues
+// 8 tiles x 4 column groups x 2 terms = 64 MFMAs, for 64 KiB the CU reads (32 KiB of
+// activations, 32 KiB of weights): half the bytes per MFMA of the four-tile items, whose rate
+// the CU's reads in flight bound. Block order and lane layouts are the one-tile kernels' (MFMA q
+// takes blocks 4g + q), so both operands are copied as they lie. Each super-chunk's activation
+// scales (8 tiles x 512 B) go through LDS; the weight scales of four super-chunks at a time
+// (64 B per row) through a per-wave LDS window.
+//
+// Per quarter s (super-chunk s / 4, MFMA q = s % 4): wait until only the weight loads of quarter
+// s + 1 are outstanding, barrier, request the activation copy of quarter s + 1 (and, when due,
+// the next super-chunk's activation scales and the next scale window), 64 MFMAs, then the weight
+// loads of quarter s + 2 into the registers quarter s has just read. The copies are issued from
+// inline assembly, so the compiler counts only the weight loads, and its own wait for quarter s's
+// weights (vmcnt 4: quarter s + 1's four loads) is the one above.
+constexpr int kWgT = kWideGroupTiles;  // row tiles per item
+constexpr int kWgWaves = 8;            // column tiles per item (one per wave)
+constexpr int kWgA = kWgT * 4096;      // activation bytes per quarter
+constexpr int kWgWin = 4;              // super-chunks per weight-scale window
+struct WideLds {
+  uint8_t a[2][kWgA];                      // quarter buffers: [tile][plane][piece][lane][16 B]
+  uint8_t sa[2][kWgT][1024];               // super-chunk activation scales: [c % 2][tile][lane][plane][4 B], + a spare half
+  uint8_t sw[kWgWaves][64 * 16 * kWgWin];  // weight-scale windows: [wave][row 0..63][super-chunk 0..3][16 B]
+};
+
+template <int MODE>
+__device__ __forceinline__ void fwd_wide_item(const FwdArgs& a, int expert, int t0, int ntl, int fb, int wave,
+                                              int lane, WideLds& lds)
+{
+  constexpr int T = kWgT;
+  const int g = lane >> 4;
+  const int nb = a.K / kGroup;
+  const int nsc = a.K / kChunk;  // the fast path: K is a multiple of 512
+  const int ns = 4 * nsc;
+  const int ct_raw = fb * kWgWaves + wave;
+  const bool active = ct_raw < a.n_ct;
+  const int ct = active ? ct_raw : a.n_ct - 1;
+
+  // first weight row of column group cg (gate/up: groups 2, 3 are W3's rows)
+  auto grp_row = [&](int cg) { return MODE == kFwdGateUp ? ct * 32 + (cg & 1) * 16 : ct * kFwdColsPerTile + cg * 16; };
+  auto s_base = [&](int cg) {
+    return (MODE == kFwdGateUp && cg >= 2 ? a.ws1 : a.ws0) + (long long)expert * a.ws_estride;
+  };
+  // weight operands: column group cg is row group rg = row0 / 16 of the forward layout, whose
+  // quarter s is the KiB at s * 1024 (lane l's 16 B at l * 16); past the last quarter an empty
+  // resource returns zeros without memory traffic and keeps the load count
+  rsrc_t wr[4];
+#pragma unroll
+  for (int cg = 0; cg < 4; ++cg) {
+    const int rg = min(grp_row(cg), a.R - 1) / 16;
+    const uint8_t* base = (MODE == kFwdGateUp && cg >= 2 ? a.fl1 : a.fl0) + (long long)expert * a.fl_estride +
+                          (long long)rg * nsc * 4096;
+    wr[cg] = make_rsrc(base, (uint32_t)((a.R + 15) / 16 - rg) * (uint32_t)nsc * 4096u);
+  }
+  const rsrc_t wr_none = make_rsrc(a.fl0, 0);
+  auto load_b = [&](int s, i32x4 (&b)[4]) {
+    const bool live = s < ns;  // uniform
+#pragma unroll
+    for (int cg = 0; cg < 4; ++cg) b[cg] = buf16_nt(live ? wr[cg] : wr_none, (uint32_t)lane * 16u, (uint32_t)s * 1024u);
+  };
+  // activation copies: wave w takes tile w (the group's last tile past its end)
+  const uint8_t* my_tile = a.a_tiles + (long long)(t0 + min(wave, ntl - 1)) * at_tile_bytes(a.K);
+  auto issue_a = [&](int s) {
+    const uint8_t* src = my_tile + (long long)(s >> 2) * kAtChunkBytes + (s & 3) * 4096;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dma16_async_s(src, (uint32_t)(lane * 16 + u * 1024), &lds.a[s & 1][wave * 4096 + u * 1024]);
+  };
+  auto issue_sa = [&](int c) {  // lanes 32..63 repeat lanes 0..31 into the spare half
+    dma16_async_s(my_tile + (long long)c * kAtChunkBytes + kAtCodeBytes, (uint32_t)((lane & 31) * 16),
+                  &lds.sa[c & 1][wave][0]);
+  };
+  // weight-scale window `win`: instruction k copies column group k's 16 rows, lane l 16 B of row
+  // l / 4 (super-chunk 4 win + l % 4) to row * 64 + (l % 4) * 16
+  auto issue_sw = [&](int win) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int n = min(grp_row(k) + (lane >> 2), a.R - 1);
+      const int cc = min(win * kWgWin + (lane & 3), nsc - 1);
+      dma16_async_s(s_base(k), (uint32_t)(n * nb + cc * 16), &lds.sw[wave][k * 1024]);
+    }
+  };
+
+  f32x4 acc[T][4];
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+    for (int cg = 0; cg < 4; ++cg) acc[tt][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // the previous item's epilogue stores complete here, in a wait the compiler sees: with stores
+  // of unknown completion order pending it would wait for every load at the loop's head
+  __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+  issue_sw(0);
+  issue_sa(0);
+  issue_a(0);
+  i32x4 b0[4], b1[4];
+  uint32_t rw[4];  // this super-chunk's weight scale dwords (byte q: block 4g + q)
+  bool damaged = false;
+
+  auto step = [&](int c, auto Q, i32x4 (&b)[4], bool tail) {
+    constexpr int q = decltype(Q)::value;
+    const int s = 4 * c + q;
+    wait_vm<4>();
+    __syncthreads();
+#pragma unroll
+    for (int cg = 0; cg < 4; ++cg) pin(b[cg]);
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    if constexpr (q == 0) {
+      const int j = l & 15;
+      uint32_t d = 0;
+#pragma unroll
+      for (int cg = 0; cg < 4; ++cg) {
+        rw[cg] = *reinterpret_cast<const uint32_t*>(&lds.sw[wave][(cg * 16 + j) * 64 + (c % kWgWin) * 16 + (l >> 4) * 4]);
+        d |= damaged_scale_bits(rw[cg]);
+      }
+      wait_lgkm0();  // before any copy may overwrite the window read here
+      damaged = __builtin_amdgcn_ballot_w64(d != 0u) != 0;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 1 < ns) {
+      issue_a(s + 1);
+      if (((s + 1) & 3) == 0) issue_sa((s + 1) >> 2);
+      // the next window, after this wave's last read of the current one (super-chunk 4 win + 3, q = 0)
+      const int win = s / (4 * kWgWin);
+      if (s % (4 * kWgWin) == 4 * (kWgWin - 1) + 1 && (win + 1) * kWgWin < nsc) issue_sw(win + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t sb[4];
+#pragma unroll
+    for (int cg = 0; cg < 4; ++cg) sb[cg] = rw[cg];
+    if (damaged) {  // scale bytes >= 253: zero block, scale 2^0 (uniform branch, rare)
+#pragma unroll
+      for (int cg = 0; cg < 4; ++cg) {
+        const bool dead = ((rw[cg] >> (8 * q)) & 0xFFu) >= 253u;
+        b[cg] = dead ? i32x4{0, 0, 0, 0} : b[cg];
+        sb[cg] = dead ? (rw[cg] & ~(0xFFu << (8 * q))) | (127u << (8 * q)) : rw[cg];
+      }
+    }
+    // tile tt's operands are read from LDS while tile tt - 1's MFMAs run (one tile ahead)
+    const uint8_t* la = &lds.a[q & 1][l * 16];
+    const uint8_t* ls = &lds.sa[c & 1][0][l * 8];
+    auto read_a = [&](int tt, i32x8& ah, i32x8& al, uint2& sc) {
+      const uint8_t* pa = la + tt * 4096;
+      ah = cat8(*reinterpret_cast<const i32x4*>(pa), *reinterpret_cast<const i32x4*>(pa + 1024));
+      al = cat8(*reinterpret_cast<const i32x4*>(pa + 2048), *reinterpret_cast<const i32x4*>(pa + 3072));
+      sc = *reinterpret_cast<const uint2*>(ls + tt * 1024);
+    };
+    i32x8 ah, al, nh, nl;
+    uint2 sc, nsc2;
+    read_a(0, nh, nl, nsc2);
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) {
+      ah = nh;
+      al = nl;
+      sc = nsc2;
+      if (tt + 1 < T) read_a(tt + 1, nh, nl, nsc2);
+      if (tt < ntl) {
+        // the four hi-term MFMAs, then the four lo-term ones: each lo MFMA reads the accumulator
+        // its hi MFMA wrote three instructions earlier rather than right before it
+        f32x4 t4[4];
+#pragma unroll
+        for (int cg = 0; cg < 4; ++cg) t4[cg] = mfma_f8f4<q, q>(ah, b[cg], acc[tt][cg], (int)sc.x, (int)sb[cg]);
+#pragma unroll
+        for (int cg = 0; cg < 4; ++cg) acc[tt][cg] = mfma_f8f4<q, q>(al, b[cg], t4[cg], (int)sc.y, (int)sb[cg]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (tail) load_b(s + 2, b);
+  };
+
+  // The last step of a super-chunk leaves its weight loads (quarter s + 2) to the head of the
+  // next iteration, so only one register buffer is in flight across the loop's back edge: with
+  // two, the compiler waits for both at the loop head.
+  load_b(0, b0);
+  for (int c = 0; c < nsc; ++c) {
+    load_b(4 * c + 1, b1);
+    step(c, std::integral_constant<int, 0>{}, b0, true);
+    step(c, std::integral_constant<int, 1>{}, b1, true);
+    step(c, std::integral_constant<int, 2>{}, b0, true);
+    step(c, std::integral_constant<int, 3>{}, b1, false);
+  }
+  wait_vm0();
+  if (!active) return;
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt) {
+    if (tt >= ntl) break;
+    WorkItem w;
+    w.tile = t0 + tt;
+    const cint_ptr tl = (cint_ptr)(a.tiles + w.tile);
+    w.expert = expert;
+    w.row0 = tl[1];
+    w.nrows = tl[2];
+    w.ct0 = fb * kWgWaves;
+    w.ct = ct;
+    w.active = true;
+    float tw[4];
+    if (MODE == kFwdDown)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tw[v] = a.row_w[w.row0 + min(4 * g + v, w.nrows - 1)];
+    epilogue_direct<MODE>(a, w, lane, acc[tt], tw);
+  }
+}
+
+// Resident grid (one eight-wave work-group per CU) over the items (wide group, block of eight
+// column tiles). Items vary in cost (a partial group has fewer tiles, and its MFMAs for the
+// missing tiles are skipped), so the work-groups take them from a work counter in list order:
+// the full groups' items first, then the partial groups', which fill in behind them. Consecutive
+// items are the eight column blocks of one group, which run at about the same time and share its
+// activations.
+template <int MODE>
+__global__ __launch_bounds__(64 * kWgWaves, 1) void fwd_wide_kernel(FwdArgs a)
+{
+  __shared__ WideLds lds;
+  __shared__ int s_item;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ng = *(cint_ptr)a.n_wgroups;
+  const int nfb = (a.n_ct + kWgWaves - 1) / kWgWaves;
+  const int total = ng * nfb;
+  for (;;) {
+    const int item = queue_next(a.wcounter, &s_item);  // also: every wave is done with the previous item's LDS
+    if (item >= total) break;
+    const int gi = item / nfb, fb = item - gi * nfb;
+    const cint_ptr gg = (cint_ptr)(a.wgroups + gi);
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    fwd_wide_item<MODE>(a, gg[0], gg[1], gg[2], fb, wave, l, lds);
+  }
+  queue_leave(a.wcounter);
+}
+
 // Work-groups that fit on the device at once (two per CU: the LDS and register budgets of
 // fwd_kernel), rounded down to a multiple of the 8 XCDs.
 int resident_groups()
@@ -869,6 +1105,7 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   if (!split) {
     b.small_tiles = nullptr;
     b.groups = nullptr;
+    b.wgroups = nullptr;
   }
   // both work-group shapes read the forward layout when every matrix of the product has one
   // (and its byte count fits a buffer resource, as for the checkpoint layout)
@@ -891,6 +1128,12 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !split) return e;
   dim3 mgrid((unsigned)(resident_groups() / 16 * 8)), mblock(64 * kGmWaves);  // one per CU, a multiple of 8
+  if (fl && b.wgroups && b.wcounter && mode != kFwdPlain) {  // wide groups, weights straight from the forward layout
+    dim3 wblock(64 * kWgWaves);
+    if (mode == kFwdGateUp) hipLaunchKernelGGL((fwd_wide_kernel<kFwdGateUp>), mgrid, wblock, 0, s, b);
+    else hipLaunchKernelGGL((fwd_wide_kernel<kFwdDown>), mgrid, wblock, 0, s, b);
+    return hipGetLastError();
+  }
   if (mode == kFwdGateUp) {
     if (fl) hipLaunchKernelGGL((fwd_gemm_kernel<kFwdGateUp, true>), mgrid, mblock, 0, s, b);
     else hipLaunchKernelGGL((fwd_gemm_kernel<kFwdGateUp, false>), mgrid, mblock, 0, s, b);

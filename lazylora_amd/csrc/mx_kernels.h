@@ -54,6 +54,11 @@ struct FwdArgs {
   const int* n_small;
   const int4* groups;
   const int* n_groups;
+  // The same large-bucket tiles as wide groups of up to kWideGroupTiles tiles, taken instead of
+  // `groups` by the large-bucket work-groups that read a forward layout (null: use `groups`).
+  const int4* wgroups;
+  const int* n_wgroups;
+  int* wcounter;  // the wide-group launch's work queue: 2 ints, zero before the first launch (queue_next)
   // Forward layout (launch_forward_layout) of W (W1 for kFwdGateUp) and W3, or null: the
   // fast path's work-groups then read their weight codes from it in whole lines (the scales,
   // and the general path, always come from wp* / ws*).
@@ -116,6 +121,7 @@ struct BwdArgs {
 
 constexpr int kFwdRowsPerTile = 16;
 constexpr int kGroupTiles = 4;     // row tiles of one large-bucket group
+constexpr int kWideGroupTiles = 8;  // row tiles of one wide group (the forward-layout large-bucket forward)
 constexpr int kGroupMinTiles = 4;  // experts with at least this many tiles take the large-bucket path
 constexpr int kFwdColsPerTile = 64;  // kFwdPlain / kFwdDown; kFwdGateUp covers 32 features
 constexpr int kBwdColsPerTile = 256;  // output columns of one transposed-product wave
@@ -150,11 +156,14 @@ hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int
 hipError_t launch_dequant(void* out, int out_bf16, const uint8_t* packed, const uint8_t* scales, int K, int R,
                           hipStream_t s);
 // Routing: per-expert counts, scan, the tile list (tiles[t] = {expert, first pair row, rows, large}),
-// the small-bucket tile indices and the large-bucket groups ({expert, first tile, tiles, 0}),
-// meta = {tiles, flags (bit 0: an id outside [0, E)), small tiles, groups}, and the pair maps.
+// the small-bucket tile indices, the large-bucket groups ({expert, first tile, tiles, 0}) of up to
+// kGroupTiles tiles and the same tiles again as wide groups of up to kWideGroupTiles (the full
+// ones first), meta = {tiles, flags (bit 0: an id outside [0, E)), small tiles, groups, wide
+// groups, full wide groups, -, -, then the work queues (2 ints each) of the wide-group launches of
+// the forward gate/up and down products, ...} (16 ints, all zeroed here), and the pair maps.
 hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, int N, int k, int E,
                         int* counts, int* offsets, int* cursor, int4* tiles, int* small_tiles, int4* groups,
-                        int* meta, int* pair_token, float* pair_w, int* pair_of, hipStream_t s);
+                        int4* wgroups, int* meta, int* pair_token, float* pair_w, int* pair_of, hipStream_t s);
 hipError_t launch_combine(float* out, const float* ypair, long long ldy, const int* pair_of, int N, int k,
                           int D, hipStream_t s);
 hipError_t launch_combine_bwd(float* grad_h, float* grad_w, const float* dxpair, long long ldy,

@@ -221,44 +221,63 @@ __global__ __launch_bounds__(256) void route_count_kernel(const void* idx, int i
 
 // Single work-group: exclusive scan of counts and of per-expert tile counts, tile list. An
 // expert with at least kGroupMinTiles tiles (a large bucket) also gets its tiles listed as
-// groups of up to kGroupTiles consecutive tiles; the other experts' tile indices go to the
-// small-bucket list. meta = {tiles, flags, small tiles, groups}.
+// groups of up to kGroupTiles consecutive tiles, and again as wide groups of up to
+// kWideGroupTiles: every full wide group first (expert order), then the experts' last, partial
+// ones, so that a work queue taking them in order hands out the largest items first. The other
+// experts' tile indices go to the small-bucket list. meta = {tiles, flags, small tiles, groups,
+// wide groups, full wide groups}.
 __global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int E, int* offsets, int* cursor,
-                                                          int4* tiles, int* small_tiles, int4* groups, int* meta)
+                                                          int4* tiles, int* small_tiles, int4* groups, int4* wgroups,
+                                                          int* meta)
 {
   __shared__ int s_rows[1024];
   __shared__ int s_tiles[1024];
   __shared__ int s_small[1024];
   __shared__ int s_groups[1024];
+  __shared__ int s_wgroups[1024];
+  __shared__ int s_wpart[1024];
   const int t = threadIdx.x;
   const int per = (E + 1023) / 1024;
   const int e0 = min(t * per, E), e1 = min(e0 + per, E);
-  int rows = 0, nt = 0, ns = 0, ng = 0;
+  int rows = 0, nt = 0, ns = 0, ng = 0, nw = 0, np = 0;  // nw: full wide groups, np: partial ones
   for (int e = e0; e < e1; ++e) {
     const int et = (counts[e] + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
     rows += counts[e];
     nt += et;
-    if (et >= kGroupMinTiles) ng += (et + kGroupTiles - 1) / kGroupTiles;
-    else ns += et;
+    if (et >= kGroupMinTiles) {
+      ng += (et + kGroupTiles - 1) / kGroupTiles;
+      nw += et / kWideGroupTiles;
+      np += et % kWideGroupTiles ? 1 : 0;
+    } else {
+      ns += et;
+    }
   }
   s_rows[t] = rows;
   s_tiles[t] = nt;
   s_small[t] = ns;
   s_groups[t] = ng;
+  s_wgroups[t] = nw;
+  s_wpart[t] = np;
   __syncthreads();
   for (int d = 1; d < 1024; d <<= 1) {  // Hillis-Steele inclusive scans
     const int a = t >= d ? s_rows[t - d] : 0;
     const int b = t >= d ? s_tiles[t - d] : 0;
     const int c = t >= d ? s_small[t - d] : 0;
     const int g = t >= d ? s_groups[t - d] : 0;
+    const int w = t >= d ? s_wgroups[t - d] : 0;
+    const int v = t >= d ? s_wpart[t - d] : 0;
     __syncthreads();
     s_rows[t] += a;
     s_tiles[t] += b;
     s_small[t] += c;
     s_groups[t] += g;
+    s_wgroups[t] += w;
+    s_wpart[t] += v;
     __syncthreads();
   }
-  int row_off = s_rows[t] - rows, tile_off = s_tiles[t] - nt, small_off = s_small[t] - ns, group_off = s_groups[t] - ng;
+  const int n_full = s_wgroups[1023];
+  int row_off = s_rows[t] - rows, tile_off = s_tiles[t] - nt, small_off = s_small[t] - ns, group_off = s_groups[t] - ng,
+      wgroup_off = s_wgroups[t] - nw, wpart_off = n_full + s_wpart[t] - np;
   for (int e = e0; e < e1; ++e) {
     const int c = counts[e];
     const int et = (c + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
@@ -266,6 +285,10 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int
     cursor[e] = row_off;
     if (et >= kGroupMinTiles) {
       for (int g = 0; g < et; g += kGroupTiles) groups[group_off++] = make_int4(e, tile_off + g, min(kGroupTiles, et - g), 0);
+      for (int g = 0; g + kWideGroupTiles <= et; g += kWideGroupTiles)
+        wgroups[wgroup_off++] = make_int4(e, tile_off + g, kWideGroupTiles, 0);
+      if (et % kWideGroupTiles)
+        wgroups[wpart_off++] = make_int4(e, tile_off + et / kWideGroupTiles * kWideGroupTiles, et % kWideGroupTiles, 0);
     } else {
       for (int m = 0; m < et; ++m) small_tiles[small_off++] = tile_off + m;
     }
@@ -278,6 +301,8 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int
     meta[0] = s_tiles[1023];
     meta[2] = s_small[1023];
     meta[3] = s_groups[1023];
+    meta[4] = s_wgroups[1023] + s_wpart[1023];
+    meta[5] = s_wgroups[1023];
   }
 }
 
@@ -479,17 +504,17 @@ hipError_t launch_zero(void* p, size_t bytes, hipStream_t s)
 }
 
 hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, int N, int k, int E, int* counts,
-                        int* offsets, int* cursor, int4* tiles, int* small_tiles, int4* groups, int* meta,
-                        int* pair_token, float* pair_w, int* pair_of, hipStream_t s)
+                        int* offsets, int* cursor, int4* tiles, int* small_tiles, int4* groups, int4* wgroups,
+                        int* meta, int* pair_token, float* pair_w, int* pair_of, hipStream_t s)
 {
   const int P = N * k;
   hipError_t e = launch_zero(counts, sizeof(int) * (size_t)E, s);
   if (e != hipSuccess) return e;
-  e = launch_zero(meta, sizeof(int) * 4, s);
+  e = launch_zero(meta, sizeof(int) * 16, s);
   if (e != hipSuccess) return e;
   if (P > 0) hipLaunchKernelGGL(route_count_kernel, dim3((P + 255) / 256), dim3(256), 0, s, topk_idx, idx64, P, E, counts, meta);
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, s, counts, E, offsets, cursor, tiles, small_tiles,
-                     groups, meta);
+                     groups, wgroups, meta);
   if (P > 0)
     hipLaunchKernelGGL(route_place_kernel, dim3((P + 255) / 256), dim3(256), 0, s, topk_idx, idx64, topk_w, P, k, E,
                        cursor, pair_token, pair_w, pair_of);

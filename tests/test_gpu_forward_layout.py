@@ -65,9 +65,16 @@ def adapters(lo):
                  for A, B, s in lo.adapters())
 
 
-def both_ways(k, L, H, I, W, G, act="swiglu", lora=None):
+def both_ways(k, L, H, I, W, G, act="swiglu", lora=None, large=False):
     """Forward, backward recomputing the forward, and backward reusing it: without and with the
-    forward layout."""
+    forward layout. Without large buckets (experts of four or more 16-row tiles) the results are
+    bit-identical: every product reads the same bytes in the same order either way. With them
+    (large=True) the large-bucket forward takes its MX blocks in the one-tile kernels' grouping
+    with the forward layout and four consecutive blocks per MFMA without it, so the fp32 sums
+    differ in rounding only (a sum that lands on the other side of an e4m3 rounding boundary of the act
+    requantisation moves one term of the down product): the two must agree to rel-L2 1e-4 (well
+    below the 5e-3 parity bar,
+    which each meets against the oracle in the routed-layer tests)."""
     res = []
     for use in (False, True):
         if use:
@@ -83,7 +90,12 @@ def both_ways(k, L, H, I, W, G, act="swiglu", lora=None):
         res.append(flat)
     L.drop_forward_layout()
     for i, (a, b) in enumerate(zip(*res)):
-        assert torch.equal(a, b), f"result {i} differs with the forward layout"
+        if large:
+            r = oracle.rel_l2(b.cpu().numpy(), a.cpu().numpy())
+            print(f"result {i}: rel-L2 {r:.2e} between the layouts")
+            assert r <= 1e-4, f"result {i} differs with the forward layout: rel-L2 {r:.2e}"
+        else:
+            assert torch.equal(a, b), f"result {i} differs with the forward layout"
 
 
 def inputs(rng, N, D, E, topk, sizes=None):
@@ -115,7 +127,7 @@ def test_routed_layer_large_buckets_and_lora(k):
     rng = np.random.default_rng(62)
     L = layer_of(oracle.random_experts(rng, 4, 1024, 512, 118, 122))
     lora = adapters(oracle.random_lora(rng, 1024, 512, 8))
-    both_ways(k, L, *inputs(rng, 0, 1024, 4, 1, sizes=[150, 70, 30, 6]), lora=lora)
+    both_ways(k, L, *inputs(rng, 0, 1024, 4, 1, sizes=[150, 70, 30, 6]), lora=lora, large=True)
 
 
 def test_reference_expert_shape_with_lora(k):
@@ -191,6 +203,6 @@ def test_baseline_size(k, zipf):
     idx, w = oracle.softmax_topk(logits, 8)
     H, I, W, G = (torch.from_numpy(a).cuda() for a in (rng.standard_normal((N, D)).astype(np.float32), idx, w,
                                                        rng.standard_normal((N, D)).astype(np.float32)))
-    both_ways(k, L, H, I, W, G)
+    both_ways(k, L, H, I, W, G, large=zipf)
     del L
     torch.cuda.empty_cache()

@@ -116,13 +116,14 @@ def test_skewed_routing_large_buckets(k):
     assert_close(gw.cpu().numpy(), gw64, "skew grad_w")
 
 
-@pytest.mark.parametrize("topk", [1, 2])
-def test_large_bucket_groups(k, topk):
+@pytest.mark.parametrize("topk,fl", [(1, False), (2, False), (1, True), (2, True)])
+def test_large_bucket_groups(k, topk, fl):
     """Buckets of 200, 129, 65, 64, 49, 48, 17 and 1 rows: the experts with four or more 16-row
     tiles take the grouped work-groups (groups of 4 tiles, ragged last groups down to one tile,
-    ragged last tile), the rest the one-tile work-groups; K = 1024 and 512 keep both products on
-    the path that splits them."""
-    case(f"large-bucket groups: E=9, D=1024, F=512, top-{topk}")
+    ragged last tile; with a forward layout (fl) wide groups of 8 tiles: 13 = 8 + 5, 9 = 8 + 1,
+    5, 4), the rest the one-tile work-groups; K = 1024 and 512 keep both products on the path
+    that splits them."""
+    case(f"large-bucket groups: E=9, D=1024, F=512, top-{topk}, forward layout={fl}")
     rng = np.random.default_rng(18 + topk)
     E, D, F = 9, 1024, 512
     ex = oracle.random_experts(rng, E, D, F, 118, 122)
@@ -140,6 +141,8 @@ def test_large_bucket_groups(k, topk):
     h = rng.standard_normal((N, D)).astype(np.float32)
     g = rng.standard_normal((N, D)).astype(np.float32)
     L = layer_of(ex)
+    if fl:
+        L.prepare_forward_layout()
     H, I, W, G = (torch.from_numpy(a).cuda() for a in (h, idx, w, g))
     for act in ("swiglu", "situ"):
         assert_close(k.routed_forward(H, I, W, L, act=act).cpu().numpy(), oracle.routed_forward(h, idx, w, ex, act),
@@ -559,12 +562,15 @@ def assert_all_tokens(got, want, label, tol):
     assert r[worst] <= tol, f"{label}: token {worst} rel-L2 {r[worst]:.3e} > {tol:.1e}"
 
 
-@pytest.mark.parametrize("zipf", [False, True])
-def test_baseline_layer_all_tokens(k, clib, full_layer, full_layer_host, zipf):
+@pytest.mark.parametrize("zipf,fl", [(False, False), (True, False), (True, True)])
+def test_baseline_layer_all_tokens(k, clib, full_layer, full_layer_host, zipf, fl):
     """BASELINE configs 3/4 at full size: every one of the 1024 tokens of out, grad_h and grad_w
     against the C restatement of the reference path (lazy_trainer.py:806-880), uniform and
-    Zipf-skewed routing."""
-    case(f"config 3/4 layer, zipf={zipf}: fwd+bwd, all 1024 tokens vs C oracle")
+    Zipf-skewed routing; the Zipf layer also with its forward layout (fl), where its large buckets
+    take the wide-group forward."""
+    case(f"config 3/4 layer, zipf={zipf}, forward layout={fl}: fwd+bwd, all 1024 tokens vs C oracle")
+    if fl:
+        full_layer.prepare_forward_layout()
     rng = np.random.default_rng(21 + zipf)
     N, E, topk = 1024, 896, 8
     h = rng.standard_normal((N, 7168)).astype(np.float32)
@@ -579,6 +585,7 @@ def test_baseline_layer_all_tokens(k, clib, full_layer, full_layer_host, zipf):
     gh, gw = gh.cpu().numpy(), gw.cpu().numpy()
     assert_all_tokens(out, clib.moe_forward(h, idx, w, full_layer_host), f"layer fwd zipf={zipf}", 5e-3)
     gh_c, gw_c = clib.moe_backward(h, idx, w, full_layer_host, g)
+    full_layer.drop_forward_layout()
     assert_all_tokens(gh, gh_c, f"layer grad_h zipf={zipf}", 5e-3)
     assert_all_tokens(gw, gw_c, f"layer grad_w zipf={zipf}", 1e-2)
 
