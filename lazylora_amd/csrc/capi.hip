@@ -102,7 +102,7 @@ long long pad32(long long v) { return (v + 31) / 32 * 32; }
 // what the forward left behind.
 struct MoeLayout {
   size_t meta, counts, offsets, cursor, tiles, small_tiles, groups, wgroups, pair_token, pair_w, pair_of;
-  size_t at_x, xt_x, at_act;
+  size_t at_x, xt_x, x3_x, at_act;
   size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part;
   size_t l_u, l_delta, l_v, l_vsum, l_q, l_rq, l_dh, l_dsum, l_part;  // LoRA (rank <= kLoraMaxRank)
   size_t end;
@@ -129,6 +129,7 @@ MoeLayout moe_layout(int N, int k, int E, int D, int F)
   L.pair_of = o; o = align_up(o + sizeof(int) * (size_t)P);
   L.at_x = o; o += at_bytes(L.max_tiles, D);
   L.xt_x = o; o = align_up(o + (size_t)(mx::xt_rows(N) * mx::xt_row_bytes(D)));
+  L.x3_x = o; o = align_up(o + (size_t)(mx::xt_rows(N) * mx::x3_row_bytes(D)));
   L.at_act = o; o += at_bytes(L.max_tiles, F);
   L.saved = o; o = align_up(o + sizeof(float) * (size_t)(P * 2 * F));
   L.ypair = o; o = align_up(o + sizeof(float) * (size_t)(P * D));
@@ -257,12 +258,13 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   // the device). Without the split every tile reads the XT rows, so they are always written.
   const bool gu_split = mx::fwd_bucket_split(F, D);
   MX_TRY(mx::launch_quant_rows(h, h_dtype == MXFP4_BF16, D, N, D, gu_split ? at<int>(ws, L.meta) : nullptr,
-                               at<uint8_t>(ws, L.xt_x), s),
+                               at<uint8_t>(ws, L.xt_x), at<uint8_t>(ws, L.x3_x), at<int>(ws, L.meta) + 6, s),
          "quantise h");
   if (gu_split) {
     MX_TRY(mx::launch_quant_tiles(h, h_dtype == MXFP4_BF16, D, N, D, at<int4>(ws, L.tiles), at<int>(ws, L.meta),
                                   L.max_tiles, at<int>(ws, L.pair_token), 1, at<uint8_t>(ws, L.xt_x),
-                                  at<int>(ws, L.meta), at<uint8_t>(ws, L.at_x), s),
+                                  at<int>(ws, L.meta), at<uint8_t>(ws, L.at_x), at<uint8_t>(ws, L.x3_x),
+                                  at<int>(ws, L.meta) + 6, s),
            "quantise h tiles");
   }
   MX_PHASE("quant_h", s);
@@ -278,6 +280,9 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   a.a_rows = at<uint8_t>(ws, L.xt_x);
   a.a_row_bytes = mx::xt_row_bytes(D);
   a.a_zero_row = N;
+  a.x3 = at<uint8_t>(ws, L.x3_x);
+  a.x3_row_bytes = mx::x3_row_bytes(D);
+  a.x3_any = at<int>(ws, L.meta) + 6;
   a.row_token = at<int>(ws, L.pair_token);
   a.tiles = at<int4>(ws, L.tiles); a.n_tiles = at<int>(ws, L.meta);
   a.n_ct = F / 32;
@@ -341,7 +346,7 @@ int gemm_into(float* y, const float* x, const uint8_t* packed, const uint8_t* sc
 {
   const int tiles = (M + mx::kFwdRowsPerTile - 1) / mx::kFwdRowsPerTile;
   MX_TRY(mx::launch_quant_tiles(x, 0, K, M, K, nullptr, nullptr, tiles, nullptr, 0, nullptr, nullptr, tiles_dev,
-                                stream),
+                                nullptr, nullptr, stream),
          "gemm: quantise x");
   mx::FwdArgs a = {};
   a.wp0 = packed; a.ws0 = scales;

@@ -106,6 +106,15 @@ MX_DEV int xt_scale_off(int k, int plane)
   return c * kXtChunkBytes + kXtCodeBytes + (plane * 4 + g) * 4 + q;
 }
 
+// ------------------------------------------------------------------ X3: the third term of x
+// Token-major, per row x3_row_bytes(K) bytes: the third-term codes in natural element order (one
+// e4m3 byte per element, at_nchunks(K) * 512), the third-term block scales (16 bytes per
+// super-chunk, block b at b), then one flag byte per super-chunk (kX3Flags of them: 1 when a
+// block of that super-chunk has a third term). Blocks without a third term hold zero codes. The
+// third term covers the first kX3Flags super-chunks (K <= 16384); later blocks keep two terms.
+constexpr int kX3Flags = 32;
+__host__ __device__ inline long long x3_row_bytes(int K) { return (long long)at_nchunks(K) * 528 + kX3Flags; }
+
 // ------------------------------------------------------------------ small helpers
 MX_DEV float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
 MX_DEV uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
@@ -135,6 +144,7 @@ MX_DEV float group16_sum(float v)
 struct Quant2 {
   uint32_t hi, lo;
   uint32_t s_hi, s_lo;
+  float amax;  // the block's max |x|
 };
 MX_DEV Quant2 quant2_block16(float v0, float v1)
 {
@@ -161,6 +171,47 @@ MX_DEV Quant2 quant2_block16(float v0, float v1)
   r.lo = ql;
   r.s_hi = (uint32_t)sb;
   r.s_lo = (uint32_t)sl;
+  r.amax = amax;
+  return r;
+}
+
+// A third e4m3 term for blocks that two terms leave short. Two terms keep ~8 significant bits of
+// the block maximum; when one element dominates its block (max |x| > 16 x the rms of the other
+// 31) it usually dominates the row's dot products too (an outlier channel), and its rounding
+// (up to 2^-8 relative) then shows undiluted in that token's outputs. Such blocks are flagged and
+// get a third term: the residual after hi + lo, quantised again with its own scale (~12 bits for
+// the maximum). For every other block the third term is zero and its flag is clear.
+// Returns the third term's bytes (element 2n | 2n+1 << 8 of the lane), its scale byte and the flag
+// (the same on all 16 lanes of the block). q2 is the block's two-term result.
+struct Quant3 {
+  uint32_t th, s_th;
+  bool flag;
+};
+MX_DEV Quant3 quant3_block16(float v0, float v1, const Quant2& q2)
+{
+  Quant3 r{0u, 127u, false};
+  // in the hi term's scaled domain (|y| < 256): the flag and the residual after hi + lo
+  const float inv = bits_f((uint32_t)(254 - (int)q2.s_hi) << 23);  // 2^(127 - s_hi)
+  const float y0 = v0 * inv, y1 = v1 * inv;
+  const float m = q2.amax * inv;
+  const float ss = group16_sum(y0 * y0 + y1 * y1);
+  // max > 16 rms(rest) <=> 31 m^2 > 256 (ss - m^2) <=> 287 m^2 > 256 ss
+  r.flag = 287.0f * m * m > 256.0f * ss;
+  if (!r.flag) return r;
+  const float hi0 = __builtin_amdgcn_cvt_f32_fp8((int)q2.hi, 0), hi1 = __builtin_amdgcn_cvt_f32_fp8((int)q2.hi, 1);
+  // lo's codes scaled by 2^(s_hi - s_lo) in the hi domain
+  const float lsc = bits_f((uint32_t)(127 + (int)q2.s_lo - (int)q2.s_hi) << 23);
+  const float lo0 = __builtin_amdgcn_cvt_f32_fp8((int)q2.lo, 0) * lsc, lo1 = __builtin_amdgcn_cvt_f32_fp8((int)q2.lo, 1) * lsc;
+  const float d0 = (y0 - hi0) - lo0, d1 = (y1 - hi1) - lo1;
+  const float dmax = group16_max(fmaxf(fabsf(d0), fabsf(d1)));
+  const int ed = (int)((f_bits(dmax) >> 23) & 0xFF);
+  if (ed < 27) return r;  // nothing left worth a term (the block is exact in two terms)
+  // scale 2^(t - 127) relative to x: the residual's maximum maps into [128, 256)
+  const int t = (int)q2.s_hi + ed - 134;
+  const int st = t > 0 ? t : 0;
+  const float mm = bits_f((uint32_t)(127 + (int)q2.s_hi - st) << 23);  // 2^(s_hi - st)
+  r.th = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(d0 * mm, d1 * mm, 0, false) & 0xFFFFu;
+  r.s_th = (uint32_t)st;
   return r;
 }
 

@@ -94,6 +94,57 @@ __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tile
   return true;
 }
 
+__device__ __forceinline__ i32x8 cat8(const i32x4& x, const i32x4& y)
+{
+  return i32x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+__device__ __forceinline__ i32x8 cat8_ld(const uint8_t* p0, const uint8_t* p1)
+{
+  return cat8(*reinterpret_cast<const i32x4*>(p0), *reinterpret_cast<const i32x4*>(p1));
+}
+
+// ---------------------------------------------------------------- third term of x
+// The flag bytes of super-chunks 4g..4g+3 and 16+4g..16+4g+3 of X3 row `row` (null: an unused
+// slot, no flags), as lane (i, g) of a tile loads them for x3_mask.
+__device__ __forceinline__ uint2 x3_flags(const FwdArgs& a, const uint8_t* row, int lane)
+{
+  if (!row) return uint2{0u, 0u};
+  const int g = lane >> 4;
+  const uint8_t* f = row + (long long)at_nchunks(a.K) * 528;
+  return uint2{*reinterpret_cast<const uint32_t*>(f + 4 * g), *reinterpret_cast<const uint32_t*>(f + 16 + 4 * g)};
+}
+// Bit c of the result (uniform): some row slot of the tile has a third term in super-chunk c
+// (quant3_block16); the lanes' flag bytes (x3_flags) OR-ed over the wave.
+__device__ __forceinline__ uint32_t x3_mask(uint2 d, int lane)
+{
+  const int g = lane >> 4;
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) m |= (((d.x >> (8 * j)) & 1u) << (4 * g + j)) | (((d.y >> (8 * j)) & 1u) << (16 + 4 * g + j));
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) m |= (uint32_t)__shfl_xor((int)m, o, 64);
+  return __builtin_amdgcn_readfirstlane(m);
+}
+// X3 row of tile slot i (null when the slot is unused)
+__device__ __forceinline__ const uint8_t* x3_slot_row(const FwdArgs& a, int row0, int nrows, int i)
+{
+  return i < nrows ? a.x3 + (long long)a.row_token[row0 + i] * a.x3_row_bytes : nullptr;
+}
+// Whether X3 row `row` has a third term in super-chunk c (codes and scales are written only then)
+__device__ __forceinline__ bool x3_row_flag(const FwdArgs& a, const uint8_t* row, int c)
+{
+  return row && row[(long long)at_nchunks(a.K) * 528 + c] != 0;
+}
+
+// The third-term operand of lane (i, g) for MFMA q of super-chunk c in the one-tile block order
+// (MFMA q's logical block lb is block 4 lb + q): bytes 0-15 from block 4 (g / 2) + q, bytes 16-31
+// from block 8 + 4 (g / 2) + q, elements 16 (g % 2) .. of each; `row` is the X3 row.
+__device__ __forceinline__ i32x8 x3_operand(const uint8_t* row, int c, int q, int g)
+{
+  const uint8_t* p = row + c * 512 + (g >> 1) * 128 + q * 32 + (g & 1) * 16;
+  return cat8_ld(p, p + 256);
+}
+
 template <int Q>
 __device__ __forceinline__ void mfma_step(f32x4 (&acc)[4], const i32x8& ah, const i32x8& al,
                                           const i32x4 (&b)[4][4], const uint32_t (&sb)[4], int sah,
@@ -130,10 +181,7 @@ __device__ __forceinline__ void sanitize_if_damaged(i32x4 (&b)[4][4], uint32_t (
   if (__builtin_amdgcn_ballot_w64(d != 0u) != 0) sanitize(b, s);
 }
 
-__device__ __forceinline__ i32x8 cat8(const i32x4& x, const i32x4& y)
-{
-  return i32x8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-}
+
 
 // Where lane (i = lane % 16, g = lane / 16) of a one-tile work-group finds its A: piece u
 // (= (q * 2 + plane) * 2 + piece) of super-chunk c at base + c * kC + u * kU, its scale dwords
@@ -391,6 +439,28 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
   for (int grp = 0; grp < 4; ++grp) acc[grp] = f32x4{0.f, 0.f, 0.f, 0.f};
   float tw[4];  // kFwdDown: combine weights of this lane's output rows, requested with the first loads
 
+  // gate/up: the third term of x where the tile's rows have one (super-chunks of m3, rare); its
+  // operands come straight from the X3 rows of the slots' tokens
+  // The flag loads are issued here and reduced at the first chunk, after the pipeline's first
+  // loads: their latency hides behind those.
+  uint32_t m3 = 0;
+  uint2 f3 = uint2{0u, 0u};
+  const bool use3 = MODE == kFwdGateUp && a.x3 != nullptr && *(cint_ptr)a.x3_any != 0;
+  if (use3) f3 = x3_flags(a, x3_slot_row(a, w.row0, w.nrows, j), lane);
+  auto third_term = [&](int c, const i32x4 (&b)[4][4], const uint32_t (&sb)[4]) {
+    int l = lane;  // lane-derived values recomputed here: nothing of this stays live across the loop
+    asm volatile("" : "+v"(l));
+    const uint8_t* row = x3_slot_row(a, w.row0, w.nrows, l & 15);
+    const bool mine = x3_row_flag(a, row, c);  // this lane's row has a third term in chunk c
+    const uint32_t s3 = mine ? *reinterpret_cast<const uint32_t*>(row + (long long)nsc * 512 + c * 16 + 4 * g) : 0x7F7F7F7Fu;
+    static_for<4>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const i32x8 a3 = mine ? x3_operand(row, c, q, g) : i32x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) acc[grp] = mfma_f8f4<q, q>(a3, b[grp][q], acc[grp], (int)s3, (int)sb[grp]);
+    });
+  };
+
   auto load_b = [&](int c, i32x4 (&b)[4][4]) {
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp)
@@ -531,6 +601,8 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
     issue_scales(0);
     issue_a(0, 0);
     load_b_buf(1, b1);
+    // the flag loads were issued before the first chunk's loads, which the first step waits for
+    if (use3) m3 = x3_mask(f3, lane);
     for (int c = 0;;) {
       step(c, b0);
       if (++c >= nsc) break;
@@ -538,6 +610,25 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       if (++c >= nsc) break;
     }
     wait_vm0();  // (no copy is in flight past the last chunk; kept explicit for the epilogue)
+    // gate/up: the third term of the flagged super-chunks (rare), after the pipelined loop so that
+    // it adds nothing to the loop's registers; their weights are loaded again (checkpoint layout)
+    for (uint32_t mm = m3 & (nsc >= kX3Flags ? ~0u : ((1u << nsc) - 1u)); mm; mm &= mm - 1) {
+      const int c = __builtin_ctz(mm);
+      int l = lane;  // addresses rebuilt from the lane: nothing of this stays live across the loop
+      asm volatile("" : "+v"(l));
+      i32x4 b[4][4];
+      uint32_t sb[4];
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        const long long n = min(grp_row(grp) + (l & 15), a.R - 1);
+        sb[grp] = *reinterpret_cast<const uint32_t*>(grp_ws(grp) + n * nb + c * 16 + (l >> 4) * 4);
+        const uint8_t* wr0 = grp_wp(grp) + n * (a.K / 2) + c * 256 + (l >> 4) * 64;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[grp][q] = ldg16(wr0 + 16 * q);
+      }
+      sanitize(b, sb);
+      third_term(c, b, sb);
+    }
   } else {
     if (MODE == kFwdDown)
 #pragma unroll
@@ -580,6 +671,8 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       mfma_step<1>(acc, ah[1], al[1], b, sb, (int)s2.x, (int)s2.y);
       mfma_step<2>(acc, ah[2], al[2], b, sb, (int)s2.x, (int)s2.y);
       mfma_step<3>(acc, ah[3], al[3], b, sb, (int)s2.x, (int)s2.y);
+      if (use3 && c == 0) m3 = x3_mask(f3, lane);
+      if (c < kX3Flags && ((m3 >> c) & 1u)) third_term(c, b, sb);  // uniform
     }
   }
 
@@ -737,6 +830,17 @@ __device__ __forceinline__ void fwd_gemm_item(const FwdArgs& a, int expert, int 
     for (int tt = 0; tt < T; ++tt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) tw[tt][v] = a.row_w[w[tt].row0 + min(4 * g + v, w[tt].nrows - 1)];
+  // gate/up: third-term masks of the tiles (bit c: super-chunk c, rare) and their union
+  uint32_t m3[T], m3_any = 0;
+  const bool use3 = MODE == kFwdGateUp && a.x3 != nullptr && *(cint_ptr)a.x3_any != 0;
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt) {
+    m3[tt] = 0;
+    if (use3 && tt < ntl) {
+      m3[tt] = x3_mask(x3_flags(a, x3_slot_row(a, w[tt].row0, w[tt].nrows, lane & 15), lane), lane);
+      m3_any |= m3[tt];
+    }
+  }
 
   // One step per quarter s (super-chunk s / 4, MFMA q = s % 4): wait for its copies (the
   // next quarter's stay in flight), barrier, request quarter s + 2 into the buffer step s - 1
@@ -802,6 +906,23 @@ __device__ __forceinline__ void fwd_gemm_item(const FwdArgs& a, int expert, int 
       for (int cg = 0; cg < 4; ++cg) {
         acc[tt][cg] = mfma_f8f4<0, 0>(ah, b[cg], acc[tt][cg], sah, (int)sb[cg]);
         acc[tt][cg] = mfma_f8f4<0, 0>(al, b[cg], acc[tt][cg], sal, (int)sb[cg]);
+      }
+    }
+    // third-term MFMAs of flagged tiles (a slow path): in this block order MFMA q's logical
+    // block lb is block 4q + lb, so lane (i, g) takes blocks 4q + g / 2 and 4q + 2 + g / 2,
+    // elements 16 (g % 2) .., and the scale of block 4q + g
+    if (c < kX3Flags && ((m3_any >> c) & 1u)) {  // uniform
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) {
+        if (tt < ntl && ((m3[tt] >> c) & 1u)) {
+          const uint8_t* row = x3_slot_row(a, w[tt].row0, w[tt].nrows, jl);
+          const bool mine = x3_row_flag(a, row, c);
+          const uint8_t* p = mine ? row + c * 512 + q * 128 + (gl >> 1) * 32 + (gl & 1) * 16 : nullptr;
+          const i32x8 a3 = mine ? cat8_ld(p, p + 64) : i32x8{0, 0, 0, 0, 0, 0, 0, 0};
+          const int s3 = mine ? (int)row[(long long)nsc * 512 + c * 16 + 4 * q + gl] : 127;
+#pragma unroll
+          for (int cg = 0; cg < 4; ++cg) acc[tt][cg] = mfma_f8f4<0, 0>(a3, b[cg], acc[tt][cg], s3, (int)sb[cg]);
+        }
       }
     }
   }
@@ -933,6 +1054,35 @@ __device__ __forceinline__ void fwd_wide_item(const FwdArgs& a, int expert, int 
   // the previous item's epilogue stores complete here, in a wait the compiler sees: with stores
   // of unknown completion order pending it would wait for every load at the loop's head
   __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+  // gate/up: third-term masks of the tiles (m3[tt], bit c: super-chunk c, rare) and their union
+  uint32_t m3[T], m3_any = 0;
+  const bool use3 = MODE == kFwdGateUp && a.x3 != nullptr && *(cint_ptr)a.x3_any != 0;
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt) {
+    m3[tt] = 0;
+    if (use3 && tt < ntl) {
+      const cint_ptr tl = (cint_ptr)(a.tiles + t0 + tt);
+      m3[tt] = x3_mask(x3_flags(a, x3_slot_row(a, tl[1], tl[2], lane & 15), lane), lane);
+      m3_any |= m3[tt];
+    }
+  }
+  // tile tt's third-term MFMAs of quarter (c, q), operands straight from the X3 rows (a slow path)
+  auto third_term = [&](int c, auto Q, const i32x4 (&b)[4], const uint32_t (&sb)[4]) {
+    constexpr int q = decltype(Q)::value;
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) {
+      if (tt < ntl && ((m3[tt] >> c) & 1u)) {
+        const cint_ptr tl = (cint_ptr)(a.tiles + t0 + tt);
+        const uint8_t* row = x3_slot_row(a, tl[1], tl[2], lane & 15);
+        const bool mine = x3_row_flag(a, row, c);
+        const uint32_t s3 = mine ? *reinterpret_cast<const uint32_t*>(row + (long long)nsc * 512 + c * 16 + 4 * g) : 0x7F7F7F7Fu;
+        const i32x8 a3 = mine ? x3_operand(row, c, q, g) : i32x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int cg = 0; cg < 4; ++cg) acc[tt][cg] = mfma_f8f4<q, q>(a3, b[cg], acc[tt][cg], (int)s3, (int)sb[cg]);
+      }
+    }
+  };
+
   issue_sw(0);
   issue_sa(0);
   issue_a(0);
@@ -1009,6 +1159,7 @@ __device__ __forceinline__ void fwd_wide_item(const FwdArgs& a, int expert, int 
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (c < kX3Flags && ((m3_any >> c) & 1u)) third_term(c, Q, b, sb);  // uniform
     if (tail) load_b(s + 2, b);
   };
 
@@ -1059,6 +1210,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void fwd_wide_kernel(FwdArgs a)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = *(cint_ptr)a.n_wgroups;
+  if (ng == 0) return;  // no large buckets: the whole grid leaves without touching the queue
   const int nfb = (a.n_ct + kWgWaves - 1) / kWgWaves;
   const int total = ng * nfb;
   for (;;) {

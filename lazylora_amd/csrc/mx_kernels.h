@@ -46,6 +46,11 @@ struct FwdArgs {
   // lora_delta[row_token[p], 0:2R) before the GLU
   const int* row_token;
   const float* lora_delta;  // [tokens, 2R] fp32, or null
+  // kFwdGateUp: the third term of x (X3 layout, rows as a_rows, x3_row_bytes apart), or null, and
+  // the call-wide flag (non-zero: some block has a third term; zero: the products skip it all)
+  const uint8_t* x3;
+  long long x3_row_bytes;
+  const int* x3_any;
   // Bucket split (with a tile list and K a multiple of 512): the tiles of small buckets
   // (indices into `tiles`) take the one-row-tile work-groups; large-bucket groups of up to
   // kGroupTiles tiles ({expert, first tile, tiles, 0}) take work-groups that share each column
@@ -142,15 +147,19 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
 // large_only: only the tiles of large buckets (tiles[t].w != 0); the others are left untouched.
 // xt (with meta and row_map): the XT rows of x written by launch_quant_rows on the same stream;
 // when that call wrote them (meta says some bucket is small) the tiles are copied from them
-// instead of quantising x again (the same bytes).
+// instead of quantising x again (the same bytes). x3 (with row_map): where the tiles are quantised
+// from x, also the X3 rows of their tokens (launch_quant_rows writes them otherwise). x3_any
+// (with x3): set to non-zero when some block has a third term (it must be zero before the call).
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
                               const int* n_tiles, int max_tiles, const int* row_map, int large_only, const uint8_t* xt,
-                              const int* meta, uint8_t* out, hipStream_t s);
+                              const int* meta, uint8_t* out, uint8_t* x3, int* x3_any, hipStream_t s);
 // Rows 0 .. rows - 1 of x into the XT layout (xt_row_bytes(K) per row), followed by zero rows
-// up to xt_rows(rows): row `rows` is the all-zero row a tile's unused slots gather.
+// up to xt_rows(rows): row `rows` is the all-zero row a tile's unused slots gather. x3 (or null):
+// the third term of the flagged blocks in the X3 layout (x3_row_bytes(K) per row; rows < rows).
+// With meta saying every bucket is large the call writes nothing (launch_quant_tiles writes X3).
 inline long long xt_rows(int rows) { return ((long long)rows + 16) / 16 * 16; }
 hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, const int* meta, uint8_t* out,
-                             hipStream_t s);
+                             uint8_t* x3, int* x3_any, hipStream_t s);
 hipError_t launch_split_bf16(const float* x, long long ldx, int rows, int K, int Kpad, uint16_t* hi,
                              uint16_t* lo, hipStream_t s);
 hipError_t launch_dequant(void* out, int out_bf16, const uint8_t* packed, const uint8_t* scales, int K, int R,
@@ -159,8 +168,9 @@ hipError_t launch_dequant(void* out, int out_bf16, const uint8_t* packed, const 
 // the small-bucket tile indices, the large-bucket groups ({expert, first tile, tiles, 0}) of up to
 // kGroupTiles tiles and the same tiles again as wide groups of up to kWideGroupTiles (the full
 // ones first), meta = {tiles, flags (bit 0: an id outside [0, E)), small tiles, groups, wide
-// groups, full wide groups, -, -, then the work queues (2 ints each) of the wide-group launches of
-// the forward gate/up and down products, ...} (16 ints, all zeroed here), and the pair maps.
+// groups, full wide groups, third term present (set by the quantisers), -, then the work queues
+// (2 ints each) of the wide-group launches of the forward gate/up and down products, ...} (16
+// ints, all zeroed here), and the pair maps.
 hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, int N, int k, int E,
                         int* counts, int* offsets, int* cursor, int4* tiles, int* small_tiles, int4* groups,
                         int4* wgroups, int* meta, int* pair_token, float* pair_w, int* pair_of, hipStream_t s);

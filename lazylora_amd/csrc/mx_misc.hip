@@ -7,6 +7,25 @@ namespace mx {
 namespace {
 
 // ---------------------------------------------------------------- activation quantisation
+// The third term of one row's super-chunk c (c < kX3Flags) into its X3 row, by the 16 lanes of
+// the row: the codes and scales only when some block of the chunk is flagged (readers use them
+// only then), the chunk's flag byte always.
+MX_DEV void x3_store(uint8_t* x3r, int nsc, int c, int l16, const Quant3 (&q3)[kChunkBlocks], bool any3, int* x3_any)
+{
+  // the call-wide "some block has a third term" flag, which lets the products skip every
+  // third-term step: one atomic per wave that has a flagged row, by the first such lane
+  const uint64_t fl = __builtin_amdgcn_ballot_w64(any3 && l16 == 0);
+  if (fl != 0 && (int)(threadIdx.x & 63) == __builtin_ctzll(fl)) atomicOr(x3_any, 1);
+  if (any3) {
+#pragma unroll
+    for (int b = 0; b < kChunkBlocks; ++b) {
+      *reinterpret_cast<uint16_t*>(x3r + c * kChunk + b * kGroup + 2 * l16) = (uint16_t)q3[b].th;
+      if (l16 == 0) x3r[(long long)nsc * 512 + c * 16 + b] = (uint8_t)q3[b].s_th;
+    }
+  }
+  if (l16 == 0) x3r[(long long)nsc * 528 + c] = any3 ? 1 : 0;
+}
+
 // One work-group per (tile, super-chunk). Its 16 lane groups take the 16 row slots; each walks
 // the 16 blocks of the chunk, quantises them to two e4m3 terms and writes codes and scales into
 // an LDS copy of the chunk in the AT layout; the work-group then writes the chunk out with
@@ -16,7 +35,7 @@ template <bool BF16>
 __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long long ldx, int rows, int K,
                                                           const int4* tiles, const int* n_tiles, const int* row_map,
                                                           int large_only, const uint8_t* xt, const int* meta,
-                                                          uint8_t* out)
+                                                          uint8_t* out, uint8_t* x3, int* x3_any)
 {
   __shared__ __attribute__((aligned(16))) uint8_t chunk[kAtChunkBytes];
   const int nsc = at_nchunks(K);
@@ -77,6 +96,11 @@ __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long lo
       }
     }
   }
+  // x3 (the routed gate/up product when the token-major rows are skipped): also the third term
+  // of the slot's token row (a token in several tiles gets the same bytes each time)
+  const bool third = x3 && valid && c < kX3Flags;
+  Quant3 q3[kChunkBlocks];
+  bool any3 = false;
 #pragma unroll
   for (int b = 0; b < kChunkBlocks; ++b) {
     const int k = c * kChunk + b * kGroup + 2 * l16;
@@ -87,7 +111,10 @@ __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long lo
       chunk[at_scale_off(i, k, 0) - cbase] = (uint8_t)q.s_hi;
       chunk[at_scale_off(i, k, 1) - cbase] = (uint8_t)q.s_lo;
     }
+    q3[b] = third ? quant3_block16(v0[b], v1[b], q) : Quant3{0u, 127u, false};
+    any3 |= q3[b].flag;
   }
+  if (third) x3_store(x3 + src * x3_row_bytes(K), nsc, c, l16, q3, any3, x3_any);
   __syncthreads();
   uint8_t* dst = out + (long long)t * at_tile_bytes(K) + cbase;
   for (int o = threadIdx.x * 16; o < kAtChunkBytes; o += 256 * 16)
@@ -385,11 +412,13 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(float* grad_h, float* 
 // r0 .. r0 + 15 of x; rows at or past `rows` (at least the one that follows the last) get zeros,
 // the row a tile's unused slots read. Only the one-tile work-groups read this layout: with the
 // routing's meta (non-null), a layer whose buckets are all large (groups, no small tiles) skips it.
+// x3 (non-null): also the third term of the flagged blocks (quant3_block16) in the X3 layout,
+// written whether or not XT is skipped (every gate/up work-group reads it).
 template <bool BF16>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const void* x, long long ldx, int rows, int K,
-                                                         const int* meta, uint8_t* out)
+                                                         const int* meta, uint8_t* out, uint8_t* x3, int* x3_any)
 {
-  if (meta && meta[2] == 0 && meta[3] > 0) return;  // the whole grid
+  if (meta && meta[2] == 0 && meta[3] > 0) return;  // the whole grid (quant_tiles writes X3 then)
   __shared__ __attribute__((aligned(16))) uint8_t chunk[16 * kXtChunkBytes];
   const int nsc = at_nchunks(K);
   const int rg = (int)(blockIdx.x / nsc), c = (int)(blockIdx.x - (long long)rg * nsc);
@@ -416,6 +445,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* x, long lon
     }
   }
   uint8_t* mine = chunk + i * kXtChunkBytes;
+  const bool third = x3 && c < kX3Flags;
+  Quant3 q3[kChunkBlocks];
+  bool any3 = false;
 #pragma unroll
   for (int b = 0; b < kChunkBlocks; ++b) {
     const int k = c * kChunk + b * kGroup + 2 * l16;
@@ -426,7 +458,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* x, long lon
       mine[xt_scale_off(k, 0) - cbase] = (uint8_t)q.s_hi;
       mine[xt_scale_off(k, 1) - cbase] = (uint8_t)q.s_lo;
     }
+    q3[b] = third ? quant3_block16(v0[b], v1[b], q) : Quant3{0u, 127u, false};
+    any3 |= q3[b].flag;
   }
+  if (third) x3_store(x3 + (long long)row * x3_row_bytes(K), nsc, c, l16, q3, any3, x3_any);
   __syncthreads();
   // 16 rows x 66 sixteen-byte units, each row's chunk contiguous in memory
   const long long rb = xt_row_bytes(K);
@@ -446,29 +481,31 @@ __global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, long long n_word
 
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
                               const int* n_tiles, int max_tiles, const int* row_map, int large_only, const uint8_t* xt,
-                              const int* meta, uint8_t* out, hipStream_t s)
+                              const int* meta, uint8_t* out, uint8_t* x3, int* x3_any, hipStream_t s)
 {
   const long long groups = (long long)max_tiles * at_nchunks(K);  // (tile, super-chunk) work-groups
   if (groups == 0) return hipSuccess;
   if (xt && (!meta || !row_map || !tiles)) return hipErrorInvalidValue;
+  if (x3 && (!row_map || !x3_any)) return hipErrorInvalidValue;
   dim3 grid((unsigned)groups), block(256);
   if (x_bf16)
     hipLaunchKernelGGL(quant_tiles_kernel<true>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map,
-                       large_only, xt, meta, out);
+                       large_only, xt, meta, out, x3, x3_any);
   else
     hipLaunchKernelGGL(quant_tiles_kernel<false>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map,
-                       large_only, xt, meta, out);
+                       large_only, xt, meta, out, x3, x3_any);
   return hipGetLastError();
 }
 
 hipError_t launch_quant_rows(const void* x, int x_bf16, long long ldx, int rows, int K, const int* meta, uint8_t* out,
-                             hipStream_t s)
+                             uint8_t* x3, int* x3_any, hipStream_t s)
 {
   const long long groups = (long long)xt_rows(rows) / 16 * at_nchunks(K);  // (16 rows, super-chunk)
   if (groups == 0) return hipSuccess;
+  if (x3 && !x3_any) return hipErrorInvalidValue;
   dim3 grid((unsigned)groups), block(256);
-  if (x_bf16) hipLaunchKernelGGL(quant_rows_kernel<true>, grid, block, 0, s, x, ldx, rows, K, meta, out);
-  else hipLaunchKernelGGL(quant_rows_kernel<false>, grid, block, 0, s, x, ldx, rows, K, meta, out);
+  if (x_bf16) hipLaunchKernelGGL(quant_rows_kernel<true>, grid, block, 0, s, x, ldx, rows, K, meta, out, x3, x3_any);
+  else hipLaunchKernelGGL(quant_rows_kernel<false>, grid, block, 0, s, x, ldx, rows, K, meta, out, x3, x3_any);
   return hipGetLastError();
 }
 

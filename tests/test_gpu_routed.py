@@ -495,10 +495,12 @@ def test_outlier_activations_gemm(k, clib):
 
 def test_outlier_activations_routed_layer(k, clib):
     """A routed layer at the BASELINE expert shape (64 experts, 256 tokens, top-8) with outlier
-    channels in h, every token against the C restatement, forward and backward. The whole tensors
-    meet the stated bar (rel-L2 5e-3); a token whose gate/up are dominated by one x1e4 channel
-    carries that channel's two-term e4m3 rounding (up to 2^-8 relative) undiluted, so per token
-    the bar is 1e-2 (measured worst: ~4e-3 forward, ~7e-3 grad_h)."""
+    channels in h, every token against the C restatement, forward and backward, each token of out
+    and grad_h within the stated bar (rel-L2 5e-3). With two e4m3 terms a token whose gate/up are
+    dominated by one x1e4 channel carried that channel's rounding (up to 2^-8 relative) undiluted
+    (worst tokens 3.5e-3 out, 6.9e-3 grad_h, as a float64 simulation of the quantiser also gives);
+    blocks whose maximum exceeds 16x the rms of the rest now get a third term. grad_w also goes
+    through the down product's two-term activations: 1e-2 per token, as in the other layer tests."""
     case("routed layer with outlier channels: E=64, D=7168, F=2048, N=256, top-8")
     rng = np.random.default_rng(29)
     ex = oracle.random_experts(rng, 64, 7168, 2048, 117, 121)
@@ -508,11 +510,41 @@ def test_outlier_activations_routed_layer(k, clib):
     L = layer_of(ex)
     H, I, W, G = (torch.from_numpy(a).cuda() for a in (h, idx, w, g))
     out = k.routed_forward(H, I, W, L).cpu().numpy()
-    assert_all_tokens(out, clib.moe_forward(h, idx, w, ex), "outlier layer fwd", 1e-2)
+    assert_all_tokens(out, clib.moe_forward(h, idx, w, ex), "outlier layer fwd", 5e-3)
     gh, gw = k.routed_backward(H, I, W, L, G)
     gh_c, gw_c = clib.moe_backward(h, idx, w, ex, g)
-    assert_all_tokens(gh.cpu().numpy(), gh_c, "outlier layer grad_h", 1e-2)
-    assert_all_tokens(gw.cpu().numpy(), gw_c, "outlier layer grad_w", 2e-2)
+    assert_all_tokens(gh.cpu().numpy(), gh_c, "outlier layer grad_h", 5e-3)
+    assert_all_tokens(gw.cpu().numpy(), gw_c, "outlier layer grad_w", 1e-2)
+
+
+@pytest.mark.parametrize("fl", [False, True])
+def test_outlier_activations_large_buckets(k, clib, fl):
+    """Outlier channels in h with large buckets (150 and 70 rows of 243, top-1): the grouped
+    gate/up work-groups (with a forward layout, the wide groups) add the third term of flagged
+    blocks as the one-tile ones do; every token of out and grad_h within 5e-3 of the C restatement.
+    With one slot per token grad_w is one scalar per token, a 7168-term dot product whose relative
+    error is unbounded where the terms nearly cancel, so it is held to the bar as a whole tensor."""
+    case(f"outlier channels, large buckets: E=4, D=7168, F=2048, top-1, forward layout={fl}")
+    rng = np.random.default_rng(30 + fl)
+    E, D, F = 4, 7168, 2048
+    ex = oracle.random_experts(rng, E, D, F, 117, 121)
+    idx = np.concatenate([np.full(c, e) for e, c in enumerate([150, 70, 20, 3])]).astype(np.int64)
+    rng.shuffle(idx)
+    N = idx.size
+    idx = idx[:, None]
+    w = rng.uniform(0.5, 1.5, (N, 1)).astype(np.float32)
+    h = outlier_rows(rng, N, D)
+    g = rng.standard_normal((N, D)).astype(np.float32)
+    L = layer_of(ex)
+    if fl:
+        L.prepare_forward_layout()
+    H, I, W, G = (torch.from_numpy(a).cuda() for a in (h, idx, w, g))
+    out = k.routed_forward(H, I, W, L).cpu().numpy()
+    assert_all_tokens(out, clib.moe_forward(h, idx, w, ex), f"outlier large fwd fl={fl}", 5e-3)
+    gh, gw = k.routed_backward(H, I, W, L, G)
+    gh_c, gw_c = clib.moe_backward(h, idx, w, ex, g)
+    assert_all_tokens(gh.cpu().numpy(), gh_c, f"outlier large grad_h fl={fl}", 5e-3)
+    assert_close(gw.cpu().numpy(), gw_c, f"outlier large grad_w fl={fl}")
 
 
 @pytest.fixture(scope="module")
