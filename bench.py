@@ -485,6 +485,8 @@ def main():
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
 
     extra = {}
+    if lora is not None:
+        extra["lora_overhead"] = time_lora_ab(args, k, layer, H, I, W, G, ws, lora)
     zipf_inputs = None
     if not args.no_extra and layout.get("forward_layout"):
         # the same step reading only the checkpoint layout, for comparison (then the copy is rebuilt)
@@ -614,6 +616,36 @@ def time_forward(args, k, layer, H, I, W, ws, n_active):
     log(f"[bench] forward alone: {ms:.3f} ms ({n_active} active experts)")
     return {"ms_per_forward": ms, "tokens_per_s": N / (ms * 1e-3), "active_experts": n_active,
             "weight_GBps": EXPERT_BYTES * n_active / (ms * 1e-3) / 1e9}
+
+
+def time_lora_ab(args, k, layer, H, I, W, G, ws, lora, rounds=6):
+    """The step with the adapters against the same step without them, timed in alternating
+    rounds of args.steps steps in one process (so clock and thermal drift affect both alike):
+    median ms per step of each and the median of the paired differences."""
+    def run(lo):
+        k.routed_forward(H, I, W, layer, act=args.act, save_for_backward=True, workspace=ws, lora=lo)
+        k.routed_backward(H, I, W, layer, G, act=args.act, reuse_forward=True, workspace=ws, lora=lo)
+
+    stream = torch.cuda.current_stream()
+    on, off = [], []
+    for _ in range(rounds):
+        for lo, out in ((None, off), (lora, on)):
+            run(lo)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(args.steps):
+                run(lo)
+            end.record(stream)
+            torch.cuda.synchronize()
+            out.append(start.elapsed_time(end) / args.steps)
+    diff = [a - b for a, b in zip(on, off)]
+    res = {"rank": args.lora_rank, "rounds": rounds, "steps_per_round": args.steps,
+           "lora_off_ms": float(np.median(off)), "lora_on_ms": float(np.median(on)),
+           "overhead_ms": float(np.median(diff)), "overhead_ms_per_round": [round(d, 4) for d in diff]}
+    log(f"[bench] LoRA rank {args.lora_rank}: {res['lora_on_ms']:.3f} ms/step vs {res['lora_off_ms']:.3f} without "
+        f"(+{res['overhead_ms']:.3f} ms, median of {rounds} alternating rounds)")
+    return res
 
 
 def time_layer(args, k, layer, H, I, W, G, ws, lora, n_active, calibrate=False):

@@ -98,13 +98,104 @@ size_t at_bytes(long long tiles, int K) { return align_up((size_t)(tiles * mx::a
 
 long long pad32(long long v) { return (v + 31) / 32 * 32; }
 
+mx::LoraMat mat_f32(const void* p, long long ld) { return mx::LoraMat{mx::kLoraF32, p, nullptr, ld, 0, 0}; }
+mx::LoraFactor jmajor(const float* m, long long ld, float scale) { return mx::LoraFactor{m, ld, 0, scale}; }
+mx::LoraFactor kmajor(const float* m, long long ld, float scale) { return mx::LoraFactor{m, ld, 1, scale}; }
+
+// Row-dot job over nseg segments of K columns (the second at source column koff1).
+mx::LoraPassJob rowdot_job(const mx::LoraMat& src, int rows, const int* rows_dev, int nseg, int K, int koff1, int r,
+                           int nfac, mx::LoraFactor f0, mx::LoraFactor f1)
+{
+  mx::LoraPassJob j = {};
+  j.type = mx::kLoraRowDot; j.src = src; j.rows = rows; j.rows_dev = rows_dev;
+  j.nseg = nseg; j.K = K; j.koff[1] = koff1; j.r = r; j.nfac = nfac; j.f[0] = f0; j.f[1] = f1;
+  return j;
+}
+
+// Outer-product job: m coefficients per segment, from coef columns coff_s (the second at coff1).
+// Pair sources (row_of = pair_of) are walked over the (token, slot) pairs, k slots per token.
+mx::LoraPassJob outer_job(const mx::LoraMat& src, int rows, int nseg, int K, int koff1, int r, const float* coef,
+                          long long ldc, int coff1, const int* row_of, int k, const float* row_w, int m)
+{
+  mx::LoraPassJob j = {};
+  j.type = mx::kLoraOuter; j.src = src; j.rows = rows;
+  j.nseg = nseg; j.K = K; j.koff[1] = koff1; j.r = r;
+  j.coef = coef; j.ldc = ldc; j.coff[1] = coff1; j.row_of = row_of; j.k = k; j.row_w = row_w; j.m = m;
+  return j;
+}
+
+// The passes of the LoRA stages (pointers may be null when only sizing the partials):
+// adapter inputs U = [A_gate x | A_up x] (pass_in); v = A_down act per pair (pass_mid);
+// q = B_down^T g per token (pass_q); dh = [B_gate^T d_gate | B_up^T d_up] per pair with the B_gate,
+// B_up, A_down and B_down gradients (pass_dx); the A_gate / A_up gradients (pass_grads).
+struct LoraPtrs {
+  mx::LoraMat x, g, act, d;
+  const float* m[6];
+  const int* n_valid;
+  const int* pair_of;
+  const float* topk_w;
+  int k;
+  const float *u, *q, *vsum, *dsum;
+};
+
+int lora_pass_jobs(int stage, const LoraPtrs& p, int N, long long P, int D, int F, int r, mx::LoraPassJob* j)
+{
+  switch (stage) {
+    case 0:
+      j[0] = rowdot_job(p.x, N, nullptr, 1, D, 0, r, 2, jmajor(p.m[0], D, 1.f), jmajor(p.m[2], D, 1.f));
+      return 1;
+    case 1:
+      j[0] = rowdot_job(p.act, (int)P, p.n_valid, 1, F, 0, r, 1, jmajor(p.m[4], F, 1.f), jmajor(p.m[4], F, 1.f));
+      return 1;
+    case 2:
+      j[0] = rowdot_job(p.g, N, nullptr, 1, D, 0, r, 1, kmajor(p.m[5], r, 1.f), kmajor(p.m[5], r, 1.f));
+      return 1;
+    case 3: {
+      int n = 0;
+      j[n] = outer_job(p.d, (int)P, 2, F, F, r, p.u, 2 * r, r, p.pair_of, p.k, nullptr, r);
+      j[n].f[0] = kmajor(p.m[1], r, 1.f);
+      j[n].f[1] = kmajor(p.m[3], r, 1.f);
+      if (r <= 16) {
+        j[n++].type = mx::kLoraRowOuter;  // with the row dots dh = [B_gate^T d_gate | B_up^T d_up]
+      } else {
+        ++n;
+        j[n++] = rowdot_job(p.d, (int)P, p.n_valid, 2, F, F, r, 1, kmajor(p.m[1], r, 1.f), kmajor(p.m[3], r, 1.f));
+      }
+      j[n++] = outer_job(p.act, (int)P, 1, F, 0, r, p.q, r, 0, p.pair_of, p.k, p.topk_w, r);
+      j[n++] = outer_job(p.g, N, 1, D, 0, r, p.vsum, r, 0, nullptr, 1, nullptr, r);
+      return n;
+    }
+    default:
+      j[0] = outer_job(p.x, N, 1, D, 0, r, p.dsum, 2 * r, 0, nullptr, 1, nullptr, 2 * r);
+      return 1;
+  }
+}
+constexpr int kLoraStages = 5;
+
+// Partial floats of the largest LoRA pass over every rank.
+size_t lora_part_floats(int N, long long P, int D, int F)
+{
+  LoraPtrs p = {};
+  p.x = mat_f32(nullptr, D); p.g = mat_f32(nullptr, D);
+  p.act = mx::LoraMat{mx::kLoraGLU, nullptr, nullptr, 2LL * F, F, 0};
+  p.d = mx::LoraMat{mx::kLoraHiLo, nullptr, nullptr, 2LL * F, 0, 0};
+  size_t best = 0;
+  for (int r = 1; r <= mx::kLoraMaxRank; ++r)
+    for (int st = 0; st < kLoraStages; ++st) {
+      mx::LoraPassJob j[4];
+      const int n = lora_pass_jobs(st, p, N, P, D, F, r, j);
+      best = std::max(best, mx::lora_pass_partial_floats(j, n));
+    }
+  return best;
+}
+
 // Routed-layer workspace: one layout for forward and backward so the backward can reuse
 // what the forward left behind.
 struct MoeLayout {
   size_t meta, counts, offsets, cursor, tiles, small_tiles, groups, wgroups, pair_token, pair_w, pair_of;
   size_t at_x, xt_x, x3_x, at_act;
   size_t saved, ypair, g_hi, g_lo, d_hi, d_lo, gw_part;
-  size_t l_u, l_delta, l_v, l_vsum, l_q, l_rq, l_dh, l_dsum, l_part;  // LoRA (rank <= kLoraMaxRank)
+  size_t l_u, l_delta, l_vsum, l_q, l_rq, l_dsum, l_part;  // LoRA (rank <= kLoraMaxRank)
   size_t end;
   int max_tiles, n_ct_bwd;
 };
@@ -141,19 +232,11 @@ MoeLayout moe_layout(int N, int k, int E, int D, int F)
   const size_t R = mx::kLoraMaxRank;
   L.l_u = o; o = align_up(o + sizeof(float) * (size_t)N * 2 * R);
   L.l_delta = o; o = align_up(o + sizeof(float) * (size_t)N * 2 * F);
-  L.l_v = o; o = align_up(o + sizeof(float) * (size_t)P * R);
   L.l_vsum = o; o = align_up(o + sizeof(float) * (size_t)N * R);
   L.l_q = o; o = align_up(o + sizeof(float) * (size_t)N * R);
   L.l_rq = o; o = align_up(o + sizeof(float) * (size_t)N * F);
-  L.l_dh = o; o = align_up(o + sizeof(float) * (size_t)P * 2 * R);
   L.l_dsum = o; o = align_up(o + sizeof(float) * (size_t)N * 2 * R);
-  size_t part = mx::lora_outer_partial_floats(N, 2 * (int)R, D);
-  part = std::max(part, mx::lora_outer_partial_floats((int)P, (int)R, F));
-  for (int nseg = 1; nseg <= 2; ++nseg) {
-    part = std::max(part, mx::lora_rowdot_partial_floats(N, D, nseg, (int)R));
-    part = std::max(part, mx::lora_rowdot_partial_floats((int)P, F, nseg, (int)R));
-  }
-  L.l_part = o; o = align_up(o + sizeof(float) * part);
+  L.l_part = o; o = align_up(o + sizeof(float) * lora_part_floats(N, P, D, F));
   L.end = o;
   return L;
 }
@@ -218,6 +301,63 @@ int check_lora(const float* const* lora, const float* scaling, int rank, Lora& l
   return MXFP4_OK;
 }
 
+// Device pointers of the LoRA stages: sources, adapters, routing and coefficient buffers.
+LoraPtrs lora_ptrs(const Lora& lo, const void* h, int h_dtype, const float* topk_w, int k, const float* grad_out,
+                   void* ws, const MoeLayout& L, int E, int D, int F, int act_kind)
+{
+  LoraPtrs p = {};
+  p.x = mx::LoraMat{h_dtype == MXFP4_BF16 ? mx::kLoraBF16 : mx::kLoraF32, h, nullptr, D, 0, 0};
+  p.g = mat_f32(grad_out, D);
+  p.act = mx::LoraMat{mx::kLoraGLU, at<float>(ws, L.saved), nullptr, 2LL * F, F, act_kind};
+  p.d = mx::LoraMat{mx::kLoraHiLo, at<uint16_t>(ws, L.d_hi), at<uint16_t>(ws, L.d_lo), 2LL * F, 0, 0};
+  for (int i = 0; i < 6; ++i) p.m[i] = lo.m[i];
+  p.n_valid = at<int>(ws, L.offsets) + E;
+  p.pair_of = at<int>(ws, L.pair_of);
+  p.topk_w = topk_w;
+  p.k = k;
+  p.u = at<float>(ws, L.l_u);
+  p.q = at<float>(ws, L.l_q);
+  p.vsum = at<float>(ws, L.l_vsum);
+  p.dsum = at<float>(ws, L.l_dsum);
+  return p;
+}
+
+hipError_t run_lora_pass(int stage, const LoraPtrs& p, int N, long long P, int D, int F, int r, void* ws,
+                         const MoeLayout& L, mx::LoraPartial* parts, hipStream_t s)
+{
+  mx::LoraPassJob j[4];
+  const int n = lora_pass_jobs(stage, p, N, P, D, F, r, j);
+  return mx::launch_lora_pass(j, n, at<float>(ws, L.l_part), parts, s);
+}
+
+// Finish job turning row-dot partials into coefficient rows (see launch_lora_finish).
+mx::LoraFinishJob coef_job(const mx::LoraPartial& part, int prow, int m, int r, float s0, float s1, int ntok,
+                           float* out)
+{
+  mx::LoraFinishJob f = {};
+  f.type = mx::kLoraFinCoef; f.part = part; f.prow = prow; f.m = m; f.r = r;
+  f.scale[0] = s0; f.scale[1] = s1; f.ntok = ntok; f.out = out;
+  return f;
+}
+
+// Finish job writing an outer-product gradient.
+mx::LoraFinishJob grad_job(const mx::LoraPartial& part, int om, int Ctot, int Kseg, const mx::LoraOuterDst& dst)
+{
+  mx::LoraFinishJob f = {};
+  f.type = mx::kLoraFinOuter; f.part = part; f.om = om; f.Ctot = Ctot; f.Kseg = Kseg; f.dst = dst;
+  return f;
+}
+
+mx::LoraOuterDst dst_of(float* p0, long long ld0, int km0, float s0, float* p1, long long ld1, int km1, float s1,
+                        int split_j)
+{
+  mx::LoraOuterDst d = {};
+  d.p[0] = p0; d.ld[0] = ld0; d.kmajor[0] = km0; d.scale[0] = s0;
+  d.p[1] = p1 ? p1 : p0; d.ld[1] = p1 ? ld1 : ld0; d.kmajor[1] = p1 ? km1 : km0; d.scale[1] = p1 ? s1 : s0;
+  d.split_j = split_j;
+  return d;
+}
+
 // Forward-layout copies {W1, W3, W2} (null array or entries: that product reads the checkpoint
 // layout). An entry needs its matrix's K (D for W1 and W3, F for W2) to be a multiple of 512.
 int check_forward_layout(const uint8_t* const* fl, int D, int F)
@@ -232,14 +372,10 @@ int check_forward_layout(const uint8_t* const* fl, int D, int F)
   return MXFP4_OK;
 }
 
-mx::LoraMat mat_f32(const void* p, long long ld) { return mx::LoraMat{mx::kLoraF32, p, nullptr, ld, 0, 0}; }
-mx::LoraFactor jmajor(const float* m, long long ld, float scale) { return mx::LoraFactor{m, ld, 0, scale}; }
-mx::LoraFactor kmajor(const float* m, long long ld, float scale) { return mx::LoraFactor{m, ld, 1, scale}; }
-
 // Routing + quantised x + gate/up (+GLU) into the workspace. With LoRA also the per-token
 // adapter inputs U = [A_gate x | A_up x], their gate/up deltas (added in the product's
-// epilogue), v = A_down act per pair and V = sum over a token's slots of w * v; gate|up are
-// then always saved, since v and the backward read them.
+// epilogue) and V = sum over a token's slots of w * A_down act; gate|up are then always saved,
+// since V and the backward read them.
 int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const float* w, int N, int k,
               const uint8_t* const* wts, const uint8_t* const* fl, int E, int D, int F, int act_kind, bool save,
               const Lora& lo, void* ws, const MoeLayout& L, hipStream_t s)
@@ -296,31 +432,27 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
   a.save = (save || lo.r) ? at<float>(ws, L.saved) : nullptr;
   a.act_kind = act_kind;
   const int r = lo.r;
-  if (r) {
-    const mx::LoraMat x{h_dtype == MXFP4_BF16 ? mx::kLoraBF16 : mx::kLoraF32, h, nullptr, D, 0, 0};
-    const mx::LoraFactor fa[2] = {jmajor(lo.m[0], D, 1.f), jmajor(lo.m[2], D, 1.f)};
-    const int koff[2] = {0, 0};
-    MX_TRY(mx::launch_lora_rowdot(x, N, nullptr, D, r, 2, fa, koff, at<float>(ws, L.l_part), at<float>(ws, L.l_u), s),
-           "LoRA: A x");
+  LoraPtrs lp = {};
+  mx::LoraPartial parts[4];
+  if (r) {  // U = [A_gate x | A_up x] per token, expanded into the gate/up deltas s B U
+    lp = lora_ptrs(lo, h, h_dtype, w, k, nullptr, ws, L, E, D, F, act_kind);
+    MX_TRY(run_lora_pass(0, lp, N, P, D, F, r, ws, L, parts, s), "LoRA: A x");
     const mx::LoraFactor fb[2] = {kmajor(lo.m[1], r, lo.sg), kmajor(lo.m[3], r, lo.su)};
-    const int coff[2] = {0, r}, col0[2] = {0, F}, ncol[2] = {F, F};
-    MX_TRY(mx::launch_lora_expand(at<float>(ws, L.l_u), 2 * r, N, r, 2, fb, coff, col0, ncol,
-                                  at<float>(ws, L.l_delta), 2LL * F, 2 * F, 0, s),
+    const int coff[2] = {0, r};
+    const float one[2] = {1.f, 1.f};
+    MX_TRY(mx::launch_lora_expand(at<float>(ws, L.l_u), 2 * r, N, r, at<float>(ws, L.l_delta), 2LL * F, 2 * F, F, fb,
+                                  coff, s, &parts[0], one),
            "LoRA: gate/up deltas");
     a.lora_delta = at<float>(ws, L.l_delta);
     MX_PHASE("lora_in", s);
   }
   MX_TRY(mx::launch_fwd(a, mx::kFwdGateUp, L.max_tiles, s), "gate/up product");
   MX_PHASE("fwd_gateup", s);
-  if (r) {
-    const mx::LoraMat act{mx::kLoraGLU, at<float>(ws, L.saved), nullptr, 2LL * F, F, act_kind};
-    const mx::LoraFactor fd = jmajor(lo.m[4], F, 1.f);
-    const int koff = 0;
-    MX_TRY(mx::launch_lora_rowdot(act, (int)P, at<int>(ws, L.offsets) + E, F, r, 1, &fd, &koff, at<float>(ws, L.l_part),
-                                  at<float>(ws, L.l_v), s),
-           "LoRA: A_down act");
-    MX_TRY(mx::launch_lora_slot_sum(at<float>(ws, L.l_v), r, at<int>(ws, L.pair_of), w, N, k, at<float>(ws, L.l_vsum), s),
-           "LoRA: slot sum");
+  if (r) {  // V = sum over a token's slots of w * A_down act
+    MX_TRY(run_lora_pass(1, lp, N, P, D, F, r, ws, L, parts, s), "LoRA: A_down act");
+    mx::LoraFinishJob f = coef_job(parts[0], (int)P, r, r, 1.f, 1.f, N, at<float>(ws, L.l_vsum));
+    f.pair_of = at<int>(ws, L.pair_of); f.topk_w = w; f.k = k;
+    MX_TRY(mx::launch_lora_finish(&f, 1, s), "LoRA: slot sum");
     MX_PHASE("lora_mid", s);
   }
   return MXFP4_OK;
@@ -553,17 +685,16 @@ int mxfp4_moe_forward_fl(float* out, const void* h, int h_dtype, const void* top
   a.wcounter = at<int>(workspace, L.meta) + 10;
   MX_TRY(mx::launch_fwd(a, mx::kFwdDown, L.max_tiles, stream), "moe_forward: down product");
   MX_PHASE("fwd_down", stream);
-  MX_TRY(mx::launch_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D, stream),
-         "moe_forward: combine");
-  MX_PHASE("fwd_combine", stream);
-  if (lo.r) {  // out += s_down B_down V, V = sum over the token's slots of w A_down act
+  if (lo.r) {  // out = combine + s_down B_down V, V = sum over the token's slots of w A_down act
     const mx::LoraFactor fb = kmajor(lo.m[5], lo.r, lo.sd);
-    const int coff = 0, col0 = 0, ncol = D;
-    MX_TRY(mx::launch_lora_expand(at<float>(workspace, L.l_vsum), lo.r, N, lo.r, 1, &fb, &coff, &col0, &ncol, out, D,
-                                  D, 1, stream),
-           "moe_forward: LoRA down");
-    MX_PHASE("lora_out", stream);
+    MX_TRY(mx::launch_lora_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D,
+                                   at<float>(workspace, L.l_vsum), lo.r, 1, &fb, nullptr, nullptr, 0, stream),
+           "moe_forward: combine");
+  } else {
+    MX_TRY(mx::launch_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D, stream),
+           "moe_forward: combine");
   }
+  MX_PHASE("fwd_combine", stream);
   return MXFP4_OK;
 }
 
@@ -633,16 +764,17 @@ int mxfp4_moe_backward_fl(float* grad_h, float* grad_w, const float* grad_out, c
          "moe_backward: split grad_out");
   MX_PHASE("split_grad", stream);
   const int r = lo.r;
+  const long long P = (long long)N * k;
+  LoraPtrs lp = {};
+  mx::LoraPartial parts[4];
   if (r) {  // q = s_down B_down^T g per token, and its expansion A_down^T q for the W2 epilogue
-    const mx::LoraFactor fb = kmajor(lo.m[5], r, lo.sd);
-    const int koff = 0;
-    MX_TRY(mx::launch_lora_rowdot(mat_f32(grad_out, D), N, nullptr, D, r, 1, &fb, &koff,
-                                  at<float>(workspace, L.l_part), at<float>(workspace, L.l_q), stream),
-           "moe_backward: LoRA B_down^T g");
+    lp = lora_ptrs(lo, h, h_dtype, topk_w, k, grad_out, workspace, L, E, D, F, act_kind);
+    MX_TRY(run_lora_pass(2, lp, N, P, D, F, r, workspace, L, parts, stream), "moe_backward: LoRA B_down^T g");
     const mx::LoraFactor fa = jmajor(lo.m[4], F, 1.f);
-    const int coff = 0, col0 = 0, ncol = F;
-    MX_TRY(mx::launch_lora_expand(at<float>(workspace, L.l_q), r, N, r, 1, &fa, &coff, &col0, &ncol,
-                                  at<float>(workspace, L.l_rq), F, F, 0, stream),
+    const int coff = 0;
+    const float sd[2] = {lo.sd, lo.sd};
+    MX_TRY(mx::launch_lora_expand(at<float>(workspace, L.l_q), r, N, r, at<float>(workspace, L.l_rq), F, F, 0, &fa,
+                                  &coff, stream, &parts[0], sd),
            "moe_backward: LoRA A_down^T q");
     MX_PHASE("lora_q", stream);
   }
@@ -664,6 +796,25 @@ int mxfp4_moe_backward_fl(float* grad_h, float* grad_w, const float* grad_out, c
   b.lora_rq = r ? at<float>(workspace, L.l_rq) : nullptr;
   MX_TRY(mx::launch_bwd(b, mx::kBwdDownT, L.max_tiles, stream), "moe_backward: W2 transposed product");
   MX_PHASE("bwd_down_t", stream);
+  if (r) {
+    // one pass over d = [d_gate | d_up], act and g: dh = [s_gate B_gate^T d_gate | s_up B_up^T d_up]
+    // per pair, summed over each token's slots into Dsum, and the B_gate, B_up, A_down and B_down
+    // gradients (lora_layer.py:178-226, summed over the experts)
+    MX_TRY(run_lora_pass(3, lp, N, P, D, F, r, workspace, L, parts, stream), "moe_backward: LoRA pass over d");
+    mx::LoraFinishJob f[4];
+    const int o = r <= 16 ? 0 : 1;  // rank above 16: the row dots are a job of their own
+    const mx::LoraPartial dh = r <= 16 ? mx::LoraPartial{parts[0].p2, parts[0].count2, nullptr, 0} : parts[1];
+    f[0] = coef_job(dh, (int)P, 2 * r, r, lo.sg, lo.su, N, at<float>(workspace, L.l_dsum));
+    f[0].pair_of = at<int>(workspace, L.pair_of); f[0].k = k;
+    // B_gate, B_up: s * sum over pairs of d_gate (d_up) (x) A_gate x (A_up x) of the pair's token
+    f[1] = grad_job(parts[0], r, 2 * F, F, dst_of(lora_grads[1], r, 1, lo.sg, lora_grads[3], r, 1, lo.su, 0));
+    // A_down: sum over pairs of w q(token) (x) act
+    f[2] = grad_job(parts[1 + o], r, F, 0, dst_of(lora_grads[4], F, 0, 1.f, nullptr, 0, 0, 0.f, 0));
+    // B_down: s * sum over tokens of g (x) V
+    f[3] = grad_job(parts[2 + o], r, D, 0, dst_of(lora_grads[5], r, 1, lo.sd, nullptr, 0, 0, 0.f, 0));
+    MX_TRY(mx::launch_lora_finish(f, 4, stream), "moe_backward: LoRA slot sums and B/A_down gradients");
+    MX_PHASE("lora_dx", stream);
+  }
 
   mx::BwdArgs c = {};
   c.wp0 = w1p; c.ws0 = w1s; c.wp1 = w3p; c.ws1 = w3s;
@@ -677,62 +828,23 @@ int mxfp4_moe_backward_fl(float* grad_h, float* grad_w, const float* grad_out, c
   set_buckets(c, workspace, L);
   MX_TRY(mx::launch_bwd(c, mx::kBwdGateUpT, L.max_tiles, stream), "moe_backward: W1|W3 transposed product");
   MX_PHASE("bwd_gateup_t", stream);
-  MX_TRY(mx::launch_combine_bwd(grad_h, grad_w, at<float>(workspace, L.ypair), D, at<float>(workspace, L.gw_part),
-                                L.n_ct_bwd, at<int>(workspace, L.pair_of), N, k, D, stream),
-         "moe_backward: combine");
-  MX_PHASE("bwd_combine", stream);
-  if (r) {
-    float* ws_f = at<float>(workspace, L.l_part);
-    const long long P = (long long)N * k;
-    const int* n_valid = at<int>(workspace, L.offsets) + E;
-    // dh = [s_gate B_gate^T d_gate | s_up B_up^T d_up] per pair, summed over each token's slots
-    const mx::LoraMat dmat{mx::kLoraHiLo, at<uint16_t>(workspace, L.d_hi), at<uint16_t>(workspace, L.d_lo), 2LL * F, 0,
-                           0};
-    const mx::LoraFactor fb[2] = {kmajor(lo.m[1], r, lo.sg), kmajor(lo.m[3], r, lo.su)};
-    const int koff[2] = {0, F};
-    MX_TRY(mx::launch_lora_rowdot(dmat, (int)P, n_valid, F, r, 2, fb, koff, ws_f, at<float>(workspace, L.l_dh), stream),
-           "moe_backward: LoRA B^T d");
-    MX_TRY(mx::launch_lora_slot_sum(at<float>(workspace, L.l_dh), 2 * r, at<int>(workspace, L.pair_of), nullptr, N, k,
-                                    at<float>(workspace, L.l_dsum), stream),
-           "moe_backward: LoRA slot sum");
-    // grad_h += A_gate^T Dg + A_up^T Du
+  if (r) {  // grad_h = combine + A_gate^T Dsum_gate + A_up^T Dsum_up
     const mx::LoraFactor fa[2] = {jmajor(lo.m[0], D, 1.f), jmajor(lo.m[2], D, 1.f)};
-    const int coff[2] = {0, r}, col0[2] = {0, 0}, ncol[2] = {D, D};
-    MX_TRY(mx::launch_lora_expand(at<float>(workspace, L.l_dsum), 2 * r, N, r, 2, fa, coff, col0, ncol, grad_h, D, D,
-                                  1, stream),
-           "moe_backward: LoRA grad_h");
-    MX_PHASE("lora_dx", stream);
-    // adapter gradients (lora_layer.py:178-226, summed over the experts)
-    const mx::LoraMat x{h_dtype == MXFP4_BF16 ? mx::kLoraBF16 : mx::kLoraF32, h, nullptr, D, 0, 0};
-    const mx::LoraMat act{mx::kLoraGLU, at<float>(workspace, L.saved), nullptr, 2LL * F, F, act_kind};
-    mx::LoraOuterDst d = {};
-    // A_gate / A_up: sum over tokens of [Dg | Du] (x) x
-    d.p[0] = lora_grads[0]; d.ld[0] = D; d.kmajor[0] = 0; d.scale[0] = 1.f;
-    d.p[1] = lora_grads[2]; d.ld[1] = D; d.kmajor[1] = 0; d.scale[1] = 1.f;
-    d.split_j = r;
-    MX_TRY(mx::launch_lora_outer(x, 0, N, nullptr, k, nullptr, at<float>(workspace, L.l_dsum), 2 * r, 0, 2 * r, D, ws_f,
-                                 d, stream),
-           "moe_backward: LoRA grad A_gate/A_up");
-    // B_gate, B_up: s * sum over pairs of d_gate (d_up) (x) A_gate x (A_up x) of the pair's token
-    for (int u = 0; u < 2; ++u) {
-      d = {};
-      d.p[0] = lora_grads[1 + 2 * u]; d.ld[0] = r; d.kmajor[0] = 1; d.scale[0] = u ? lo.su : lo.sg;
-      MX_TRY(mx::launch_lora_outer(dmat, u * F, (int)P, at<int>(workspace, L.pair_of), k, nullptr,
-                                   at<float>(workspace, L.l_u), 2 * r, u * r, r, F, ws_f, d, stream),
-             "moe_backward: LoRA grad B_gate/B_up");
-    }
-    // A_down: sum over pairs of w q(token) (x) act
-    d = {};
-    d.p[0] = lora_grads[4]; d.ld[0] = F; d.kmajor[0] = 0; d.scale[0] = 1.f;
-    MX_TRY(mx::launch_lora_outer(act, 0, (int)P, at<int>(workspace, L.pair_of), k, topk_w, at<float>(workspace, L.l_q),
-                                 r, 0, r, F, ws_f, d, stream),
-           "moe_backward: LoRA grad A_down");
-    // B_down: s * sum over tokens of g (x) V
-    d = {};
-    d.p[0] = lora_grads[5]; d.ld[0] = r; d.kmajor[0] = 1; d.scale[0] = lo.sd;
-    MX_TRY(mx::launch_lora_outer(mat_f32(grad_out, D), 0, N, nullptr, k, nullptr, at<float>(workspace, L.l_vsum), r, 0,
-                                 r, D, ws_f, d, stream),
-           "moe_backward: LoRA grad B_down");
+    MX_TRY(mx::launch_lora_combine(grad_h, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D,
+                                   at<float>(workspace, L.l_dsum), r, 2, fa, grad_w, at<float>(workspace, L.gw_part),
+                                   L.n_ct_bwd, stream),
+           "moe_backward: combine");
+  } else {
+    MX_TRY(mx::launch_combine_bwd(grad_h, grad_w, at<float>(workspace, L.ypair), D, at<float>(workspace, L.gw_part),
+                                  L.n_ct_bwd, at<int>(workspace, L.pair_of), N, k, D, stream),
+           "moe_backward: combine");
+  }
+  MX_PHASE("bwd_combine", stream);
+  if (r) {  // A_gate / A_up: sum over tokens of [Dsum_gate | Dsum_up] (x) x
+    MX_TRY(run_lora_pass(4, lp, N, P, D, F, r, workspace, L, parts, stream), "moe_backward: LoRA pass over x");
+    const mx::LoraFinishJob f =
+        grad_job(parts[0], 2 * r, D, 0, dst_of(lora_grads[0], D, 0, 1.f, lora_grads[2], D, 0, 1.f, r));
+    MX_TRY(mx::launch_lora_finish(&f, 1, stream), "moe_backward: LoRA grad A_gate/A_up");
     MX_PHASE("lora_grads", stream);
   }
   return MXFP4_OK;

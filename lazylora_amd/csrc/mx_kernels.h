@@ -206,26 +206,8 @@ struct LoraFactor {
 
 constexpr int kLoraMaxRank = 32;
 
-// out[row, s*r + j] = f_s.scale * sum_{k < K} src(row, koff_s + k) * f_s(j, k), segments s < nseg
-// (nseg <= 2), rows < rows; rows at or past *rows_dev (when given) get 0. K is a multiple of 32.
-// `partial` holds lora_rowdot_partial_floats(rows, K, nseg, r) floats of scratch.
-size_t lora_rowdot_partial_floats(int rows, int K, int nseg, int r);
-hipError_t launch_lora_rowdot(const LoraMat& src, int rows, const int* rows_dev, int K, int r, int nseg,
-                              const LoraFactor* f, const int* koff, float* partial, float* out, hipStream_t s);
-// out[t, :] (+)= sum over segments s of f_s.scale * sum_{j < r} coef[t, coff_s + j] * f_s(j, c - col0_s)
-// for the columns c in [col0_s, col0_s + ncol_s); Cout columns in all.
-hipError_t launch_lora_expand(const float* coef, int ldc, int rows, int r, int nseg, const LoraFactor* f,
-                              const int* coff, const int* col0, const int* ncol, float* out, long long ldo, int Cout,
-                              int accumulate, hipStream_t s);
-// out[t, j] = sum over the token's slots in slot order of (topk_w[t, s] if weighted) * src[pair_of[t, s], j]
-hipError_t launch_lora_slot_sum(const float* src, int m, const int* pair_of, const float* topk_w, int N, int k,
-                                float* out, hipStream_t s);
-// Column-wise outer-product reduction: G[j, c] = sum over rows q of coef(q, j) * src(row(q), c_off + c),
-// j < m (<= 64), c < C (a multiple of 4), then written through `dst`. Rows q are tokens
-// (pair_of == null: row = q, coef row q) or the (token, slot) pairs in token order (row =
-// pair_of[q], skipped when negative; coef row = q / k, times topk_w[q] when weighted); coef
-// columns start at coff. The sums run over fixed row chunks added in chunk order, so the result
-// does not depend on scheduling. `partial` holds lora_outer_partial_floats(Q, m, C) floats.
+// Destination of an outer-product gradient: element (j, c) of segment s goes to
+// p[s][kmajor[s] ? c * ld[s] + j : j * ld[s] + c] times scale[s].
 struct LoraOuterDst {
   float* p[2];
   long long ld[2];
@@ -233,10 +215,90 @@ struct LoraOuterDst {
   float scale[2];
   int split_j;  // coefficients j >= split_j go to p[1] (index minus split_j), or 0
 };
-size_t lora_outer_partial_floats(int Q, int m, int C);
-hipError_t launch_lora_outer(const LoraMat& src, int c_off, int Q, const int* pair_of, int k, const float* topk_w,
-                             const float* coef, int ldc, int coff, int m, int C, float* partial,
-                             const LoraOuterDst& dst, hipStream_t s);
+
+// One job of a LoRA pass (launch_lora_pass), over a source of `rows` rows (tokens, or pairs in
+// bucket order; rows at or past *rows_dev, when given, are skipped) in nseg <= 2 segments of K
+// columns (a multiple of 32), segment s starting at source column koff[s]:
+//   kLoraRowDot: partial row dots of out[row, s*r + j] = sum_k src(row, koff_s + k) f_s(j, k)
+//     (nseg 2), or of out[row, n*r + j] with factor f_n on the one segment (nseg 1, n < nfac <= 2);
+//   kLoraOuter: partial column sums of G[j, s*K + c] = sum over q < rows of
+//     row_w[q] * coef[crow(q), coff_s + j] * src(row(q), koff_s + c), j < m <= 64: with row_of,
+//     q runs over (token, slot) pairs in token order, row(q) = row_of[q] (skipped when negative)
+//     and crow(q) = q / k, so the sums do not depend on the bucket order; else row(q) = crow(q)
+//     = q. row_w null: 1.
+// Factor scales are not applied here (the finish applies them).
+//   kLoraRowOuter: both, over one two-term (hi + lo) pair source with row_of (nseg segments, m = r <=
+//     16 coefficients per segment, factor f_s on segment s): each element is read once.
+enum LoraJobType : int { kLoraRowDot = 0, kLoraOuter = 1, kLoraRowOuter = 2 };
+struct LoraPassJob {
+  int type;
+  LoraMat src;
+  int rows;
+  const int* rows_dev;
+  int nseg, K;
+  int koff[2];
+  int r;
+  int nfac;
+  LoraFactor f[2];
+  const float* coef;
+  long long ldc;
+  int coff[2];
+  const int* row_of;
+  int k;
+  const float* row_w;
+  int m;
+};
+// Partials a pass job leaves for its finish: `count` slices (row dots: [count, rows, m_out]) or
+// row chunks (outer products: [count, m, nseg * K]); a fused job leaves its outer-product
+// partials in p and its row-dot partials in p2 (count2 slices of [rows, nseg * r]).
+struct LoraPartial {
+  const float* p;
+  int count;
+  const float* p2;
+  int count2;
+};
+size_t lora_pass_partial_floats(const LoraPassJob* jobs, int n);
+// Up to 4 jobs in one launch; parts[i] receives job i's partials (inside `partial`, which holds
+// lora_pass_partial_floats(jobs, n) floats).
+hipError_t launch_lora_pass(const LoraPassJob* jobs, int n, float* partial, LoraPartial* parts, hipStream_t s);
+
+// One job of launch_lora_finish: the partials added in a fixed order.
+//   kLoraFinCoef: value (row, j) = scale[j / r] * sum over slices of the row-dot partials
+//     ([count, prow, m]); with pair_of, rows are pairs and out[t, j] = sum over token t's slots, in
+//     slot order, of (topk_w[t, s] or 1) * value(pair_of[t, s], j); else out[t, j] = value(t, j);
+//     out is [ntok, m].
+//   kLoraFinOuter: G[j, c] = sum over chunks of the outer partials ([count, om, Ctot]), written
+//     through dst; segments by column (Kseg > 0: s = c / Kseg) or by j (dst.split_j).
+enum LoraFinType : int { kLoraFinCoef = 0, kLoraFinOuter = 1 };
+struct LoraFinishJob {
+  int type;
+  LoraPartial part;
+  int prow, m, r;
+  float scale[2];
+  const int* pair_of;
+  const float* topk_w;
+  int k, ntok;
+  float* out;
+  int om, Ctot, Kseg;
+  LoraOuterDst dst;
+};
+hipError_t launch_lora_finish(const LoraFinishJob* jobs, int n, hipStream_t s);
+
+// out[t, c] = ef_s.scale * sum_{j < r} coef[t, ecoff_s + j] * ef_s(j, c - s*Cseg) for t < ntok,
+// c < Cexp (multiples of 4), segment s = c / Cseg (Cseg 0 or >= Cexp: one segment; two segments
+// share the factor layout); coef rows hold m floats, out rows are ldo apart. With part (row-dot
+// partials [count, ntok, m] of tokens), the coefficient rows are first reduced from them
+// (coef[t, j] = part_scale[j / r] * the slices' sum, added in slice order) and written to coef.
+hipError_t launch_lora_expand(float* coef, int m, int ntok, int r, float* out, long long ldo, int Cexp,
+                              int Cseg, const LoraFactor* ef, const int* ecoff, hipStream_t s,
+                              const LoraPartial* part = nullptr, const float* part_scale = nullptr);
+
+// out[t, c] = sum over token t's slots, in slot order, of rows[pair_of[t, s], c] (skipped when
+// negative) + sum over segments s < nseg of f_s.scale * sum_{j < r} coef[t, s*r + j] f_s(j, c);
+// with grad_w, also grad_w[t, s] = sum over ct < n_ct of gw_part[pair, ct] (the backward combine).
+hipError_t launch_lora_combine(float* out, const float* rows, long long ldy, const int* pair_of, int N, int k, int D,
+                               const float* coef, int r, int nseg, const LoraFactor* f, float* grad_w,
+                               const float* gw_part, int n_ct, hipStream_t s);
 
 // Router selection (sigmoid, bias, top-k, renormalise, scale), one wave per token.
 hipError_t launch_router_topk(long long* topk_idx, float* topk_w, const float* logits, const float* bias, int N,
