@@ -226,14 +226,17 @@ def expert_sweep(args, k, Ms):
         for _ in range(args.warmup):
             k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
         torch.cuda.synchronize()
-        k.set_timing(True)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(args.steps):
             k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
         end.record()
         torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / args.steps
+        ms = start.elapsed_time(end) / args.steps  # phase timer off: its event records cost time
+        k.set_timing(True)
+        for _ in range(args.steps):
+            k.routed_forward(H, I, W, layer, act=args.act, workspace=ws)
+        torch.cuda.synchronize()
         calls = k.phase_times()
         k.set_timing(False)
         ph = {}
@@ -666,7 +669,8 @@ def time_layer(args, k, layer, H, I, W, G, ws, lora, n_active, calibrate=False):
         torch.cuda.synchronize()
         del src, dst
 
-    k.set_timing(True)
+    # the step time with the library's phase timer off (its per-phase event records cost time on
+    # the stream), then the per-phase times over a separate run of the same steps
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -675,11 +679,14 @@ def time_layer(args, k, layer, H, I, W, G, ws, lora, n_active, calibrate=False):
         step()
     end.record(stream)
     torch.cuda.synchronize()
-    ms_total = start.elapsed_time(end)
+    ms_step = start.elapsed_time(end) / args.steps
+    log(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step")
+    k.set_timing(True)
+    for _ in range(max(3, args.steps // 4)):
+        step()
+    torch.cuda.synchronize()
     calls = k.phase_times()
     k.set_timing(False)
-    ms_step = ms_total / args.steps
-    log(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step")
     phase_ms = {}
     for call in calls:
         for name, ms in call:

@@ -161,19 +161,20 @@ int mxfp4_moe_backward_lora(float *grad_h, float *grad_w, const float *grad_out,
                             int lora_rank, float *const *lora_grads, int flags, void *workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
-/* Forward layout: a load-time copy of expert code bytes for the routed layer's forward products.
+/* Forward layout: a load-time copy of expert weights for the routed layer's forward products.
  * No counterpart in the reference, whose weights stay in the checkpoint layout; it is for
  * callers that keep a layer resident in HBM over many steps. For E stacked packed [R, K]
- * matrices (K a multiple of 512) mxfp4_forward_layout writes mxfp4_forward_layout_bytes(E, R, K)
- * bytes: per expert, 16-row group and 512-element super-chunk, the 4 KiB of codes that the
- * one-tile forward work-groups read, in the order their load instructions consume them (each
- * instruction then reads 1 KiB contiguous instead of 16-byte pieces of 16 rows; the large-bucket
- * work-groups' copies read four 256-byte runs instead of 16 rows' 64-byte runs). Scales are not
- * copied. The copy must be rebuilt whenever the weights change. dst and packed: 16-byte aligned,
- * not overlapping. */
+ * matrices (K a multiple of 512) with their E8M0 scales [R, K / 32], mxfp4_forward_layout writes
+ * mxfp4_forward_layout_bytes(E, R, K) bytes: per expert, 16-row group and 512-element
+ * super-chunk, the 4 KiB of codes that the one-tile forward work-groups read, in the order their
+ * load instructions consume them (each instruction then reads 1 KiB contiguous instead of
+ * 16-byte pieces of 16 rows; the large-bucket work-groups' copies read four 256-byte runs instead
+ * of 16 rows' 64-byte runs), then the same blocks' scales, 256 B per group and super-chunk in the
+ * order one 4-byte load per lane reads them (each scale line read once). The copy must be rebuilt
+ * whenever the weights change. dst, packed and scales: 16-byte aligned, dst overlapping neither. */
 size_t mxfp4_forward_layout_bytes(int E, int R, int K);
-int mxfp4_forward_layout(uint8_t *dst, const uint8_t *packed, int E, int R, int K,
-                         hipStream_t stream);
+int mxfp4_forward_layout(uint8_t *dst, const uint8_t *packed, const uint8_t *scales, int E, int R,
+                         int K, hipStream_t stream);
 
 /* mxfp4_moe_forward_lora / mxfp4_moe_backward_lora that also read forward layouts: fwd_layout is
  * a host array of 3 device pointers {W1, W3, W2}, the mxfp4_forward_layout of w1p, w3p, w2p (W1

@@ -400,7 +400,7 @@ int moe_front(const void* h, int h_dtype, const void* idx, int idx_dtype, const 
     MX_TRY(mx::launch_quant_tiles(h, h_dtype == MXFP4_BF16, D, N, D, at<int4>(ws, L.tiles), at<int>(ws, L.meta),
                                   L.max_tiles, at<int>(ws, L.pair_token), 1, at<uint8_t>(ws, L.xt_x),
                                   at<int>(ws, L.meta), at<uint8_t>(ws, L.at_x), at<uint8_t>(ws, L.x3_x),
-                                  at<int>(ws, L.meta) + 6, s),
+                                  at<int>(ws, L.meta) + 6, s, at<int4>(ws, L.groups), at<int>(ws, L.meta) + 3),
            "quantise h tiles");
   }
   MX_PHASE("quant_h", s);
@@ -629,18 +629,21 @@ size_t mxfp4_forward_layout_bytes(int E, int R, int K)
   return (size_t)E * (size_t)mx::forward_layout_bytes(R, K);
 }
 
-int mxfp4_forward_layout(uint8_t* dst, const uint8_t* packed, int E, int R, int K, hipStream_t stream)
+int mxfp4_forward_layout(uint8_t* dst, const uint8_t* packed, const uint8_t* scales, int E, int R, int K,
+                         hipStream_t stream)
 {
   if (E < 0 || R < 0 || K <= 0 || K % 512)
     return fail(MXFP4_EINVAL, "forward_layout: K must be a positive multiple of 512%s");
   if (E == 0 || R == 0) return MXFP4_OK;
-  if (!dst || !packed) return fail(MXFP4_EINVAL, "forward_layout: null pointer%s");
-  if (!aligned16(dst) || !aligned16(packed))
-    return fail(MXFP4_EINVAL, "forward_layout: dst and packed must be 16-byte aligned%s");
+  if (!dst || !packed || !scales) return fail(MXFP4_EINVAL, "forward_layout: null pointer%s");
+  if (!aligned16(dst) || !aligned16(packed) || !aligned16(scales))
+    return fail(MXFP4_EINVAL, "forward_layout: dst, packed and scales must be 16-byte aligned%s");
   const uintptr_t d0 = (uintptr_t)dst, d1 = d0 + mxfp4_forward_layout_bytes(E, R, K);
   const uintptr_t p0 = (uintptr_t)packed, p1 = p0 + (size_t)E * R * (K / 2);
-  if (d0 < p1 && p0 < d1) return fail(MXFP4_EINVAL, "forward_layout: dst overlaps packed%s");
-  MX_TRY(mx::launch_forward_layout(packed, dst, E, R, K, stream), "forward_layout");
+  const uintptr_t s0 = (uintptr_t)scales, s1 = s0 + (size_t)E * R * (K / 32);
+  if ((d0 < p1 && p0 < d1) || (d0 < s1 && s0 < d1))
+    return fail(MXFP4_EINVAL, "forward_layout: dst overlaps packed or scales%s");
+  MX_TRY(mx::launch_forward_layout(packed, scales, dst, E, R, K, stream), "forward_layout");
   return MXFP4_OK;
 }
 

@@ -269,6 +269,10 @@ MX_DEV i32x4 buf16_nt(rsrc_t r, uint32_t voff, uint32_t soff)
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2);
 }
 MX_DEV uint8_t buf8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0); }
+MX_DEV uint32_t buf4_nt(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 2);
+}
 
 // f(integral_constant<int, i>) for i = 0 .. N-1
 template <int N, int I = 0, typename Fn>

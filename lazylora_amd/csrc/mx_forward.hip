@@ -515,17 +515,21 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
     // (rg * nsc + c) * 4096 and holds MFMA q's operand at q * 1024, lane l's 16 B at l * 16: the
     // same bytes, each load instruction one contiguous 1 KiB.
     rsrc_t wr[4], wr_none[4];
+    rsrc_t sr[4];  // forward layout: the row group's weight-scale blocks
     uint32_t woff[4];
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       if constexpr (FL) {
         // the resource starts at the row group, so the lane offset is the same for all four
         const int rg = min(grp_row(grp), a.R - 1) / 16;
-        const uint8_t* base = (MODE == kFwdGateUp && grp >= 2 ? a.fl1 : a.fl0) + (long long)w.expert * a.fl_estride +
-                              (long long)rg * nsc * 4096;
-        wr[grp] = make_rsrc(base, (uint32_t)((a.R + 15) / 16 - rg) * (uint32_t)nsc * 4096u);
+        const int nrg = (a.R + 15) / 16;
+        const uint8_t* ebase = (MODE == kFwdGateUp && grp >= 2 ? a.fl1 : a.fl0) + (long long)w.expert * a.fl_estride;
+        const uint8_t* base = ebase + (long long)rg * nsc * 4096;
+        wr[grp] = make_rsrc(base, (uint32_t)(nrg - rg) * (uint32_t)nsc * 4096u);
         wr_none[grp] = make_rsrc(base, 0);
         woff[grp] = (uint32_t)lane * 16u;
+        sr[grp] = make_rsrc(ebase + (long long)nrg * nsc * 4096 + (long long)rg * nsc * 256,
+                            (uint32_t)(nrg - rg) * (uint32_t)nsc * 256u);
       } else {
         const uint8_t* base = grp_wp(grp);
         wr[grp] = make_rsrc(base, (uint32_t)a.R * (uint32_t)(a.K / 2));
@@ -533,7 +537,9 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
         woff[grp] = (uint32_t)(wrow[grp] - base) + boff[grp];
       }
     }
-    auto load_b_buf = [&](int c, i32x4 (&b)[4][4]) {
+    // forward layout: with a chunk's weights, the lanes' scale dwords of it (block (rg, c) holds
+    // lane l's dword at 4 l, one whole 256 B per instruction); a chunk past the last reads nothing
+    auto load_b_buf = [&](int c, i32x4 (&b)[4][4], uint32_t (&sbuf)[4]) {
       const bool live = c < nsc;  // uniform
 #pragma unroll
       for (int grp = 0; grp < 4; ++grp)
@@ -544,7 +550,13 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
           else
             b[grp][q] = buf16(live ? wr[grp] : wr_none[grp], woff[grp] + 16 * q, (uint32_t)c * 256);
         }
+      if constexpr (FL) {
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp)
+          sbuf[grp] = buf4_nt(live ? sr[grp] : wr_none[grp], (uint32_t)lane * 4u, (uint32_t)c * 256);
+      }
     };
+    constexpr int kChunkLoads = FL ? 20 : 16;  // vector loads per chunk of weights (and FL scales)
 
     // Two chunks of weights in flight: a buffer is refilled with chunk c + 2 as soon as chunk
     // c's MFMAs have read it, and chunk c + 1's loads are in flight meanwhile. The activation
@@ -552,15 +564,20 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
     // weight loads of chunk c + 1 (issued at the end of chunk c - 1), so at the top of chunk c
     // everything but those 16 has landed. The copies are issued from
     // inline assembly: a copy the compiler knows of makes it drain every load at each barrier.
-    auto step = [&](int c, i32x4 (&cur)[4][4]) {
-      wait_vm<16>();
+    auto step = [&](int c, i32x4 (&cur)[4][4], uint32_t (&cur_s)[4]) {
+      wait_vm<kChunkLoads>();
       __syncthreads();
       // everything this chunk needs from LDS, before any new copy into LDS is requested
       uint32_t sb[4];
 #pragma unroll
-      for (int grp = 0; grp < 4; ++grp)
-        sb[grp] = *reinterpret_cast<const uint32_t*>(sw + (grp * 16 + j) * kScaleRowBytes +
-                                                     (((c % kScaleWin) ^ (j & 7)) * 16) + g * 4);
+      for (int grp = 0; grp < 4; ++grp) {
+        if constexpr (FL) {
+          sb[grp] = cur_s[grp];
+        } else {
+          sb[grp] = *reinterpret_cast<const uint32_t*>(sw + (grp * 16 + j) * kScaleRowBytes +
+                                                       (((c % kScaleWin) ^ (j & 7)) * 16) + g * 4);
+        }
+      }
       const uint8_t* la = &lds.a[c & 1][lane * 16];
       i32x8 ah[4], al[4];
 #pragma unroll
@@ -575,13 +592,15 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       wait_lgkm0();
       // chunk c's weights are complete (wait_vm above)
 #pragma unroll
-      for (int grp = 0; grp < 4; ++grp)
+      for (int grp = 0; grp < 4; ++grp) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) pin(cur[grp][q]);
+        if constexpr (FL) pin(sb[grp]);
+      }
       __builtin_amdgcn_sched_barrier(0);
       if (c + 1 < nsc) {
         issue_a(c + 1, (c + 1) & 1);
-        if ((c + 1) % kScaleWin == 0) issue_scales((c + 1) / kScaleWin);
+        if (!FL && (c + 1) % kScaleWin == 0) issue_scales((c + 1) / kScaleWin);
       }
       __builtin_amdgcn_sched_barrier(0);
       sanitize_if_damaged(cur, sb);
@@ -590,23 +609,24 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
       mfma_step<2>(acc, ah[2], al[2], cur, sb, (int)s2.x, (int)s2.y);
       mfma_step<3>(acc, ah[3], al[3], cur, sb, (int)s2.x, (int)s2.y);
       __builtin_amdgcn_sched_barrier(0);
-      load_b_buf(c + 2, cur);
+      load_b_buf(c + 2, cur, cur_s);
     };
 
     if (MODE == kFwdDown)
 #pragma unroll
       for (int v = 0; v < 4; ++v) tw[v] = a.row_w[w.row0 + min(4 * g + v, w.nrows - 1)];
     i32x4 b0[4][4], b1[4][4];
-    load_b_buf(0, b0);
-    issue_scales(0);
+    uint32_t s0[4], s1[4];
+    load_b_buf(0, b0, s0);
+    if (!FL) issue_scales(0);
     issue_a(0, 0);
-    load_b_buf(1, b1);
+    load_b_buf(1, b1, s1);
     // the flag loads were issued before the first chunk's loads, which the first step waits for
     if (use3) m3 = x3_mask(f3, lane);
     for (int c = 0;;) {
-      step(c, b0);
+      step(c, b0, s0);
       if (++c >= nsc) break;
-      step(c, b1);
+      step(c, b1, s1);
       if (++c >= nsc) break;
     }
     wait_vm0();  // (no copy is in flight past the last chunk; kept explicit for the epilogue)
@@ -1300,43 +1320,64 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
 
 long long forward_layout_bytes(int R, int K)
 {
-  return (long long)((R + 15) / 16) * (K / kChunk) * 4096;
+  return (long long)((R + 15) / 16) * (K / kChunk) * (4096 + 256);
 }
 
 namespace {
 
-// One thread per 16-byte piece of the forward layout: piece l of operand block q of super-chunk
-// c of row group rg (at byte ((rg * nsc + c) * 4 + q) * 1024 + l * 16 of the expert's layout)
-// is MX block 4 (l / 16) + q of that super-chunk of row 16 rg + l % 16, the 16 bytes lane l of
-// the one-tile kernels reads for MFMA q; rows past R repeat row R - 1, as those kernels' loads do.
-__global__ __launch_bounds__(256) void forward_layout_kernel(const uint8_t* packed, uint8_t* out, int R, int K,
-                                                             long long per_expert, long long total)
+// One thread per 16-byte piece of the forward layout. Codes: piece l of operand block q of
+// super-chunk c of row group rg (at byte ((rg * nsc + c) * 4 + q) * 1024 + l * 16 of the expert's
+// layout) is MX block 4 (l / 16) + q of that super-chunk of row 16 rg + l % 16, the 16 bytes lane l
+// of the one-tile kernels reads for MFMA q. Scales, after the codes of all row groups: the 256 B of
+// (rg, c) at ((nrg * nsc) * 4096 + (rg * nsc + c) * 256) hold lane l's scale dword (blocks
+// 4 (l / 16) .. + 3 of super-chunk c of row 16 rg + l % 16) at 4 l. Rows past R repeat row R - 1,
+// as those kernels' loads do.
+__global__ __launch_bounds__(256) void forward_layout_kernel(const uint8_t* packed, const uint8_t* scales,
+                                                             uint8_t* out, int R, int K, long long per_expert,
+                                                             long long total)
 {
   const long long p = (long long)blockIdx.x * 256 + threadIdx.x;
   if (p >= total) return;
   const int nsc = K / kChunk;
   const long long e = p / per_expert;
   long long r = p - e * per_expert;
-  const int l = (int)(r & 63);
-  r >>= 6;
-  const int q = (int)(r & 3);
-  r >>= 2;
+  const long long code_pieces = (long long)((R + 15) / 16) * nsc * 256;
+  if (r < code_pieces) {
+    const int l = (int)(r & 63);
+    r >>= 6;
+    const int q = (int)(r & 3);
+    r >>= 2;
+    const int rg = (int)(r / nsc), c = (int)(r - (long long)rg * nsc);
+    const int row = min(rg * 16 + (l & 15), R - 1);
+    const uint8_t* src = packed + (e * R + row) * (long long)(K / 2) + c * 256 + (4 * (l >> 4) + q) * 16;
+    *reinterpret_cast<i32x4*>(out + p * 16) = *reinterpret_cast<const i32x4*>(src);
+    return;
+  }
+  r -= code_pieces;  // piece k of scale block (rg, c): the dwords of lanes 4k .. 4k + 3
+  const int k = (int)(r & 15);
+  r >>= 4;
   const int rg = (int)(r / nsc), c = (int)(r - (long long)rg * nsc);
-  const int row = min(rg * 16 + (l & 15), R - 1);
-  const uint8_t* src = packed + (e * R + row) * (long long)(K / 2) + c * 256 + (4 * (l >> 4) + q) * 16;
-  *reinterpret_cast<i32x4*>(out + p * 16) = *reinterpret_cast<const i32x4*>(src);
+  i32x4 v;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int l = 4 * k + u;
+    const int row = min(rg * 16 + (l & 15), R - 1);
+    v[u] = *reinterpret_cast<const int*>(scales + (e * R + row) * (long long)(K / 32) + c * 16 + 4 * (l >> 4));
+  }
+  *reinterpret_cast<i32x4*>(out + p * 16) = v;
 }
 
 }  // namespace
 
-hipError_t launch_forward_layout(const uint8_t* packed, uint8_t* out, int E, int R, int K, hipStream_t s)
+hipError_t launch_forward_layout(const uint8_t* packed, const uint8_t* scales, uint8_t* out, int E, int R, int K,
+                                 hipStream_t s)
 {
   if (E <= 0 || R <= 0) return hipSuccess;
   if (K <= 0 || K % kChunk) return hipErrorInvalidValue;
   const long long per_expert = forward_layout_bytes(R, K) / 16;
   const long long total = per_expert * E;
-  hipLaunchKernelGGL(forward_layout_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, packed, out, R,
-                     K, per_expert, total);
+  hipLaunchKernelGGL(forward_layout_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, packed, scales,
+                     out, R, K, per_expert, total);
   return hipGetLastError();
 }
 

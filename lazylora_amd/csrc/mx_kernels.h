@@ -65,19 +65,24 @@ struct FwdArgs {
   const int* n_wgroups;
   int* wcounter;  // the wide-group launch's work queue: 2 ints, zero before the first launch (queue_next)
   // Forward layout (launch_forward_layout) of W (W1 for kFwdGateUp) and W3, or null: the
-  // fast path's work-groups then read their weight codes from it in whole lines (the scales,
-  // and the general path, always come from wp* / ws*).
+  // one-tile fast path's work-groups then read their weight codes and scales from it in whole
+  // lines, the wide large-bucket work-groups their codes (the general path, the wide groups'
+  // scales and the rare third-term pass always read wp* / ws*).
   const uint8_t* fl0;
   const uint8_t* fl1;
   long long fl_estride;  // bytes between experts in fl*
 };
 
-// Forward layout of E stacked packed [R, K] matrices (K a multiple of 512), per expert
-// forward_layout_bytes(R, K) bytes: the 4 KiB at (rg * K / 512 + c) * 4096 hold super-chunk c of
-// the 16 rows 16 rg .., MFMA q's operand block at q * 1024, lane l's 16 bytes (MX block
-// 4 (l / 16) + q of row 16 rg + l % 16) at l * 16; rows past R repeat row R - 1.
+// Forward layout of E stacked packed [R, K] matrices (K a multiple of 512) and their E8M0 scales
+// [R, K / 32], per expert forward_layout_bytes(R, K) bytes, nrg = ceil(R / 16) row groups and
+// nsc = K / 512 super-chunks: codes, the 4 KiB at (rg * nsc + c) * 4096 hold super-chunk c of the
+// 16 rows 16 rg .., MFMA q's operand block at q * 1024, lane l's 16 bytes (MX block
+// 4 (l / 16) + q of row 16 rg + l % 16) at l * 16; then scales, the 256 B at
+// nrg * nsc * 4096 + (rg * nsc + c) * 256 hold lane l's scale dword (blocks 4 (l / 16) .. + 3 of
+// super-chunk c of row 16 rg + l % 16) at 4 l. Rows past R repeat row R - 1.
 long long forward_layout_bytes(int R, int K);
-hipError_t launch_forward_layout(const uint8_t* packed, uint8_t* out, int E, int R, int K, hipStream_t s);
+hipError_t launch_forward_layout(const uint8_t* packed, const uint8_t* scales, uint8_t* out, int E, int R, int K,
+                                 hipStream_t s);
 
 // ---------------------------------------------------------------- transposed products
 enum BwdMode : int {
@@ -150,9 +155,12 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
 // instead of quantising x again (the same bytes). x3 (with row_map): where the tiles are quantised
 // from x, also the X3 rows of their tokens (launch_quant_rows writes them otherwise). x3_any
 // (with x3): set to non-zero when some block has a third term (it must be zero before the call).
+// groups (with large_only; n_groups on the device): the large buckets' tiles are found through
+// the routing's group list by a resident grid, instead of one work-group per tile and chunk.
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
                               const int* n_tiles, int max_tiles, const int* row_map, int large_only, const uint8_t* xt,
-                              const int* meta, uint8_t* out, uint8_t* x3, int* x3_any, hipStream_t s);
+                              const int* meta, uint8_t* out, uint8_t* x3, int* x3_any, hipStream_t s,
+                              const int4* groups = nullptr, const int* n_groups = nullptr);
 // Rows 0 .. rows - 1 of x into the XT layout (xt_row_bytes(K) per row), followed by zero rows
 // up to xt_rows(rows): row `rows` is the all-zero row a tile's unused slots gather. x3 (or null):
 // the third term of the flagged blocks in the X3 layout (x3_row_bytes(K) per row; rows < rows).

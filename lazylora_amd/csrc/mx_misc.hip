@@ -31,28 +31,15 @@ MX_DEV void x3_store(uint8_t* x3r, int nsc, int c, int l16, const Quant3 (&q3)[k
 // an LDS copy of the chunk in the AT layout; the work-group then writes the chunk out with
 // contiguous 16-byte stores. Slots past the tile's row count, and K positions past the row
 // end, get zeros.
+// One (tile, super-chunk) of quant_tiles_kernel: tile t holds rows row0 .. row0 + nrows - 1 of
+// the row map (or of x); chunk is the work-group's LDS staging copy.
 template <bool BF16>
-__global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long long ldx, int rows, int K,
-                                                          const int4* tiles, const int* n_tiles, const int* row_map,
-                                                          int large_only, const uint8_t* xt, const int* meta,
-                                                          uint8_t* out, uint8_t* x3, int* x3_any)
+MX_DEV void quant_tile_chunk(const void* x, long long ldx, int rows, int K, int t, int c, int row0, int nrows,
+                             const int* row_map, const uint8_t* xt, const int* meta, uint8_t* out, uint8_t* x3,
+                             int* x3_any, uint8_t* chunk)
 {
-  __shared__ __attribute__((aligned(16))) uint8_t chunk[kAtChunkBytes];
   const int nsc = at_nchunks(K);
-  const int t = (int)(blockIdx.x / nsc), c = (int)(blockIdx.x - (long long)t * nsc);
-  const int ntiles = tiles ? *n_tiles : (rows + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
-  if (t >= ntiles) return;  // the whole work-group
   const int i = threadIdx.x >> 4, l16 = threadIdx.x & 15;
-  int row0, nrows;
-  if (tiles) {
-    const int4 tt = tiles[t];
-    if (large_only && tt.w == 0) return;  // the whole work-group: a small bucket's tile
-    row0 = tt.y;
-    nrows = tt.z;
-  } else {
-    row0 = t * kFwdRowsPerTile;
-    nrows = min(kFwdRowsPerTile, rows - row0);
-  }
   const long long cbase = (long long)c * kAtChunkBytes;  // at_*_off are tile-relative
   if (xt && !(meta[2] == 0 && meta[3] > 0)) {
     // The token-major rows are written (quant_rows_kernel runs before this kernel and quantises
@@ -119,6 +106,47 @@ __global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long lo
   uint8_t* dst = out + (long long)t * at_tile_bytes(K) + cbase;
   for (int o = threadIdx.x * 16; o < kAtChunkBytes; o += 256 * 16)
     *reinterpret_cast<i32x4*>(dst + o) = *reinterpret_cast<const i32x4*>(chunk + o);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void quant_tiles_kernel(const void* x, long long ldx, int rows, int K,
+                                                          const int4* tiles, const int* n_tiles, const int* row_map,
+                                                          int large_only, const int4* groups, const int* n_groups,
+                                                          const uint8_t* xt, const int* meta, uint8_t* out,
+                                                          uint8_t* x3, int* x3_any)
+{
+  __shared__ __attribute__((aligned(16))) uint8_t chunk[kAtChunkBytes];
+  const int nsc = at_nchunks(K);
+  if (groups) {
+    // the large buckets' tiles, by groups: a resident grid loops over (group, tile, super-chunk),
+    // so a routing without large buckets costs one read of the group count per work-group
+    const int total = *n_groups * kGroupTiles * nsc;
+    for (int wi = blockIdx.x; wi < total; wi += gridDim.x) {
+      const int g = wi / (kGroupTiles * nsc), r = wi - g * (kGroupTiles * nsc);
+      const int ti = r / nsc, c = r - ti * nsc;
+      const int4 gr = groups[g];
+      if (ti >= gr.z) continue;  // uniform
+      const int t = gr.y + ti;
+      const int4 tt = tiles[t];
+      __syncthreads();  // the previous item's reads of chunk are complete
+      quant_tile_chunk<BF16>(x, ldx, rows, K, t, c, tt.y, tt.z, row_map, xt, meta, out, x3, x3_any, chunk);
+    }
+    return;
+  }
+  const int t = (int)(blockIdx.x / nsc), c = (int)(blockIdx.x - (long long)t * nsc);
+  const int ntiles = tiles ? *n_tiles : (rows + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+  if (t >= ntiles) return;  // the whole work-group
+  int row0, nrows;
+  if (tiles) {
+    const int4 tt = tiles[t];
+    if (large_only && tt.w == 0) return;  // the whole work-group: a small bucket's tile
+    row0 = tt.y;
+    nrows = tt.z;
+  } else {
+    row0 = t * kFwdRowsPerTile;
+    nrows = min(kFwdRowsPerTile, rows - row0);
+  }
+  quant_tile_chunk<BF16>(x, ldx, rows, K, t, c, row0, nrows, row_map, xt, meta, out, x3, x3_any, chunk);
 }
 
 // ---------------------------------------------------------------- fp32 -> bf16 hi + lo
@@ -198,6 +226,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(void* out, const uint8_t* 
   }
 }
 
+constexpr int kQuantResidentBlocks = 1024;  // resident grid of quant_tiles over the large buckets
+
 // ---------------------------------------------------------------- routing
 // (token, slot) pairs are bucketed by expert: counts -> exclusive offsets -> placement.
 // The order of pairs inside a bucket is left to atomics; nothing downstream depends on it,
@@ -252,17 +282,12 @@ __global__ __launch_bounds__(256) void route_count_kernel(const void* idx, int i
 // kWideGroupTiles: every full wide group first (expert order), then the experts' last, partial
 // ones, so that a work queue taking them in order hands out the largest items first. The other
 // experts' tile indices go to the small-bucket list. meta = {tiles, flags, small tiles, groups,
-// wide groups, full wide groups}.
-__global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int E, int* offsets, int* cursor,
-                                                          int4* tiles, int* small_tiles, int4* groups, int4* wgroups,
-                                                          int* meta)
+// wide groups, full wide groups}. cursor[e] gets offsets[e] (cursor may be counts itself: each
+// expert's count is read before its cursor is written, by the same thread).
+__device__ __forceinline__ void route_scan(const int* counts, int E, int* offsets, int* cursor, int4* tiles,
+                                           int* small_tiles, int4* groups, int4* wgroups, int* meta, int* s_rows,
+                                           int* s_tiles, int* s_small, int* s_groups, int* s_wgroups, int* s_wpart)
 {
-  __shared__ int s_rows[1024];
-  __shared__ int s_tiles[1024];
-  __shared__ int s_small[1024];
-  __shared__ int s_groups[1024];
-  __shared__ int s_wgroups[1024];
-  __shared__ int s_wpart[1024];
   const int t = threadIdx.x;
   const int per = (E + 1023) / 1024;
   const int e0 = min(t * per, E), e1 = min(e0 + per, E);
@@ -330,6 +355,81 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int
     meta[3] = s_groups[1023];
     meta[4] = s_wgroups[1023] + s_wpart[1023];
     meta[5] = s_wgroups[1023];
+  }
+}
+
+__global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int E, int* offsets, int* cursor,
+                                                          int4* tiles, int* small_tiles, int4* groups, int4* wgroups,
+                                                          int* meta)
+{
+  __shared__ int s[6][1024];
+  route_scan(counts, E, offsets, cursor, tiles, small_tiles, groups, wgroups, meta, s[0], s[1], s[2], s[3], s[4], s[5]);
+}
+
+// The whole routing in one work-group (P <= kRouteOneP pairs, E <= kRouteOneE experts): counts
+// with LDS atomics, the scan above (cursors in LDS), then the placement with LDS atomics; all 16
+// meta words are written. Replaces five launches (two clears, count, scan, place) when the pairs
+// are few.
+constexpr int kRouteOneP = 65536;
+constexpr int kRouteOneE = 8192;
+
+__global__ __launch_bounds__(1024) void route_one_kernel(const void* idx, int idx64, const float* w, int P, int k,
+                                                         int E, int* counts, int* offsets, int4* tiles,
+                                                         int* small_tiles, int4* groups, int4* wgroups, int* meta,
+                                                         int* pair_token, float* pair_w, int* pair_of)
+{
+  __shared__ int s[6][1024];
+  __shared__ int s_cnt[kRouteOneE];
+  __shared__ int s_bad;
+  const int t = threadIdx.x;
+  for (int e = t; e < E; e += 1024) s_cnt[e] = 0;
+  if (t == 0) s_bad = 0;
+  __syncthreads();
+  // 8 pairs per thread and round, their index loads all issued before the atomics
+  for (int p0 = 0; p0 < P; p0 += 8 * 1024) {
+    int raw[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int p = p0 + u * 1024 + t;
+      raw[u] = p < P ? read_idx(idx, idx64, p) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (p0 + u * 1024 + t >= P) continue;
+      if (raw[u] >= 0 && raw[u] < E) atomicAdd(&s_cnt[raw[u]], 1);
+      else s_bad = 1;
+    }
+  }
+  __syncthreads();
+  for (int e = t; e < E; e += 1024) counts[e] = s_cnt[e];
+  // meta: the scan writes words 0 and 2..5; the flags word and words 6..15 (the products' flags
+  // and work-queue counters, which start at zero) are written here
+  if (t == 1) meta[1] = s_bad;
+  if (t >= 6 && t < 16) meta[t] = 0;
+  route_scan(s_cnt, E, offsets, s_cnt, tiles, small_tiles, groups, wgroups, meta, s[0], s[1], s[2], s[3], s[4], s[5]);
+  __syncthreads();
+  for (int p0 = 0; p0 < P; p0 += 8 * 1024) {
+    int raw[8];
+    float wv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int p = min(p0 + u * 1024 + t, P - 1);
+      raw[u] = read_idx(idx, idx64, p);
+      wv[u] = w[p];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int p = p0 + u * 1024 + t;
+      if (p >= P) continue;
+      if (raw[u] < 0 || raw[u] >= E) {
+        pair_of[p] = -1;
+        continue;
+      }
+      const int pos = atomicAdd(&s_cnt[raw[u]], 1);
+      pair_token[pos] = p / k;
+      pair_w[pos] = wv[u];
+      pair_of[p] = pos;
+    }
   }
 }
 
@@ -481,19 +581,22 @@ __global__ __launch_bounds__(256) void zero_kernel(uint32_t* p, long long n_word
 
 hipError_t launch_quant_tiles(const void* x, int x_bf16, long long ldx, int rows, int K, const int4* tiles,
                               const int* n_tiles, int max_tiles, const int* row_map, int large_only, const uint8_t* xt,
-                              const int* meta, uint8_t* out, uint8_t* x3, int* x3_any, hipStream_t s)
+                              const int* meta, uint8_t* out, uint8_t* x3, int* x3_any, hipStream_t s,
+                              const int4* groups, const int* n_groups)
 {
-  const long long groups = (long long)max_tiles * at_nchunks(K);  // (tile, super-chunk) work-groups
-  if (groups == 0) return hipSuccess;
+  long long blocks = (long long)max_tiles * at_nchunks(K);  // (tile, super-chunk) work-groups
+  if (blocks == 0) return hipSuccess;
   if (xt && (!meta || !row_map || !tiles)) return hipErrorInvalidValue;
   if (x3 && (!row_map || !x3_any)) return hipErrorInvalidValue;
-  dim3 grid((unsigned)groups), block(256);
+  if (groups && (!large_only || !tiles || !n_groups)) return hipErrorInvalidValue;
+  if (groups) blocks = std::min(blocks, (long long)kQuantResidentBlocks);  // a resident grid over the groups
+  dim3 grid((unsigned)blocks), block(256);
   if (x_bf16)
     hipLaunchKernelGGL(quant_tiles_kernel<true>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map,
-                       large_only, xt, meta, out, x3, x3_any);
+                       large_only, groups, n_groups, xt, meta, out, x3, x3_any);
   else
     hipLaunchKernelGGL(quant_tiles_kernel<false>, grid, block, 0, s, x, ldx, rows, K, tiles, n_tiles, row_map,
-                       large_only, xt, meta, out, x3, x3_any);
+                       large_only, groups, n_groups, xt, meta, out, x3, x3_any);
   return hipGetLastError();
 }
 
@@ -545,6 +648,11 @@ hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, in
                         int* meta, int* pair_token, float* pair_w, int* pair_of, hipStream_t s)
 {
   const int P = N * k;
+  if (P <= kRouteOneP && E <= kRouteOneE) {
+    hipLaunchKernelGGL(route_one_kernel, dim3(1), dim3(1024), 0, s, topk_idx, idx64, topk_w, P, k, E, counts, offsets,
+                       tiles, small_tiles, groups, wgroups, meta, pair_token, pair_w, pair_of);
+    return hipGetLastError();
+  }
   hipError_t e = launch_zero(counts, sizeof(int) * (size_t)E, s);
   if (e != hipSuccess) return e;
   e = launch_zero(meta, sizeof(int) * 16, s);

@@ -99,23 +99,25 @@ class ExpertLayer:
     def prepare_forward_layout(self) -> int:
         """Builds the forward-layout copies of W1, W3 (when D is a multiple of 512) and W2 (when F
         is), which the routed forward's small-bucket work-groups then read with whole 1 KiB loads
-        (mxfp4_forward_layout; results are bit-identical). Each copy holds the packed codes it
-        copies with the rows padded to a multiple of 16 (ceil(R / 16) * 16 * K / 2 bytes per
-        expert: the same size when R is a multiple of 16); returns the bytes added.
+        of codes and whole-line loads of scales (mxfp4_forward_layout; results are
+        bit-identical). Each copy holds the packed codes and E8M0 scales it copies with the rows
+        padded to a multiple of 16 (ceil(R / 16) * 16 * (K / 2 + K / 32) bytes per expert: the
+        same size when R is a multiple of 16); returns the bytes added.
 
-        The copies reflect the weights as they are now. An in-place torch write to the codes
-        (or rebinding the tensors) is detected before the next routed call, which then drops
-        the copy with a warning; loader.upload drops it too. Writes the version counters do not
-        see (through `.data`, ctypes or hipMemcpy, or by another C caller) are not detected:
+        The copies reflect the weights as they are now. An in-place torch write to the codes or
+        scales (or rebinding the tensors) is detected before the next routed call, which then
+        drops the copy with a warning; loader.upload drops it too. Writes the version counters do
+        not see (through `.data`, ctypes or hipMemcpy, or by another C caller) are not detected:
         call drop_forward_layout() or prepare_forward_layout() after them, or the forward reads
-        the old codes."""
+        the old weights."""
         from lazylora_amd.native import kernel
 
         k = kernel()
         if k is None:
             raise RuntimeError("the forward layout needs the native library on a GPU")
-        w13 = (k.forward_layout(self.w1p), k.forward_layout(self.w3p)) if self.D % 512 == 0 else (None, None)
-        w2 = k.forward_layout(self.w2p) if self.F % 512 == 0 else None
+        w13 = ((k.forward_layout(self.w1p, self.w1s), k.forward_layout(self.w3p, self.w3s)) if self.D % 512 == 0
+               else (None, None))
+        w2 = k.forward_layout(self.w2p, self.w2s) if self.F % 512 == 0 else None
         self._fl = (w13[0], w13[1], w2)
         self._fl_versions = self._code_versions()
         return sum(t.numel() for t in self._fl if t is not None)
@@ -126,8 +128,8 @@ class ExpertLayer:
 
     def _code_versions(self):
         # torch counts in-place writes per tensor (a write through a view counts for its base)
-        return (self.w1p._version, self.w3p._version, self.w2p._version, self.w1p.data_ptr(),
-                self.w3p.data_ptr(), self.w2p.data_ptr())
+        ts = (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s)
+        return tuple(t._version for t in ts) + tuple(t.data_ptr() for t in ts)
 
     def forward_layout_pointers(self):
         """Host array of the three forward-layout device pointers for mxfp4_moe_*_fl, or None.
@@ -136,7 +138,7 @@ class ExpertLayer:
         if self._fl is None:
             return None
         if self._code_versions() != self._fl_versions:
-            warnings.warn("expert codes changed after prepare_forward_layout(): the forward-layout copy is dropped "
+            warnings.warn("expert weights changed after prepare_forward_layout(): the forward-layout copy is dropped "
                           "(call prepare_forward_layout() again to rebuild it)", RuntimeWarning, stacklevel=3)
             self._fl = None
             return None

@@ -93,7 +93,7 @@ def _load_library() -> ctypes.CDLL:
     lib.mxfp4_forward_layout_bytes.restype = sz
     lib.mxfp4_forward_layout_bytes.argtypes = [ci, ci, ci]
     lib.mxfp4_forward_layout.restype = ci
-    lib.mxfp4_forward_layout.argtypes = [vp, vp, ci, ci, ci, vp]
+    lib.mxfp4_forward_layout.argtypes = [vp, vp, vp, ci, ci, ci, vp]
     lib.mxfp4_moe_route_status.restype = ci
     lib.mxfp4_moe_route_status.argtypes = [vp, vp, vp]
     lib.mxfp4_router_topk.restype = ci
@@ -211,22 +211,28 @@ class MXFP4Kernel:
         """Parallel width of the device (compute units), the analogue of mxfp4_threads()."""
         return int(self.lib.mxfp4_threads())
 
-    def forward_layout(self, packed: torch.Tensor) -> torch.Tensor:
+    def forward_layout(self, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
         """The forward layout (mxfp4_forward_layout) of stacked packed matrices [E, R, K/2] uint8
-        in HBM, K a multiple of 512: a new flat uint8 tensor on the same device. No counterpart
-        in the reference; ExpertLayer.prepare_forward_layout keeps these for a resident layer."""
+        and their scales [E, R, K/32] uint8 in HBM, K a multiple of 512: a new flat uint8 tensor
+        on the same device. No counterpart in the reference; ExpertLayer.prepare_forward_layout
+        keeps these for a resident layer."""
         if packed.dtype != torch.uint8 or packed.dim() != 3 or not packed.is_cuda:
             raise ValueError("packed must be a CUDA uint8 tensor [E, R, K/2]")
         E, R, Kh = packed.shape
         K = 2 * Kh
         if K % 512:
             raise ValueError(f"the forward layout needs K to be a multiple of 512, got K={K}")
-        src = packed.contiguous()
+        if scales.dtype != torch.uint8 or tuple(scales.shape) != (E, R, K // 32) or scales.device != packed.device:
+            raise ValueError("scales must be a uint8 tensor [E, R, K/32] on the codes' device")
+        src, ssrc = packed.contiguous(), scales.contiguous()
         if src.data_ptr() % 16:
             src = src.clone()
+        if ssrc.data_ptr() % 16:
+            ssrc = ssrc.clone()
         n = int(self.lib.mxfp4_forward_layout_bytes(E, R, K))
         out = torch.empty(max(n, 16), dtype=torch.uint8, device=packed.device)
-        _check(self.lib.mxfp4_forward_layout(out.data_ptr(), src.data_ptr(), E, R, K, _stream(packed.device)),
+        _check(self.lib.mxfp4_forward_layout(out.data_ptr(), src.data_ptr(), ssrc.data_ptr(), E, R, K,
+                                             _stream(packed.device)),
                self.lib)
         return out
 

@@ -70,16 +70,22 @@ def test_host_side_argument_errors(lib):
 def test_forward_layout_host_checks(lib):
     vp = ctypes.c_void_p
     dummy = vp(256)  # never dereferenced: every call below fails (or finishes) before a launch
-    # 2 experts x 3 row groups (R = 40: the last group holds 8 rows) x 2 super-chunks x 4 KiB
-    assert lib.mxfp4_forward_layout_bytes(2, 40, 1024) == 2 * 3 * 2 * 4096
+    # 2 experts x 3 row groups (R = 40: the last group holds 8 rows) x 2 super-chunks x (4 KiB of
+    # codes + 256 B of scales)
+    assert lib.mxfp4_forward_layout_bytes(2, 40, 1024) == 2 * 3 * 2 * (4096 + 256)
     assert lib.mxfp4_forward_layout_bytes(2, 40, 1056) == 0  # K not a multiple of 512
-    assert lib.mxfp4_forward_layout(dummy, dummy, 2, 40, 1056, None) == -1
+    far = vp(1 << 40)  # scales far from every other range below
+    assert lib.mxfp4_forward_layout(dummy, dummy, far, 2, 40, 1056, None) == -1
     assert b"multiple of 512" in lib.mxfp4_last_error()
-    assert lib.mxfp4_forward_layout(None, dummy, 2, 40, 1024, None) == -1     # null output
-    assert lib.mxfp4_forward_layout(vp(264), dummy, 2, 40, 1024, None) == -1  # unaligned output
-    assert lib.mxfp4_forward_layout(dummy, vp(256 + 4096), 2, 40, 1024, None) == -1  # overlapping
+    assert lib.mxfp4_forward_layout(None, dummy, far, 2, 40, 1024, None) == -1     # null output
+    assert lib.mxfp4_forward_layout(dummy, dummy, None, 2, 40, 1024, None) == -1   # null scales
+    assert lib.mxfp4_forward_layout(vp(264), dummy, far, 2, 40, 1024, None) == -1  # unaligned output
+    assert lib.mxfp4_forward_layout(dummy, vp(1 << 41), vp(264), 2, 40, 1024, None) == -1  # unaligned scales
+    assert lib.mxfp4_forward_layout(dummy, vp(256 + 4096), far, 2, 40, 1024, None) == -1  # overlapping codes
     assert b"overlaps" in lib.mxfp4_last_error()
-    assert lib.mxfp4_forward_layout(None, None, 0, 40, 1024, None) == 0       # E = 0: no-op
+    assert lib.mxfp4_forward_layout(dummy, vp(1 << 41), vp(256 + 4096), 2, 40, 1024, None) == -1  # overlapping scales
+    assert b"overlaps" in lib.mxfp4_last_error()
+    assert lib.mxfp4_forward_layout(None, None, None, 0, 40, 1024, None) == 0       # E = 0: no-op
     # the routed calls with forward layouts {W1, W3, W2}: D = 1024, F = 544
     args = [dummy, dummy, 0, dummy, 3, dummy, 4, 2] + [dummy] * 6
     tail = [8, 1024, 544, 0, None, None, 0, 0, dummy, 1 << 40, None]
@@ -236,8 +242,8 @@ def test_from_bundles_places_streamed_experts_by_id():
 
 
 def test_forward_layout_dropped_after_inplace_write():
-    """A forward-layout copy made before an in-place write to the codes is stale: the layer drops
-    it (with a warning) instead of handing its pointers to the routed calls."""
+    """A forward-layout copy made before an in-place write to the codes or scales is stale: the
+    layer drops it (with a warning) instead of handing its pointers to the routed calls."""
     import warnings
     from lazylora_amd.experts import ExpertLayer
     E, D, F = 2, 512, 512
@@ -254,4 +260,10 @@ def test_forward_layout_dropped_after_inplace_write():
         assert L.forward_layout_pointers() is None
     assert any(issubclass(w.category, RuntimeWarning) for w in caught)
     assert L._fl is None
+    L._fl = (z(16), z(16), None)  # the copies hold the scales too: a write to them also makes them stale
+    L._fl_versions = L._code_versions()
+    L.w1s.add_(1)
+    with warnings.catch_warnings(record=True):
+        warnings.simplefilter("always")
+        assert L.forward_layout_pointers() is None
 

@@ -25,19 +25,24 @@ def case(msg):
     print(f"\n[case] {msg}", flush=True)
 
 
-def layout_numpy(packed: np.ndarray, R: int, K: int) -> np.ndarray:
-    """Per expert, row group rg, super-chunk c, operand block q and lane l: the 16 bytes of MX
-    block 4 (l // 16) + q of super-chunk c of row 16 rg + l % 16, rows past R repeating R - 1."""
+def layout_numpy(packed: np.ndarray, scales: np.ndarray, R: int, K: int) -> np.ndarray:
+    """Per expert: codes, per row group rg, super-chunk c, operand block q and lane l the 16 bytes
+    of MX block 4 (l // 16) + q of super-chunk c of row 16 rg + l % 16; then scales, per rg, c and
+    lane l the 4 scale bytes of blocks 4 (l // 16) .. + 3 of that super-chunk of that row. Rows past
+    R repeat R - 1."""
     E = packed.shape[0]
     nsc, G = K // 512, (R + 15) // 16
-    out = np.empty((E, G, nsc, 4, 64, 16), np.uint8)
+    codes = np.empty((E, G, nsc, 4, 64, 16), np.uint8)
+    sc = np.empty((E, G, nsc, 64, 4), np.uint8)
     for l in range(64):
         rows = np.minimum(np.arange(G) * 16 + l % 16, R - 1)
         chunks = packed[:, rows, :].reshape(E, G, nsc, 256)
+        schunks = scales[:, rows, :].reshape(E, G, nsc, 16)
         for q in range(4):
             blk = 4 * (l // 16) + q
-            out[:, :, :, q, l, :] = chunks[:, :, :, blk * 16:(blk + 1) * 16]
-    return out.reshape(-1)
+            codes[:, :, :, q, l, :] = chunks[:, :, :, blk * 16:(blk + 1) * 16]
+        sc[:, :, :, l, :] = schunks[:, :, :, 4 * (l // 16):4 * (l // 16) + 4]
+    return np.concatenate([codes.reshape(E, -1), sc.reshape(E, -1)], axis=1).reshape(-1)
 
 
 @pytest.mark.parametrize("E,R,K", [(3, 40, 1024), (2, 64, 512), (1, 16, 7168)])
@@ -45,8 +50,9 @@ def test_layout_bytes(k, E, R, K):
     case(f"forward layout bytes E={E} R={R} K={K}")
     rng = np.random.default_rng(E * 1000 + R + K)
     packed = rng.integers(0, 256, (E, R, K // 2), dtype=np.uint8)
-    got = k.forward_layout(torch.from_numpy(packed).cuda()).cpu().numpy()
-    want = layout_numpy(packed, R, K)
+    scales = rng.integers(0, 256, (E, R, K // 32), dtype=np.uint8)
+    got = k.forward_layout(torch.from_numpy(packed).cuda(), torch.from_numpy(scales).cuda()).cpu().numpy()
+    want = layout_numpy(packed, scales, R, K)
     assert got.size == want.size == k.lib.mxfp4_forward_layout_bytes(E, R, K)
     assert np.array_equal(got, want)
 
