@@ -8,10 +8,11 @@ renormalised softmax weights, upstream gradient ~N(0,1) fp32. One step = the rou
 (saving gate/up for the backward) + the manual backward (dX through the transposed experts,
 GLU derivative, routing-weight gradient). Weights and inputs are resident in HBM before the
 timed region starts; nothing is skipped inside it. Before the timed regions the layer also gets
-its forward-layout copy of the expert codes (ExpertLayer.prepare_forward_layout: the same bytes
-in the order the forward work-groups load them, built once, as a serving process
-would at load time; `config.weight_layout` reports its size and build time;
---no-forward-layout reads the checkpoint layout only).
+its forward- and backward-layout copies of the expert weights (ExpertLayer.prepare_forward_layout,
+prepare_backward_layout: the same bytes in the order the forward and the transposed work-groups
+load them, built once, as a resident training or serving process would at load time;
+`config.weight_layout` reports their sizes and build times; --no-forward-layout and
+--no-backward-layout leave either out).
 
 Prints one JSON line. `value` is MoE-layer fwd+bwd tokens/s; `roofline` is the dominant
 kernel's algorithmic weight bytes per launch over its mean duration, measured with HIP events
@@ -21,9 +22,10 @@ repo's C restatement of the reference CPU path timed on a bounded sample of the 
     python bench.py [--steps 20] [--warmup 3] [--routing uniform|zipf] [--no-cpu] [--no-extra]
 
 The default run also times the same step reading only the checkpoint layout (key
-"checkpoint_layout_only"), the Zipf-skewed routing of the same layer (key "zipf"), config 3's
-forward alone under both routings (key "config3_forward"), config 2 at M = 1 and M = 256 tokens
-per expert (key "config2"), a 12-layer sample of config 5's out-of-core sweep (key
+"checkpoint_layout_only") and with the forward layout alone (key "forward_layout_only"), the
+Zipf-skewed routing of the same layer (key "zipf"), config 3's forward alone under both
+routings (key "config3_forward"), config 2 at M = 1 and M = 256 tokens per expert (key
+"config2"), a 12-layer sample of config 5's out-of-core sweep (key
 "config5_sample", with the same sweep under Zipf routing copying only the selected experts) and
 the reference-signature streamed node fed by a streamer of pageable ExpertWeightBundle-shaped
 objects (key "streamed_node"), each in its own timed region after the headline's. The CPU
@@ -93,18 +95,25 @@ def make_layer(seed: int):
                        codes(E, D, F // 2), scales(E, D, F // 32))
 
 
-def forward_layout(args, layer) -> dict:
-    """Builds the layer's forward-layout copy of the expert codes (a one-time load step, outside
-    every timed region) unless --no-forward-layout; returns what the JSON line reports of it."""
-    if args.no_forward_layout:
-        return {"forward_layout": False}
-    torch.cuda.synchronize()
-    t0 = time.time()
-    extra = layer.prepare_forward_layout()
-    torch.cuda.synchronize()
-    ms = (time.time() - t0) * 1e3
-    log(f"[bench] forward layout: {extra / 1e9:.2f} GB more in HBM, built in {ms:.1f} ms")
-    return {"forward_layout": True, "forward_layout_bytes": extra, "forward_layout_build_ms": round(ms, 1)}
+def forward_layout(args, layer, backward: bool = True) -> dict:
+    """Builds the layer's forward-layout copy of the expert weights unless --no-forward-layout
+    and, with `backward`, its backward-layout copy unless --no-backward-layout (one-time load
+    steps, outside every timed region); returns what the JSON line reports of them."""
+    out = {"forward_layout": not args.no_forward_layout,
+           "backward_layout": backward and not args.no_backward_layout}
+    for name, on, prep in (("forward", out["forward_layout"], layer.prepare_forward_layout),
+                           ("backward", out["backward_layout"], layer.prepare_backward_layout)):
+        if not on:
+            continue
+        torch.cuda.synchronize()
+        t0 = time.time()
+        extra = prep()
+        torch.cuda.synchronize()
+        ms = (time.time() - t0) * 1e3
+        log(f"[bench] {name} layout: {extra / 1e9:.2f} GB more in HBM, built in {ms:.1f} ms")
+        out[f"{name}_layout_bytes"] = extra
+        out[f"{name}_layout_build_ms"] = round(ms, 1)
+    return out
 
 
 def make_inputs(seed: int, routing: str):
@@ -214,7 +223,7 @@ def expert_sweep(args, k, Ms):
     scales = lambda *sh: torch.randint(117, 122, sh, dtype=torch.uint8, device="cuda", generator=gen)
     layer = ExpertLayer(codes(copies, F, D // 2), scales(copies, F, D // 32), codes(copies, F, D // 2),
                         scales(copies, F, D // 32), codes(copies, D, F // 2), scales(copies, D, F // 32))
-    forward_layout(args, layer)
+    forward_layout(args, layer, backward=False)  # a forward-only workload
     sweep = []
     for M in Ms:
         n = copies * M
@@ -447,7 +456,9 @@ def main():
     ap.add_argument("--lora-rank", type=int, default=0,
                     help="rank of the layer's gate/up/down LoRA adapters (0: off, the BASELINE configs)")
     ap.add_argument("--no-forward-layout", action="store_true",
-                    help="read only the checkpoint layout (no forward-layout copy of the expert codes)")
+                    help="no forward-layout copy of the expert weights (the forward reads the checkpoint layout)")
+    ap.add_argument("--no-backward-layout", action="store_true",
+                    help="no backward-layout copy (the transposed products read the checkpoint layout)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (reference kernel for rocprof byte counters)")
     args = ap.parse_args()
@@ -491,12 +502,22 @@ def main():
     if lora is not None:
         extra["lora_overhead"] = time_lora_ab(args, k, layer, H, I, W, G, ws, lora)
     zipf_inputs = None
-    if not args.no_extra and layout.get("forward_layout"):
-        # the same step reading only the checkpoint layout, for comparison (then the copy is rebuilt)
+    if not args.no_extra and layout.get("backward_layout") and layout.get("forward_layout"):
+        # the same step with the forward layout alone, for comparison (then the copy is rebuilt)
+        layer.drop_backward_layout()
+        ms_fo, _ = time_layer(args, k, layer, H, I, W, G, ws, lora, n_active)
+        extra["forward_layout_only"] = {"ms_per_step": ms_fo, "tokens_per_s": N / (ms_fo * 1e-3)}
+        layer.prepare_backward_layout()
+    if not args.no_extra and (layout.get("forward_layout") or layout.get("backward_layout")):
+        # the same step reading only the checkpoint layout, for comparison (then the copies are rebuilt)
         layer.drop_forward_layout()
+        layer.drop_backward_layout()
         ms_ck, _ = time_layer(args, k, layer, H, I, W, G, ws, lora, n_active)
         extra["checkpoint_layout_only"] = {"ms_per_step": ms_ck, "tokens_per_s": N / (ms_ck * 1e-3)}
-        layer.prepare_forward_layout()
+        if layout.get("forward_layout"):
+            layer.prepare_forward_layout()
+        if layout.get("backward_layout"):
+            layer.prepare_backward_layout()
     if not args.no_extra and args.routing == "uniform" and not args.lora_rank:
         # the skewed variant of configs 3/4 ([3]) on the same layer
         Hz, Iz, Wz, Gz = make_inputs(1, "zipf")

@@ -58,6 +58,7 @@ extern "C" {
 /* Flags for the routed layer. */
 #define MXFP4_MOE_SAVE 1          /* forward keeps gate|up and routing in the workspace */
 #define MXFP4_MOE_REUSE_FORWARD 2 /* backward reuses them instead of recomputing */
+#define MXFP4_MOE_BWD_LAYOUT 4    /* mxfp4_moe_*_fl: the layout array holds 6 entries (below) */
 
 /* Text of the last error raised on the calling thread ("" if none). */
 const char *mxfp4_last_error(void);
@@ -176,12 +177,30 @@ size_t mxfp4_forward_layout_bytes(int E, int R, int K);
 int mxfp4_forward_layout(uint8_t *dst, const uint8_t *packed, const uint8_t *scales, int E, int R,
                          int K, hipStream_t stream);
 
-/* mxfp4_moe_forward_lora / mxfp4_moe_backward_lora that also read forward layouts: fwd_layout is
- * a host array of 3 device pointers {W1, W3, W2}, the mxfp4_forward_layout of w1p, w3p, w2p (W1
- * and W3 both or neither; NULL entries, or a NULL array, read the checkpoint layout). An entry
- * needs its K (D for W1 and W3, F for W2) to be a multiple of 512. Results are bit-identical to
- * the calls without forward layouts; w1p, w3p, w2p are still read (the transposed products use
- * them). */
+/* Backward layout: a load-time copy of expert weights for the routed layer's transposed
+ * products (the backward). No counterpart in the reference; like the forward layout it is for
+ * callers that keep a layer resident in HBM. For E stacked packed [R, K] matrices (R a multiple
+ * of 32, K a multiple of 256) with their E8M0 scales [R, K / 32], mxfp4_backward_layout writes
+ * mxfp4_backward_layout_bytes(E, R, K) bytes (the codes and scales it copies, rearranged): per
+ * expert, 32-row step and 256-element stripe, the 4 KiB of codes that one wave of the transposed
+ * products reads, in the order its four 16-byte loads per lane consume them (each instruction
+ * reads 1 KiB contiguous instead of 8-byte pieces of eight rows), then the blocks' scales, 256 B
+ * each, one 8-byte load per lane (instead of eight scale-byte loads). 0 bytes / MXFP4_EINVAL for
+ * other shapes. The copy must be rebuilt whenever the weights change. dst, packed and scales:
+ * 16-byte aligned, dst overlapping neither. */
+size_t mxfp4_backward_layout_bytes(int E, int R, int K);
+int mxfp4_backward_layout(uint8_t *dst, const uint8_t *packed, const uint8_t *scales, int E, int R,
+                          int K, hipStream_t stream);
+
+/* mxfp4_moe_forward_lora / mxfp4_moe_backward_lora that also read load-time layouts: fwd_layout
+ * is a host array of 3 device pointers {W1, W3, W2}, the mxfp4_forward_layout of w1p, w3p, w2p
+ * (W1 and W3 both or neither; NULL entries, or a NULL array, read the checkpoint layout). An
+ * entry needs its K (D for W1 and W3, F for W2) to be a multiple of 512. With
+ * MXFP4_MOE_BWD_LAYOUT in flags the array holds 6 pointers: those 3, then the
+ * mxfp4_backward_layout of w1p, w3p, w2p (again W1 and W3 both or neither; W1 and W3 need D a
+ * multiple of 256, W2 needs F a multiple of 256), which the backward's transposed products read
+ * (the forward ignores them). Results are bit-identical to the calls without layouts; w1p..w2s
+ * are still read (the large-bucket work-groups of the transposed products use them). */
 int mxfp4_moe_forward_fl(float *out, const void *h, int h_dtype, const void *topk_idx,
                          int idx_dtype, const float *topk_w, int N, int k, const uint8_t *w1p,
                          const uint8_t *w1s, const uint8_t *w3p, const uint8_t *w3s,

@@ -360,7 +360,8 @@ mx::LoraOuterDst dst_of(float* p0, long long ld0, int km0, float s0, float* p1, 
 
 // Forward-layout copies {W1, W3, W2} (null array or entries: that product reads the checkpoint
 // layout). An entry needs its matrix's K (D for W1 and W3, F for W2) to be a multiple of 512.
-int check_forward_layout(const uint8_t* const* fl, int D, int F)
+// With MXFP4_MOE_BWD_LAYOUT, entries 3..5 are the backward-layout copies of W1, W3, W2.
+int check_forward_layout(const uint8_t* const* fl, int D, int F, int flags)
 {
   if (!fl) return MXFP4_OK;
   for (int i = 0; i < 3; ++i) {
@@ -369,6 +370,14 @@ int check_forward_layout(const uint8_t* const* fl, int D, int F)
     if (!aligned16(fl[i])) return fail(MXFP4_EINVAL, "moe: forward layouts must be 16-byte aligned%s");
   }
   if (!fl[0] != !fl[1]) return fail(MXFP4_EINVAL, "moe: give the forward layouts of W1 and W3 together%s");
+  if (!(flags & MXFP4_MOE_BWD_LAYOUT)) return MXFP4_OK;
+  for (int i = 3; i < 6; ++i) {
+    if (!fl[i]) continue;
+    if (!(i < 5 ? mx::backward_layout_ok(F, D) : mx::backward_layout_ok(D, F)))
+      return fail(MXFP4_EINVAL, "moe: a backward layout needs K a multiple of 256 (D for W1 and W3, F for W2)%s");
+    if (!aligned16(fl[i])) return fail(MXFP4_EINVAL, "moe: backward layouts must be 16-byte aligned%s");
+  }
+  if (!fl[3] != !fl[4]) return fail(MXFP4_EINVAL, "moe: give the backward layouts of W1 and W3 together%s");
   return MXFP4_OK;
 }
 
@@ -647,6 +656,30 @@ int mxfp4_forward_layout(uint8_t* dst, const uint8_t* packed, const uint8_t* sca
   return MXFP4_OK;
 }
 
+size_t mxfp4_backward_layout_bytes(int E, int R, int K)
+{
+  if (E <= 0 || !mx::backward_layout_ok(R, K)) return 0;
+  return (size_t)E * (size_t)mx::backward_layout_bytes(R, K);
+}
+
+int mxfp4_backward_layout(uint8_t* dst, const uint8_t* packed, const uint8_t* scales, int E, int R, int K,
+                          hipStream_t stream)
+{
+  if (E < 0 || !mx::backward_layout_ok(R, K))
+    return fail(MXFP4_EINVAL, "backward_layout: R must be a positive multiple of 32 and K of 256%s");
+  if (E == 0) return MXFP4_OK;
+  if (!dst || !packed || !scales) return fail(MXFP4_EINVAL, "backward_layout: null pointer%s");
+  if (!aligned16(dst) || !aligned16(packed) || !aligned16(scales))
+    return fail(MXFP4_EINVAL, "backward_layout: dst, packed and scales must be 16-byte aligned%s");
+  const uintptr_t d0 = (uintptr_t)dst, d1 = d0 + mxfp4_backward_layout_bytes(E, R, K);
+  const uintptr_t p0 = (uintptr_t)packed, p1 = p0 + (size_t)E * R * (K / 2);
+  const uintptr_t s0 = (uintptr_t)scales, s1 = s0 + (size_t)E * R * (K / 32);
+  if ((d0 < p1 && p0 < d1) || (d0 < s1 && s0 < d1))
+    return fail(MXFP4_EINVAL, "backward_layout: dst overlaps packed or scales%s");
+  MX_TRY(mx::launch_backward_layout(packed, scales, dst, E, R, K, stream), "backward_layout");
+  return MXFP4_OK;
+}
+
 int mxfp4_moe_forward_fl(float* out, const void* h, int h_dtype, const void* topk_idx, int idx_dtype,
                          const float* topk_w, int N, int k, const uint8_t* w1p, const uint8_t* w1s, const uint8_t* w3p,
                          const uint8_t* w3s, const uint8_t* w2p, const uint8_t* w2s, const uint8_t* const* fwd_layout,
@@ -656,7 +689,7 @@ int mxfp4_moe_forward_fl(float* out, const void* h, int h_dtype, const void* top
   const uint8_t* wts[6] = {w1p, w1s, w3p, w3s, w2p, w2s};
   int rc = check_moe_args(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind);
   if (rc) return rc;
-  rc = check_forward_layout(fwd_layout, D, F);
+  rc = check_forward_layout(fwd_layout, D, F, flags);
   if (rc) return rc;
   Lora lo;
   rc = check_lora(lora, lora_scaling, lora_rank, lo);
@@ -732,7 +765,7 @@ int mxfp4_moe_backward_fl(float* grad_h, float* grad_w, const float* grad_out, c
   const uint8_t* wts[6] = {w1p, w1s, w3p, w3s, w2p, w2s};
   int rc = check_moe_args(h, h_dtype, topk_idx, idx_dtype, topk_w, N, k, wts, E, D, F, act_kind);
   if (rc) return rc;
-  rc = check_forward_layout(fwd_layout, D, F);
+  rc = check_forward_layout(fwd_layout, D, F, flags);
   if (rc) return rc;
   Lora lo;
   rc = check_lora(lora, lora_scaling, lora_rank, lo);
@@ -797,6 +830,11 @@ int mxfp4_moe_backward_fl(float* grad_h, float* grad_w, const float* grad_out, c
   b.gw_part = at<float>(workspace, L.gw_part);
   set_buckets(b, workspace, L);
   b.lora_rq = r ? at<float>(workspace, L.l_rq) : nullptr;
+  const bool bl = fwd_layout && (flags & MXFP4_MOE_BWD_LAYOUT);
+  if (bl && fwd_layout[5]) {
+    b.bl0 = fwd_layout[5];
+    b.bl_estride = mx::backward_layout_bytes(D, F);
+  }
   MX_TRY(mx::launch_bwd(b, mx::kBwdDownT, L.max_tiles, stream), "moe_backward: W2 transposed product");
   MX_PHASE("bwd_down_t", stream);
   if (r) {
@@ -829,6 +867,10 @@ int mxfp4_moe_backward_fl(float* grad_h, float* grad_w, const float* grad_out, c
   c.n_ct = (D + mx::kBwdColsPerTile - 1) / mx::kBwdColsPerTile;
   c.y = at<float>(workspace, L.ypair); c.ldy = D;
   set_buckets(c, workspace, L);
+  if (bl && fwd_layout[3] && fwd_layout[4]) {
+    c.bl0 = fwd_layout[3]; c.bl1 = fwd_layout[4];
+    c.bl_estride = mx::backward_layout_bytes(F, D);
+  }
   MX_TRY(mx::launch_bwd(c, mx::kBwdGateUpT, L.max_tiles, stream), "moe_backward: W1|W3 transposed product");
   MX_PHASE("bwd_gateup_t", stream);
   if (r) {  // grad_h = combine + A_gate^T Dsum_gate + A_up^T Dsum_up

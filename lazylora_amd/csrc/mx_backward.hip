@@ -137,7 +137,11 @@ struct Cfg {
   static constexpr int kChunkBytes = kChunk * T * 2 * 1024;
 };
 
-template <int MODE, int T>
+// BL: the weights come from the backward layout (launch_backward_layout): each 32-row step of
+// a stripe is 4 KiB of codes read by four 16-byte loads per lane (each instruction 1 KiB
+// contiguous) and 256 B of scales read by one 8-byte load per lane, instead of eight 8-byte
+// loads from eight rows and eight scale-byte loads.
+template <int MODE, int T, bool BL>
 __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w, uint8_t* abuf)
 {
   constexpr int kRing = Cfg<T>::kRing;
@@ -178,18 +182,43 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
     offs[q] = (uint32_t)(8 * g + q) * cbs + (uint32_t)col_c / kGroup;
   }
 
+  // Backward layout: one buffer resource per segment over the expert's copy (empty for a
+  // stripe past C); the step's block is (step of the segment, stripe), codes first, then the
+  // scales after every block's codes. Steps past the segment's end (padding) read an empty
+  // resource: zero weights.
+  const int bl_nstr = a.C / kBwdColsPerTile;
+  const uint32_t bl_codes = (uint32_t)(a.R / kStepRows) * (uint32_t)bl_nstr * 4096u;
+  const uint32_t bl_size = stripe_ok ? bl_codes + bl_codes / 16 : 0u;
+  const uint8_t* const bl0 = BL ? a.bl0 + (long long)w.expert * a.bl_estride : nullptr;
+  const uint8_t* const bl1 = BL && a.nseg > 1 ? a.bl1 + (long long)w.expert * a.bl_estride : bl0;
+
   auto load_step = [&](int step, StepRaw& r) {
     const int row0 = step * kStepRows;
     const bool seg = a.nseg > 1 && row0 >= a.R;  // uniform
     const int rr = seg ? row0 - a.R : row0;
-    const int rows_left = stripe_ok ? max(a.R - rr, 0) : 0;
-    const rsrc_t W = make_rsrc((seg ? wbase1 : wbase0) + (long long)rr * wpitch, (uint32_t)rows_left * wpitch);
-    const rsrc_t S = make_rsrc((seg ? sbase1 : sbase0) + (long long)rr * cbs, (uint32_t)rows_left * cbs);
+    if constexpr (BL) {
+      const rsrc_t B = make_rsrc(seg ? bl1 : bl0, rr < a.R ? bl_size : 0u);
+      const uint32_t blk = (uint32_t)(rr / kStepRows) * (uint32_t)bl_nstr + (uint32_t)ct;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) r.w[q] = buf8B_nt(W, offw[q]);
+      for (int u = 0; u < 4; ++u) {  // rows 8g + 2u and 8g + 2u + 1, 8 bytes each
+        const i32x4 v = buf16_nt(B, (uint32_t)lane * 16u + (uint32_t)u * 1024u, blk * 4096u);
+        r.w[2 * u] = u32x2{(uint32_t)v[0], (uint32_t)v[1]};
+        r.w[2 * u + 1] = u32x2{(uint32_t)v[2], (uint32_t)v[3]};
+      }
+      const u32x2 sv = buf8B_nt(B, bl_codes + blk * 256u + (uint32_t)(lane >> 1) * 8u);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) r.s[q] = buf8(S, offs[q]);
+      for (int q = 0; q < 8; ++q) r.s[q] = (sv[q >> 2] >> (8 * (q & 3))) & 0xffu;
+    } else {
+      const int rows_left = stripe_ok ? max(a.R - rr, 0) : 0;
+      const rsrc_t W = make_rsrc((seg ? wbase1 : wbase0) + (long long)rr * wpitch, (uint32_t)rows_left * wpitch);
+      const rsrc_t S = make_rsrc((seg ? sbase1 : sbase0) + (long long)rr * cbs, (uint32_t)rows_left * cbs);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) r.w[q] = buf8B_nt(W, offw[q]);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) r.s[q] = buf8(S, offs[q]);
+    }
   };
+  constexpr int kStepLoads = BL ? 5 : 16;  // load instructions per step and lane
 
   // A operands: MFMA lane (i = n, g) takes elements 8g..8g+7 of the step's 32 contraction
   // indices of row i of each tile, hi and lo terms (16 bytes each). The work-group copies them
@@ -248,7 +277,7 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
       // requested: with only those outstanding, this wave's part has landed; the barrier waits
       // for the other waves' parts, and every wave has finished reading the buffer that chunk
       // c + 1 now overwrites (it held chunk c - 1)
-      wait_vm<(kRing * 16 < 63 ? kRing * 16 : 63)>();  // (the counter holds at most 63)
+      wait_vm<(kRing * kStepLoads < 63 ? kRing * kStepLoads : 63)>();  // (the counter holds at most 63)
       __syncthreads();
       const int c = s0 / kChunk;
       if ((c + 1) * kChunk < nsteps_pad) copy_chunk(c + 1);
@@ -392,16 +421,14 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
   static_for<T>(epilogue);
 }
 
-// One wave per work-group. T = 1: one item per wave (the grid covers every item). T > 1: a
-// resident grid that loops over the large-bucket items, so launches with few or no groups cost
-// almost nothing.
-// One work-group of kWaves waves per item; the grid covers every item.
-template <int MODE>
+// One work-group of kWaves waves per item (one row tile x kWaves stripes); the grid covers
+// every item. BL: the weights come from the backward layout.
+template <int MODE, bool BL>
 __global__ __launch_bounds__(64 * kWaves, 2) void bwd_kernel(BwdArgs a)
 {
   __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * Cfg<1>::kChunkBytes];
   WorkItem<1> w;
-  if (decode_work<1>(a, 0, w) == 1) bwd_item<MODE, 1>(a, w, abuf);
+  if (decode_work<1>(a, 0, w) == 1) bwd_item<MODE, 1, BL>(a, w, abuf);
 }
 
 // ---------------------------------------------------------------- large buckets
@@ -745,11 +772,15 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
     b.small_tiles = nullptr;
     b.groups = nullptr;
   }
+  const bool bl = a.bl0 != nullptr && mode != kBwdPlain;
+  if (bl && (!backward_layout_ok(a.R, a.C) || (a.nseg > 1 && !a.bl1))) return hipErrorInvalidValue;
   const long long blocks = (total + 7) / 8 * 8;
   dim3 grid((unsigned)blocks), block(64 * kWaves);
-  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain>), grid, block, 0, s, b);
-  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT>), grid, block, 0, s, b);
-  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT>), grid, block, 0, s, b);
+  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, false>), grid, block, 0, s, b);
+  else if (mode == kBwdDownT && bl) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, true>), grid, block, 0, s, b);
+  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, false>), grid, block, 0, s, b);
+  else if (bl) hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, true>), grid, block, 0, s, b);
+  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, false>), grid, block, 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !split) return e;
   // groups come from experts of at least kGroupMinTiles tiles: at most max_tiles / kGroupMinTiles + 1
@@ -758,6 +789,84 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
   if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_group_kernel<kBwdPlain>), ggrid, block, 0, s, b);
   else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_group_kernel<kBwdDownT>), ggrid, block, 0, s, b);
   else hipLaunchKernelGGL((bwd_group_kernel<kBwdGateUpT>), ggrid, block, 0, s, b);
+  return hipGetLastError();
+}
+
+bool backward_layout_ok(int R, int C)
+{
+  return R > 0 && C > 0 && R % kStepRows == 0 && C % kBwdColsPerTile == 0 &&
+         (long long)R * C / 2 + (long long)R * C / 32 < (1LL << 32);
+}
+
+long long backward_layout_bytes(int R, int C)
+{
+  return backward_layout_ok(R, C) ? (long long)R * C / 2 + (long long)R * C / 32 : 0;
+}
+
+namespace {
+
+// One thread per 16-byte piece of the backward layout of one expert's [R, C] matrix: blocks
+// (step st = 32 rows, stripe c = 256 columns) in order st * nstr + c. Codes: piece (u, l) of
+// block b at b * 4096 + u * 1024 + l * 16 holds, for lane l = 16 g + n, bytes 8n .. 8n + 7 of
+// the stripe in rows 32 st + 8g + 2u and 32 st + 8g + 2u + 1 (8 bytes each), what that lane's
+// four 16-byte loads of the step read. Scales, after every block's codes: the 256 B of block b
+// hold at 8 m + q (m = 8 g + j) the scale byte of row 32 st + 8g + q for MX block 8c + j, the
+// 8 bytes lanes 2m and 2m + 1 (columns 32j .. 32j + 31 of the stripe) read.
+__global__ __launch_bounds__(256) void backward_layout_kernel(const uint8_t* packed, const uint8_t* scales,
+                                                              uint8_t* out, int R, int C, long long per_expert,
+                                                              long long total)
+{
+  const long long p = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (p >= total) return;
+  const int nstr = C / kBwdColsPerTile;
+  const long long e = p / per_expert;
+  long long r = p - e * per_expert;
+  const long long code_pieces = (long long)(R / kStepRows) * nstr * 256;
+  const long long cb = (long long)C / 2, sb = (long long)C / kGroup;
+  if (r < code_pieces) {
+    const int l = (int)(r & 63), u = (int)((r >> 6) & 3);
+    const long long blk = r >> 8;
+    const int st = (int)(blk / nstr), c = (int)(blk - (long long)st * nstr);
+    const int row = st * kStepRows + 8 * (l >> 4) + 2 * u;
+    const uint8_t* src = packed + (e * R + row) * cb + c * 128 + 8 * (l & 15);
+    const u32x2 v0 = *reinterpret_cast<const u32x2*>(src);
+    const u32x2 v1 = *reinterpret_cast<const u32x2*>(src + cb);
+    *reinterpret_cast<i32x4*>(out + p * 16) = i32x4{(int)v0[0], (int)v0[1], (int)v1[0], (int)v1[1]};
+    return;
+  }
+  r -= code_pieces;  // piece k of scale block blk: entries m = 2k, 2k + 1
+  const int k = (int)(r & 15);
+  const long long blk = r >> 4;
+  const int st = (int)(blk / nstr), c = (int)(blk - (long long)st * nstr);
+  uint32_t v[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int m = 2 * k + h, g = m >> 3, j = m & 7;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = st * kStepRows + 8 * g + 4 * half + q;
+        word |= (uint32_t)scales[(e * R + row) * sb + 8 * c + j] << (8 * q);
+      }
+      v[2 * h + half] = word;
+    }
+  }
+  *reinterpret_cast<i32x4*>(out + p * 16) = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+}
+
+}  // namespace
+
+hipError_t launch_backward_layout(const uint8_t* packed, const uint8_t* scales, uint8_t* out, int E, int R, int C,
+                                  hipStream_t s)
+{
+  if (E <= 0) return hipSuccess;
+  if (!backward_layout_ok(R, C)) return hipErrorInvalidValue;
+  const long long per_expert = backward_layout_bytes(R, C) / 16;
+  const long long total = per_expert * E;
+  hipLaunchKernelGGL(backward_layout_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, packed, scales,
+                     out, R, C, per_expert, total);
   return hipGetLastError();
 }
 

@@ -127,6 +127,12 @@ struct BwdArgs {
   const int* n_small;
   const int4* groups;
   const int* n_groups;
+  // Backward layout (launch_backward_layout) of each row segment (W; W1 and W3 for two), or
+  // null: the one-tile work-groups of kBwdDownT / kBwdGateUpT then read it instead of wp / ws
+  // (the large-bucket work-groups keep the checkpoint layout). Needs backward_layout_ok(R, C).
+  const uint8_t* bl0;
+  const uint8_t* bl1;
+  long long bl_estride;  // bytes per expert: backward_layout_bytes(R, C)
 };
 
 constexpr int kFwdRowsPerTile = 16;
@@ -143,6 +149,17 @@ constexpr int kBwdColsPerTile = 256;  // output columns of one transposed-produc
 bool fwd_bucket_split(int R, int K);
 hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s);
 hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s);
+
+// Backward layout: a load-time copy of E stacked MXFP4 matrices [R, C] (codes [R, C/2], E8M0
+// scales [R, C/32]) for the one-tile transposed products. Per expert, blocks (32-row step st,
+// 256-column stripe c) in order st * (C / 256) + c: each block's 4 KiB of codes in the order the
+// lanes of the stripe's wave load them (lane 16g + n, load u: bytes 8n .. 8n + 7 of rows 8g + 2u
+// and 8g + 2u + 1), then, after every block's codes, 256 B of scales per block (8 bytes per lane
+// pair: the scale bytes of rows 8g .. 8g + 7 for the pair's MX block). R % 32 == 0, C % 256 == 0.
+bool backward_layout_ok(int R, int C);
+long long backward_layout_bytes(int R, int C);  // per expert; 0 unless backward_layout_ok(R, C)
+hipError_t launch_backward_layout(const uint8_t* packed, const uint8_t* scales, uint8_t* out, int E, int R, int C,
+                                  hipStream_t s);
 
 // ---------------------------------------------------------------- elementwise / routing
 // Two-term quantisation of activation rows into the AT layout of the work tiles. Tile t slot i

@@ -45,6 +45,7 @@ class ExpertLayer:
         (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s) = [
             _aligned16(t.to(self.device, non_blocking=True).contiguous()) for t in tensors]
         self._fl = None  # forward-layout copies (W1, W3, W2; None where K is not a multiple of 512)
+        self._bl = None  # backward-layout copies (W1, W3, W2; None where the shape does not allow one)
 
     @classmethod
     def empty(cls, E: int, D: int, F: int, device=None) -> "ExpertLayer":
@@ -126,23 +127,74 @@ class ExpertLayer:
         """Forgets the forward-layout copies (the routed calls then read the checkpoint layout)."""
         self._fl = None
 
+    def prepare_backward_layout(self) -> int:
+        """Builds the backward-layout copies of W1, W3 (when D is a multiple of 256) and W2 (when
+        F is), which the routed backward's one-tile transposed products then read with four
+        1 KiB loads of codes and one 512-byte load of scales per 32-row step (eight 8-byte pieces
+        of eight rows and eight scale bytes otherwise; mxfp4_backward_layout; results are
+        bit-identical). Each copy holds the codes and scales it copies: R * (K / 2 + K / 32)
+        bytes per expert; returns the bytes added. Stale copies are detected and dropped like
+        the forward layout's (prepare_forward_layout)."""
+        from lazylora_amd.native import kernel
+
+        k = kernel()
+        if k is None:
+            raise RuntimeError("the backward layout needs the native library on a GPU")
+        w13 = ((k.backward_layout(self.w1p, self.w1s), k.backward_layout(self.w3p, self.w3s)) if self.D % 256 == 0
+               else (None, None))
+        w2 = k.backward_layout(self.w2p, self.w2s) if self.F % 256 == 0 else None
+        self._bl = (w13[0], w13[1], w2)
+        self._bl_versions = self._code_versions()
+        return sum(t.numel() for t in self._bl if t is not None)
+
+    def drop_backward_layout(self) -> None:
+        """Forgets the backward-layout copies (the transposed products then read the checkpoint
+        layout)."""
+        self._bl = None
+
     def _code_versions(self):
         # torch counts in-place writes per tensor (a write through a view counts for its base)
         ts = (self.w1p, self.w1s, self.w3p, self.w3s, self.w2p, self.w2s)
         return tuple(t._version for t in ts) + tuple(t.data_ptr() for t in ts)
 
+    def _fresh(self):
+        """Drops (with a warning) layout copies made before an in-place write to the codes or
+        scales (or a rebinding of the tensors)."""
+        v = self._code_versions()
+        if self._fl is not None and v != self._fl_versions:
+            warnings.warn("expert weights changed after prepare_forward_layout(): the forward-layout copy is dropped "
+                          "(call prepare_forward_layout() again to rebuild it)", RuntimeWarning, stacklevel=4)
+            self._fl = None
+        if self._bl is not None and v != self._bl_versions:
+            warnings.warn("expert weights changed after prepare_backward_layout(): the backward-layout copy is "
+                          "dropped (call prepare_backward_layout() again to rebuild it)", RuntimeWarning,
+                          stacklevel=4)
+            self._bl = None
+
     def forward_layout_pointers(self):
         """Host array of the three forward-layout device pointers for mxfp4_moe_*_fl, or None.
         Copies made before an in-place write to the codes (or a rebinding of the tensors) are
         stale: they are dropped, with a warning, and the call reads the checkpoint layout."""
+        self._fresh()
         if self._fl is None:
             return None
-        if self._code_versions() != self._fl_versions:
-            warnings.warn("expert weights changed after prepare_forward_layout(): the forward-layout copy is dropped "
-                          "(call prepare_forward_layout() again to rebuild it)", RuntimeWarning, stacklevel=3)
-            self._fl = None
-            return None
         return (ctypes.c_void_p * 3)(*[t.data_ptr() if t is not None else None for t in self._fl])
+
+    def layout_pointers(self):
+        """(host pointer array, flags) for mxfp4_moe_*_fl: the three forward-layout pointers (or
+        None), or, with backward-layout copies, six pointers (forward W1, W3, W2, then backward
+        W1, W3, W2) and MXFP4_MOE_BWD_LAYOUT. Stale copies are dropped first, as in
+        forward_layout_pointers."""
+        from lazylora_amd.native import MOE_BWD_LAYOUT
+
+        self._fresh()
+        if self._bl is None:
+            if self._fl is None:
+                return None, 0
+            return (ctypes.c_void_p * 3)(*[t.data_ptr() if t is not None else None for t in self._fl]), 0
+        fl = self._fl if self._fl is not None else (None, None, None)
+        return (ctypes.c_void_p * 6)(*[t.data_ptr() if t is not None else None for t in (*fl, *self._bl)]), \
+            MOE_BWD_LAYOUT
 
     def pointers(self):
         return (self.w1p.data_ptr(), self.w1s.data_ptr(), self.w3p.data_ptr(), self.w3s.data_ptr(),

@@ -250,10 +250,11 @@ def upload(host: HostLayer, dst: ExpertLayer, expert_ids: Optional[Sequence[int]
     """Asynchronous host -> HBM copies of the given experts' rows (all by default) on `stream`
     (the current stream by default), one copy per contiguous run of ids and tensor. Returns the
     bytes enqueued. The host buffers must stay untouched until the copies complete. The layer's
-    forward-layout copies, if any, no longer match and are dropped."""
+    forward- and backward-layout copies, if any, no longer match and are dropped."""
     if (host.E, host.D, host.F) != (dst.E, dst.D, dst.F):
         raise ValueError("host and device layers differ in shape")
     dst.drop_forward_layout()
+    dst.drop_backward_layout()
     runs = [(0, host.E)] if expert_ids is None else _runs(expert_ids)
     total = 0
     with torch.cuda.stream(stream) if stream is not None else _nullcontext():

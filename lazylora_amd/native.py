@@ -36,6 +36,7 @@ _ACTS = {"swiglu": ACT_SWIGLU, "situ": ACT_SITU, "situ_glu": ACT_SITU, ACT_SWIGL
 F32, BF16, I32, I64 = 0, 1, 2, 3
 MOE_SAVE = 1
 MOE_REUSE_FORWARD = 2
+MOE_BWD_LAYOUT = 4
 
 _lib = None
 _kernel = None
@@ -94,6 +95,10 @@ def _load_library() -> ctypes.CDLL:
     lib.mxfp4_forward_layout_bytes.argtypes = [ci, ci, ci]
     lib.mxfp4_forward_layout.restype = ci
     lib.mxfp4_forward_layout.argtypes = [vp, vp, vp, ci, ci, ci, vp]
+    lib.mxfp4_backward_layout_bytes.restype = sz
+    lib.mxfp4_backward_layout_bytes.argtypes = [ci, ci, ci]
+    lib.mxfp4_backward_layout.restype = ci
+    lib.mxfp4_backward_layout.argtypes = [vp, vp, vp, ci, ci, ci, vp]
     lib.mxfp4_moe_route_status.restype = ci
     lib.mxfp4_moe_route_status.argtypes = [vp, vp, vp]
     lib.mxfp4_router_topk.restype = ci
@@ -128,6 +133,16 @@ def _device_for(t: torch.Tensor) -> torch.device:
 
 def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _layouts(experts):
+    """(layout pointer array or None, extra flags) of a layer for the mxfp4_moe_*_fl calls: its
+    load-time layout copies (ExpertLayer.layout_pointers), or none for objects without them."""
+    fn = getattr(experts, "layout_pointers", None)
+    if fn is None:
+        fn = getattr(experts, "forward_layout_pointers", None)
+        return (fn() if fn is not None else None), 0
+    return fn()
 
 
 def _u8(t: torch.Tensor, dev: torch.device, name: str) -> torch.Tensor:
@@ -236,6 +251,31 @@ class MXFP4Kernel:
                self.lib)
         return out
 
+    def backward_layout(self, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+        """The backward layout (mxfp4_backward_layout) of stacked packed matrices [E, R, K/2] uint8
+        and their scales [E, R, K/32] uint8 in HBM, R a multiple of 32 and K of 256: a new flat
+        uint8 tensor on the same device. No counterpart in the reference;
+        ExpertLayer.prepare_backward_layout keeps these for a resident layer."""
+        if packed.dtype != torch.uint8 or packed.dim() != 3 or not packed.is_cuda:
+            raise ValueError("packed must be a CUDA uint8 tensor [E, R, K/2]")
+        E, R, Kh = packed.shape
+        K = 2 * Kh
+        if R % 32 or K % 256:
+            raise ValueError(f"the backward layout needs R a multiple of 32 and K of 256, got R={R}, K={K}")
+        if scales.dtype != torch.uint8 or tuple(scales.shape) != (E, R, K // 32) or scales.device != packed.device:
+            raise ValueError("scales must be a uint8 tensor [E, R, K/32] on the codes' device")
+        src, ssrc = packed.contiguous(), scales.contiguous()
+        if src.data_ptr() % 16:
+            src = src.clone()
+        if ssrc.data_ptr() % 16:
+            ssrc = ssrc.clone()
+        n = int(self.lib.mxfp4_backward_layout_bytes(E, R, K))
+        out = torch.empty(max(n, 16), dtype=torch.uint8, device=packed.device)
+        _check(self.lib.mxfp4_backward_layout(out.data_ptr(), src.data_ptr(), ssrc.data_ptr(), E, R, K,
+                                              _stream(packed.device)),
+               self.lib)
+        return out
+
     # -- routed layer ------------------------------------------------------------------------
     def routed_forward(self, h: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
                        experts, act="swiglu", save_for_backward: bool = False,
@@ -251,10 +291,11 @@ class MXFP4Kernel:
         call = _RoutedCall(self.lib, h, topk_indices, topk_weights, experts, act, workspace)
         lo = _LoraCall(lora, call.dev, call.D, call.F)
         out = torch.empty((call.N, call.D), dtype=torch.float32, device=call.dev)
+        layouts, lflags = _layouts(experts)
         _check(self.lib.mxfp4_moe_forward_fl(
             out.data_ptr(), call.h.data_ptr(), call.h_dtype, call.idx.data_ptr(), call.idx_dtype,
-            call.w.data_ptr(), call.N, call.k, *experts.pointers(), experts.forward_layout_pointers(), experts.E,
-            call.D, call.F, call.act, lo.ptrs, lo.scaling, lo.r, MOE_SAVE if save_for_backward else 0,
+            call.w.data_ptr(), call.N, call.k, *experts.pointers(), layouts, experts.E,
+            call.D, call.F, call.act, lo.ptrs, lo.scaling, lo.r, (MOE_SAVE if save_for_backward else 0) | lflags,
             call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
         return out
 
@@ -281,11 +322,13 @@ class MXFP4Kernel:
         grad_w = torch.empty((call.N, call.k), dtype=torch.float32, device=call.dev)
         grads = [torch.empty_like(t) for t in lo.tensors]
         gptrs = (ctypes.c_void_p * 6)(*[t.data_ptr() for t in grads]) if lo.r else None
+        layouts, lflags = _layouts(experts)
         _check(self.lib.mxfp4_moe_backward_fl(
             grad_h.data_ptr(), grad_w.data_ptr(), g.data_ptr(), call.h.data_ptr(), call.h_dtype,
             call.idx.data_ptr(), call.idx_dtype, call.w.data_ptr(), call.N, call.k, *experts.pointers(),
-            experts.forward_layout_pointers(), experts.E, call.D, call.F, call.act, lo.ptrs, lo.scaling, lo.r, gptrs,
-            MOE_REUSE_FORWARD if reuse_forward else 0, call.ws.data_ptr(), call.nws, _stream(call.dev)), self.lib)
+            layouts, experts.E, call.D, call.F, call.act, lo.ptrs, lo.scaling, lo.r, gptrs,
+            (MOE_REUSE_FORWARD if reuse_forward else 0) | lflags, call.ws.data_ptr(), call.nws,
+            _stream(call.dev)), self.lib)
         if lo.r:
             return grad_h, grad_w, tuple(grads)
         return grad_h, grad_w

@@ -106,6 +106,48 @@ def test_forward_layout_host_checks(lib):
     assert lib.mxfp4_moe_forward_fl(dummy, dummy, 0, dummy, 3, dummy, 0, 2, *([dummy] * 6), ok, *tail0) == 0
 
 
+def test_backward_layout_host_checks(lib):
+    vp = ctypes.c_void_p
+    dummy = vp(256)  # never dereferenced: every call below fails (or finishes) before a launch
+    # per expert R * (K/2 + K/32): the codes and scales, rearranged into (32-row step, 256-column
+    # stripe) blocks
+    assert lib.mxfp4_backward_layout_bytes(2, 64, 512) == 2 * 64 * (256 + 16)
+    assert lib.mxfp4_backward_layout_bytes(2, 40, 512) == 0  # R not a multiple of 32
+    assert lib.mxfp4_backward_layout_bytes(2, 64, 384) == 0  # K not a multiple of 256
+    far = vp(1 << 40)
+    assert lib.mxfp4_backward_layout(dummy, dummy, far, 2, 64, 384, None) == -1
+    assert b"K of 256" in lib.mxfp4_last_error()
+    assert lib.mxfp4_backward_layout(dummy, dummy, far, 2, 40, 512, None) == -1
+    assert lib.mxfp4_backward_layout(None, dummy, far, 2, 64, 512, None) == -1     # null output
+    assert lib.mxfp4_backward_layout(dummy, dummy, None, 2, 64, 512, None) == -1   # null scales
+    assert lib.mxfp4_backward_layout(vp(264), dummy, far, 2, 64, 512, None) == -1  # unaligned output
+    assert lib.mxfp4_backward_layout(dummy, vp(256 + 4096), far, 2, 64, 512, None) == -1  # overlapping codes
+    assert b"overlaps" in lib.mxfp4_last_error()
+    assert lib.mxfp4_backward_layout(dummy, vp(1 << 41), vp(256 + 4096), 2, 64, 512, None) == -1
+    assert b"overlaps" in lib.mxfp4_last_error()
+    assert lib.mxfp4_backward_layout(None, None, None, 0, 64, 512, None) == 0       # E = 0: no-op
+    # the routed calls with MXFP4_MOE_BWD_LAYOUT read six entries: D = 1024, F = 544
+    args = [dummy, dummy, 0, dummy, 3, dummy, 4, 2] + [dummy] * 6
+    tail = [8, 1024, 544, 0, None, None, 0, 4, dummy, 1 << 40, None]
+    bl_w2 = (vp * 6)(None, None, None, None, None, 256)  # W2's K = F = 544 is not a multiple of 256
+    assert lib.mxfp4_moe_forward_fl(*args, bl_w2, *tail) == -1
+    assert b"multiple of 256" in lib.mxfp4_last_error()
+    bl_w1 = (vp * 6)(None, None, None, 256, None, None)  # W1 without W3
+    assert lib.mxfp4_moe_forward_fl(*args, bl_w1, *tail) == -1
+    assert b"together" in lib.mxfp4_last_error()
+    bl_odd = (vp * 6)(None, None, None, 256, 264, None)  # unaligned
+    assert lib.mxfp4_moe_forward_fl(*args, bl_odd, *tail) == -1
+    btail = [8, 1024, 544, 0, None, None, 0, None, 4, dummy, 1 << 40, None]
+    assert lib.mxfp4_moe_backward_fl(dummy, dummy, dummy, dummy, 0, dummy, 3, dummy, 4, 2, *([dummy] * 6),
+                                     bl_w1, *btail) == -1
+    # without the flag only the first three entries are read: the same array passes
+    tail_noflag = [8, 1024, 544, 0, None, None, 0, 0, dummy, 1 << 40, None]
+    assert lib.mxfp4_moe_forward_fl(dummy, dummy, 0, dummy, 3, dummy, 0, 2, *([dummy] * 6), bl_w2,
+                                    *tail_noflag) == 0
+    ok = (vp * 6)(256, 512, None, 768, 1024, None)
+    assert lib.mxfp4_moe_forward_fl(dummy, dummy, 0, dummy, 3, dummy, 0, 2, *([dummy] * 6), ok, *tail) == 0
+
+
 def test_python_api_validation(lib):
     from lazylora_amd import native
     k = native.MXFP4Kernel(lib)  # the shape checks run before any device is needed
@@ -266,4 +308,36 @@ def test_forward_layout_dropped_after_inplace_write():
     with warnings.catch_warnings(record=True):
         warnings.simplefilter("always")
         assert L.forward_layout_pointers() is None
+
+
+def test_layout_pointers_and_stale_backward_layout():
+    """layout_pointers: three forward-layout entries without flags, six entries (forward, then
+    backward) with MXFP4_MOE_BWD_LAYOUT once a backward layout exists; a write to the weights
+    drops both copies."""
+    import warnings
+    from lazylora_amd.experts import ExpertLayer
+    from lazylora_amd.native import MOE_BWD_LAYOUT
+    E, D, F = 2, 512, 512
+    z = lambda *shape: torch.zeros(shape, dtype=torch.uint8)
+    L = ExpertLayer(z(E, F, D // 2), z(E, F, D // 32), z(E, F, D // 2), z(E, F, D // 32), z(E, D, F // 2),
+                    z(E, D, F // 32), device=torch.device("cpu"))
+    assert L.layout_pointers() == (None, 0)
+    L._fl = (z(16), z(16), None)
+    L._fl_versions = L._code_versions()
+    arr, flags = L.layout_pointers()
+    assert flags == 0 and len(arr) == 3 and arr[2] is None
+    L._bl = (z(16), z(16), z(16))
+    L._bl_versions = L._code_versions()
+    arr, flags = L.layout_pointers()
+    assert flags == MOE_BWD_LAYOUT and len(arr) == 6 and arr[0] == L._fl[0].data_ptr()
+    assert arr[3] == L._bl[0].data_ptr() and arr[5] == L._bl[2].data_ptr()
+    L.drop_forward_layout()
+    arr, flags = L.layout_pointers()
+    assert flags == MOE_BWD_LAYOUT and arr[0] is None and arr[4] == L._bl[1].data_ptr()
+    L.w3p.add_(1)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        assert L.layout_pointers() == (None, 0)
+    assert any(issubclass(w.category, RuntimeWarning) for w in caught)
+    assert L._bl is None
 
