@@ -184,8 +184,8 @@ int mxfp4_forward_layout(uint8_t *dst, const uint8_t *packed, const uint8_t *sca
  * mxfp4_backward_layout_bytes(E, R, K) bytes (the codes and scales it copies, rearranged): per
  * expert, 32-row step and 256-element stripe, the 4 KiB of codes that one wave of the transposed
  * products reads, in the order its four 16-byte loads per lane consume them (each instruction
- * reads 1 KiB contiguous instead of 8-byte pieces of eight rows), then the blocks' scales, 256 B
- * each, one 8-byte load per lane (instead of eight scale-byte loads). 0 bytes / MXFP4_EINVAL for
+ * reads 1 KiB contiguous instead of 8-byte or 4-byte pieces of eight rows), then the blocks'
+ * scales, 256 B each, one 8-byte load per lane (instead of eight scale loads). 0 bytes / MXFP4_EINVAL for
  * other shapes. The copy must be rebuilt whenever the weights change. dst, packed and scales:
  * 16-byte aligned, dst overlapping neither. */
 size_t mxfp4_backward_layout_bytes(int E, int R, int K);
@@ -200,7 +200,7 @@ int mxfp4_backward_layout(uint8_t *dst, const uint8_t *packed, const uint8_t *sc
  * mxfp4_backward_layout of w1p, w3p, w2p (again W1 and W3 both or neither; W1 and W3 need D a
  * multiple of 256, W2 needs F a multiple of 256), which the backward's transposed products read
  * (the forward ignores them). Results are bit-identical to the calls without layouts; w1p..w2s
- * are still read (the large-bucket work-groups of the transposed products use them). */
+ * are still read where a product has no layout copy. */
 int mxfp4_moe_forward_fl(float *out, const void *h, int h_dtype, const void *topk_idx,
                          int idx_dtype, const float *topk_w, int N, int k, const uint8_t *w1p,
                          const uint8_t *w1s, const uint8_t *w3p, const uint8_t *w3s,

@@ -471,6 +471,14 @@ struct GStep {
   uint32_t w[8];  // the dword of each row holding this lane's weight bytes
   uint32_t s[8];  // the dword of each row holding this lane's scale byte
 };
+// The same step from the backward layout: the four 16-byte pieces of the lane pair's stripe
+// columns (rows 8g + 2u and 8g + 2u + 1, the lane's dword at 4 (n % 2) of each 8-byte half) and
+// the 8 scale bytes of rows 8g .. 8g + 7. The lane's dwords are picked where they are used, so
+// the loads stay in flight until then.
+struct GStepBL {
+  i32x4 c[4];
+  u32x2 s;
+};
 
 template <int P>
 MX_DEV void gdecode_pair(const uint32_t (&wl)[8], const float (&sf)[8], bf16x8& b0, bf16x8& b1)
@@ -489,7 +497,11 @@ MX_DEV void gdecode_pair(const uint32_t (&wl)[8], const float (&sf)[8], bf16x8& 
   b1 = __builtin_bit_cast(bf16x8, i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]});
 }
 
-template <int MODE>
+// BL: the weights come from the backward layout (see bwd_item): a wave's 128 columns are half
+// of a 256-column block, whose four 16-byte loads per lane give each lane pair its 8 rows x 8
+// bytes (each lane keeps its 4), and one 8-byte load the rows' scale bytes: 5 loads per step
+// instead of 16.
+template <int MODE, bool BL>
 __device__ __forceinline__ void bwd_group_item(const BwdArgs& a, int expert, int t0, int ntl, int cb, uint8_t* abuf,
                                                float* red)
 {
@@ -519,27 +531,48 @@ __device__ __forceinline__ void bwd_group_item(const BwdArgs& a, int expert, int
   const uint8_t* const wbase1 = a.nseg > 1 ? a.wp1 + (long long)expert * a.wp_estride : wbase0;
   const uint8_t* const sbase1 = a.nseg > 1 ? a.ws1 + (long long)expert * a.ws_estride : sbase0;
   const int colc = stripe_ok ? col : 0;
-  // the lane's bytes sit at byte (colc / 2) % 4 of their dword
-  const uint32_t wsh = 8u * (((uint32_t)colc / 2) & 3u);
-  const uint32_t ssh = 8u * (((uint32_t)colc / kGroup) & 3u);
+  // the lane's bytes sit at byte (colc / 2) % 4 of their dword (checkpoint layout; the backward
+  // layout's dwords are the lane's own)
+  const uint32_t wsh = BL ? 0u : 8u * (((uint32_t)colc / 2) & 3u);
+  const uint32_t ssh = BL ? 0u : 8u * (((uint32_t)colc / kGroup) & 3u);
   uint32_t offw[8], offs[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     offw[q] = ((uint32_t)(8 * g + q) * wpitch + (uint32_t)colc / 2) & ~3u;
     offs[q] = ((uint32_t)(8 * g + q) * cbs + (uint32_t)colc / kGroup) & ~3u;
   }
-  auto load_step = [&](int step, GStep& r) {
+  // backward layout: block (step, 256-column stripe c0w / 256), this wave's half of it; the
+  // lane pair's piece and scale entry (see launch_backward_layout)
+  const int bl_nstr = a.C / kBwdColsPerTile;
+  const uint32_t bl_codes = (uint32_t)(a.R / kStepRows) * (uint32_t)bl_nstr * 4096u;
+  const uint32_t bl_size = stripe_ok ? bl_codes + bl_codes / 16 : 0u;
+  const uint8_t* const bl0 = BL ? a.bl0 + (long long)expert * a.bl_estride : nullptr;
+  const uint8_t* const bl1 = BL && a.nseg > 1 ? a.bl1 + (long long)expert * a.bl_estride : bl0;
+  const int half = (c0w / 128) & 1;
+  const uint32_t bl_lane = (uint32_t)(16 * g + 8 * half + (n >> 1)) * 16u;
+  const uint32_t bl_slane = (uint32_t)(8 * g + 4 * half + (n >> 2)) * 8u;
+  const bool odd = (n & 1) != 0;
+  using Step = std::conditional_t<BL, GStepBL, GStep>;
+  auto load_step = [&](int step, Step& r) {
     const int rs = step * kStepRows;
     const bool seg = a.nseg > 1 && rs >= a.R;  // uniform
     const int rr = seg ? rs - a.R : rs;
-    const int rows_left = stripe_ok ? max(a.R - rr, 0) : 0;
-    const rsrc_t W = make_rsrc((seg ? wbase1 : wbase0) + (long long)rr * wpitch, (uint32_t)rows_left * wpitch);
-    const rsrc_t S = make_rsrc((seg ? sbase1 : sbase0) + (long long)rr * cbs, (uint32_t)rows_left * cbs);
+    if constexpr (BL) {
+      const rsrc_t B = make_rsrc(seg ? bl1 : bl0, rr < a.R ? bl_size : 0u);
+      const uint32_t blk = (uint32_t)(rr / kStepRows) * (uint32_t)bl_nstr + (uint32_t)(c0w / kBwdColsPerTile);
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-      r.w[q] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(W, (int)offw[q], 0, 2);
+      for (int u = 0; u < 4; ++u) r.c[u] = buf16_nt(B, bl_lane, blk * 4096u + (uint32_t)u * 1024u);
+      r.s = buf8B_nt(B, bl_codes + blk * 256u + bl_slane);
+    } else {
+      const int rows_left = stripe_ok ? max(a.R - rr, 0) : 0;
+      const rsrc_t W = make_rsrc((seg ? wbase1 : wbase0) + (long long)rr * wpitch, (uint32_t)rows_left * wpitch);
+      const rsrc_t S = make_rsrc((seg ? sbase1 : sbase0) + (long long)rr * cbs, (uint32_t)rows_left * cbs);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) r.s[q] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(S, (int)offs[q], 0, 0);
+      for (int q = 0; q < 8; ++q)
+        r.w[q] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(W, (int)offw[q], 0, 2);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) r.s[q] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(S, (int)offs[q], 0, 0);
+    }
   };
 
   // A chunk copies: unit u = (step in chunk si, tile tt, term) at ((si * T + tt) * 2 + term) KiB;
@@ -573,7 +606,7 @@ __device__ __forceinline__ void bwd_group_item(const BwdArgs& a, int expert, int
 #pragma unroll
     for (int t = 0; t < NC; ++t) acc[tt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  GStep ring[kGRing];
+  Step ring[kGRing];
   copy_chunk(0);
 #pragma unroll
   for (int p = 0; p < kGRing; ++p) {
@@ -582,7 +615,7 @@ __device__ __forceinline__ void bwd_group_item(const BwdArgs& a, int expert, int
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  constexpr int kPerStep = 16;  // vector-memory loads per step and wave
+  constexpr int kPerStep = BL ? 5 : 16;  // vector-memory loads per step and wave
   for (int s0 = 0; s0 < nsteps_pad; s0 += kGRing) {
     if (s0 % kGChunk == 0) {  // uniform; see bwd_item for the protocol
       wait_vm<(kGRing * kPerStep < 63 ? kGRing * kPerStep : 63)>();
@@ -595,21 +628,37 @@ __device__ __forceinline__ void bwd_group_item(const BwdArgs& a, int expert, int
 #pragma unroll
     for (int p = 0; p < kGRing; ++p) {
       const int si = (s0 + p) % kGChunk;
-      GStep& r = ring[p];
+      Step& r = ring[p];
       // pin the step's loaded dwords here, so that nothing computed from them is scheduled into
       // an earlier step (which would wait for this step's loads there)
+      uint32_t rw[8], rs[8];
+      if constexpr (BL) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        asm volatile("" : "+v"(r.w[q]));
-        asm volatile("" : "+v"(r.s[q]));
+        for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(r.c[u]));
+        asm volatile("" : "+v"(r.s));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          rw[2 * u] = (uint32_t)(odd ? r.c[u][1] : r.c[u][0]);
+          rw[2 * u + 1] = (uint32_t)(odd ? r.c[u][3] : r.c[u][2]);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) rs[q] = r.s[q >> 2] >> (8 * (q & 3));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          asm volatile("" : "+v"(r.w[q]));
+          asm volatile("" : "+v"(r.s[q]));
+          rw[q] = r.w[q];
+          rs[q] = r.s[q];
+        }
       }
       uint32_t wl[8];
       float sf[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const uint32_t sc = (r.s[q] >> ssh) & 0xFFu;
+        const uint32_t sc = (rs[q] >> ssh) & 0xFFu;
         const bool dead = sc >= 253u;  // the row's block contributes zero
-        wl[q] = dead ? 0u : r.w[q] >> wsh;
+        wl[q] = dead ? 0u : rw[q] >> wsh;
         sf[q] = bits_f((dead ? 127u : sc) << 23);
       }
       bf16x8 b[NC];
@@ -719,7 +768,7 @@ __device__ __forceinline__ void bwd_group_item(const BwdArgs& a, int expert, int
 
 // Resident grid over the large-bucket items (group, part, column block), dealt round-robin over
 // the XCDs like the one-tile items, so launches with few or no groups cost almost nothing.
-template <int MODE>
+template <int MODE, bool BL>
 __global__ __launch_bounds__(64 * kWaves, MX_BWD_GPER_CU) void bwd_group_kernel(BwdArgs a)
 {
   __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * kGChunkBytes];
@@ -739,7 +788,7 @@ __global__ __launch_bounds__(64 * kWaves, MX_BWD_GPER_CU) void bwd_group_kernel(
     const int ntl = gg[2] - part * kGT;
     if (ntl <= 0) continue;  // the empty part of a short group
     if (busy) __syncthreads();  // every wave has finished reading the previous item's LDS
-    bwd_group_item<MODE>(a, gg[0], gg[1] + part * kGT, min(ntl, kGT), cb, abuf, red);
+    bwd_group_item<MODE, BL>(a, gg[0], gg[1] + part * kGT, min(ntl, kGT), cb, abuf, red);
     busy = true;
   }
 }
@@ -786,9 +835,11 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
   // groups come from experts of at least kGroupMinTiles tiles: at most max_tiles / kGroupMinTiles + 1
   const long long gtotal = ((long long)max_tiles / kGroupMinTiles + 1) * kGParts * ((a.C + kGCols - 1) / kGCols);
   dim3 ggrid((unsigned)std::min<long long>((gtotal + 7) / 8 * 8, resident_groups(MX_BWD_GPER_CU)));
-  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_group_kernel<kBwdPlain>), ggrid, block, 0, s, b);
-  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_group_kernel<kBwdDownT>), ggrid, block, 0, s, b);
-  else hipLaunchKernelGGL((bwd_group_kernel<kBwdGateUpT>), ggrid, block, 0, s, b);
+  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_group_kernel<kBwdPlain, false>), ggrid, block, 0, s, b);
+  else if (mode == kBwdDownT && bl) hipLaunchKernelGGL((bwd_group_kernel<kBwdDownT, true>), ggrid, block, 0, s, b);
+  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_group_kernel<kBwdDownT, false>), ggrid, block, 0, s, b);
+  else if (bl) hipLaunchKernelGGL((bwd_group_kernel<kBwdGateUpT, true>), ggrid, block, 0, s, b);
+  else hipLaunchKernelGGL((bwd_group_kernel<kBwdGateUpT, false>), ggrid, block, 0, s, b);
   return hipGetLastError();
 }
 

@@ -128,8 +128,8 @@ struct BwdArgs {
   const int4* groups;
   const int* n_groups;
   // Backward layout (launch_backward_layout) of each row segment (W; W1 and W3 for two), or
-  // null: the one-tile work-groups of kBwdDownT / kBwdGateUpT then read it instead of wp / ws
-  // (the large-bucket work-groups keep the checkpoint layout). Needs backward_layout_ok(R, C).
+  // null: the work-groups of kBwdDownT / kBwdGateUpT then read it instead of wp / ws. Needs
+  // backward_layout_ok(R, C).
   const uint8_t* bl0;
   const uint8_t* bl1;
   long long bl_estride;  // bytes per expert: backward_layout_bytes(R, C)

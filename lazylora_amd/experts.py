@@ -129,10 +129,9 @@ class ExpertLayer:
 
     def prepare_backward_layout(self) -> int:
         """Builds the backward-layout copies of W1, W3 (when D is a multiple of 256) and W2 (when
-        F is), which the routed backward's one-tile transposed products then read with four
-        1 KiB loads of codes and one 512-byte load of scales per 32-row step (eight 8-byte pieces
-        of eight rows and eight scale bytes otherwise; mxfp4_backward_layout; results are
-        bit-identical). Each copy holds the codes and scales it copies: R * (K / 2 + K / 32)
+        F is), which the routed backward's transposed products then read with four 1 KiB loads
+        of codes and one 512-byte load of scales per wave and 32-row step (sixteen loads of
+        pieces of eight rows otherwise; mxfp4_backward_layout; results are bit-identical). Each copy holds the codes and scales it copies: R * (K / 2 + K / 32)
         bytes per expert; returns the bytes added. Stale copies are detected and dropped like
         the forward layout's (prepare_forward_layout)."""
         from lazylora_amd.native import kernel

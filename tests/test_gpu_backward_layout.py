@@ -1,10 +1,10 @@
 """The backward layout (mxfp4_backward_layout, ExpertLayer.prepare_backward_layout): its bytes
 against a NumPy construction from the definition in include/lazylora_mxfp4.h, and the routed
-backward with it against the same layer without it. The one-tile transposed work-groups read the
-same code and scale bytes from either layout and apply them in the same order (the large-bucket
-work-groups keep the checkpoint layout), so every result is bit-identical: uniform routing, large
-buckets with LoRA, only W1|W3 or only W2 laid out, with and without the forward layout, and at the
-BASELINE config-4 size."""
+backward with it against the same layer without it. The transposed work-groups (one-tile and
+large-bucket) read the same code and scale bytes from either layout and apply them in the same
+order, so every result is bit-identical: uniform routing, large buckets with LoRA, only W1|W3 or
+only W2 laid out, with and without the forward layout, and at the BASELINE config-4 size under
+uniform and Zipf routing."""
 import numpy as np
 import pytest
 import torch
@@ -105,9 +105,9 @@ def test_without_forward_layout(k):
 
 
 def test_routed_layer_large_buckets_and_lora(k):
-    """Buckets of 150, 70, 30 and 6 rows: the large ones take the grouped transposed work-groups
-    (checkpoint layout), the small ones the one-tile work-groups (backward layout); LoRA terms
-    join the W2 epilogue."""
+    """Buckets of 150, 70, 30 and 6 rows: the large ones take the grouped transposed work-groups,
+    the small ones the one-tile work-groups, both reading the backward layout (each its own way);
+    LoRA terms join the W2 epilogue."""
     case("routed layer with/without backward layout, large buckets + LoRA r=8")
     rng = np.random.default_rng(73)
     L = layer_of(oracle.random_experts(rng, 4, 1024, 512, 118, 122))
