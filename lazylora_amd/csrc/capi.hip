@@ -716,12 +716,21 @@ int mxfp4_moe_forward_fl(float* out, const void* h, int h_dtype, const void* top
   a.tiles = at<int4>(workspace, L.tiles); a.n_tiles = at<int>(workspace, L.meta);
   a.n_ct = (D + mx::kFwdColsPerTile - 1) / mx::kFwdColsPerTile;
   a.y = at<float>(workspace, L.ypair); a.ldy = D;
+  // top-1 routing without LoRA: each token has at most one row, which the down product writes
+  // straight into out (already weighted); only tokens with no row need their zeros
+  const bool direct = k == 1 && !lo.r;
+  if (direct) {
+    a.y = out;
+    a.y_rows = at<int>(workspace, L.pair_token);
+  }
   a.row_w = at<float>(workspace, L.pair_w);
   set_buckets(a, workspace, L);
   a.wcounter = at<int>(workspace, L.meta) + 10;
   MX_TRY(mx::launch_fwd(a, mx::kFwdDown, L.max_tiles, stream), "moe_forward: down product");
   MX_PHASE("fwd_down", stream);
-  if (lo.r) {  // out = combine + s_down B_down V, V = sum over the token's slots of w A_down act
+  if (direct) {
+    MX_TRY(mx::launch_zero_unrouted(out, D, D, at<int>(workspace, L.pair_of), N, stream), "moe_forward: unrouted rows");
+  } else if (lo.r) {  // out = combine + s_down B_down V, V = sum over the token's slots of w A_down act
     const mx::LoraFactor fb = kmajor(lo.m[5], lo.r, lo.sd);
     MX_TRY(mx::launch_lora_combine(out, at<float>(workspace, L.ypair), D, at<int>(workspace, L.pair_of), N, k, D,
                                    at<float>(workspace, L.l_vsum), lo.r, 1, &fb, nullptr, nullptr, 0, stream),

@@ -327,7 +327,8 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
     const int r = it * 4 + wave;
     if (r >= w.nrows) continue;
     const f32x4 val = *reinterpret_cast<const f32x4*>(ss + r * kStagePitch + lane * 4);
-    float* yr = a.y + (long long)(w.row0 + r) * a.ldy;
+    const int orow = a.y_rows ? a.y_rows[w.row0 + r] : w.row0 + r;
+    float* yr = a.y + (long long)orow * a.ldy;
     if (vec && col + 4 <= a.R) {
       __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(yr + col));
     } else {
@@ -390,7 +391,7 @@ __device__ __forceinline__ void epilogue_direct(const FwdArgs& a, const WorkItem
     if (i >= w.nrows) continue;
     const int row = w.row0 + i;
     const float wv = MODE == kFwdDown ? tw[v] : 1.0f;
-    float* yr = a.y + (long long)row * a.ldy;
+    float* yr = a.y + (long long)(a.y_rows ? a.y_rows[row] : row) * a.ldy;
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
       const int col = w.ct * kFwdColsPerTile + grp * 16 + j;

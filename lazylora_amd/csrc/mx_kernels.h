@@ -38,6 +38,7 @@ struct FwdArgs {
   // outputs
   float* y;
   long long ldy;
+  const int* y_rows;     // output row of each row (null: the row itself; top-1 routing writes tokens)
   const float* row_w;    // kFwdDown: combine weight per row
   uint8_t* q_tiles;      // kFwdGateUp: act in the AT layout with K = R (= F), same tiles
   float* save;           // kFwdGateUp: [rows, 2R] gate | up in fp32, or null
@@ -201,6 +202,9 @@ hipError_t launch_route(const void* topk_idx, int idx64, const float* topk_w, in
                         int4* wgroups, int* meta, int* pair_token, float* pair_w, int* pair_of, hipStream_t s);
 hipError_t launch_combine(float* out, const float* ypair, long long ldy, const int* pair_of, int N, int k,
                           int D, hipStream_t s);
+// Top-1 routing (the down product writes token rows itself): zeros into the rows of tokens with no
+// pair (pair_of[t] < 0, an id outside [0, E)).
+hipError_t launch_zero_unrouted(float* out, long long ldo, int D, const int* pair_of, int N, hipStream_t s);
 hipError_t launch_combine_bwd(float* grad_h, float* grad_w, const float* dxpair, long long ldy,
                               const float* gw_part, int n_ct, const int* pair_of, int N, int k, int D,
                               hipStream_t s);

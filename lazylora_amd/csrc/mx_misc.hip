@@ -479,6 +479,23 @@ MX_DEV float4 slot_sum4(const float* rows, long long ld, const int* slots, int k
   return make_float4(acc[0], acc[1], acc[2], acc[3]);
 }
 
+// Top-1 routing writes each token's row straight from the down product; a token whose id was
+// outside [0, E) has no pair row and gets zeros here instead (one work-group per 64 tokens; rows
+// are written only for such tokens).
+__global__ __launch_bounds__(256) void zero_unrouted_kernel(float* out, long long ldo, int D, const int* pair_of,
+                                                            int N)
+{
+  const int t0 = blockIdx.x * 64;
+  const int t = t0 + (int)(threadIdx.x & 63);
+  const bool bad = t < N && pair_of[t] < 0;
+  uint64_t m = __builtin_amdgcn_ballot_w64(bad);  // the same in every wave
+  while (m) {
+    const int r = t0 + __builtin_ctzll(m);
+    m &= m - 1;
+    for (int d = threadIdx.x; d < D; d += 256) out[(long long)r * ldo + d] = 0.f;
+  }
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(float* out, const float* ypair, long long ldy,
                                                       const int* pair_of, int N, int k, int D)
 {
@@ -672,6 +689,13 @@ hipError_t launch_combine(float* out, const float* ypair, long long ldy, const i
   if (N == 0 || D == 0) return hipSuccess;
   dim3 grid((unsigned)((D / 4 + 255) / 256), (unsigned)N), block(256);
   hipLaunchKernelGGL(combine_kernel, grid, block, 0, s, out, ypair, ldy, pair_of, N, k, D);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_unrouted(float* out, long long ldo, int D, const int* pair_of, int N, hipStream_t s)
+{
+  if (N <= 0 || D <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_unrouted_kernel, dim3((unsigned)((N + 63) / 64)), dim3(256), 0, s, out, ldo, D, pair_of, N);
   return hipGetLastError();
 }
 

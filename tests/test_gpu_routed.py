@@ -269,6 +269,41 @@ def test_invalid_ids(k):
     assert torch.allclose(out, ref, rtol=1e-6, atol=1e-6)
 
 
+def test_top1_rows_written_directly(k):
+    """Top-1 routing without LoRA: the down product writes each token's row into out itself (no
+    combine), and tokens whose id is outside [0, E) get zero rows (out starts as garbage)."""
+    case("top-1 routing: rows written by the down product, unrouted tokens zeroed")
+    rng = np.random.default_rng(18)
+    ex = oracle.random_experts(rng, 8, 512, 256, 119, 123)
+    L = layer_of(ex)
+    N = 70
+    hn = rng.standard_normal((N, 512)).astype(np.float32)
+    h = torch.from_numpy(hn).cuda()
+    idx = rng.integers(0, 8, (N, 1)).astype(np.int64)
+    idx[:20, 0] = 5  # one bucket of more than 16 rows
+    idx[3, 0], idx[41, 0] = -1, 8
+    w = rng.uniform(0.5, 1.5, (N, 1)).astype(np.float32)
+    ws = torch.empty(k.moe_workspace_bytes(N, 1, 8, 512, 256), dtype=torch.uint8, device="cuda")
+    ws.fill_(0x7F)
+    out = k.routed_forward(h, torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda(), L, workspace=ws)
+    assert k.route_status(ws) & 1
+    assert torch.count_nonzero(out[3]) == 0 and torch.count_nonzero(out[41]) == 0
+    keep = idx.copy()
+    keep[3, 0] = keep[41, 0] = 0
+    wk = w.copy()
+    wk[3, 0] = wk[41, 0] = 0
+    want = oracle.routed_forward(hn, keep, wk, ex, "swiglu")
+    got = out.cpu().numpy()
+    ok = np.ones(N, bool)
+    ok[[3, 41]] = False
+    assert_close(got[ok], want[ok], "top-1 direct rows")
+    # against the same layer through top-2 with a zero-weight second slot (combined by the combine)
+    idx2 = np.concatenate([keep, keep], axis=1)
+    w2 = np.concatenate([wk, np.zeros_like(wk)], axis=1)
+    two = k.routed_forward(h, torch.from_numpy(idx2).cuda(), torch.from_numpy(w2).cuda(), L).cpu().numpy()
+    assert np.array_equal(got[ok], two[ok])
+
+
 def test_autograd_node(k):
     case("RoutedExpertsFunction through torch.autograd")
     from lazylora_amd.routed import RoutedExpertsFunction
