@@ -41,29 +41,45 @@ constexpr int kStepRows = 32;
 typedef const __attribute__((address_space(4))) int* cint_ptr;
 
 constexpr int kWaves = 4;  // waves (stripes) per work-group
+// One-tile items of eight stripes (eight waves, one work-group per CU): the tile's A operands are
+// copied once for 2048 columns instead of once per 1024. Used for the W2 transposed product from
+// the backward layout (C a multiple of 8 stripes) when the launch has at least kWideMinItems such
+// items; fewer would leave CUs idle that four-stripe items (two work-groups per CU) keep busy.
+constexpr int kWideWaves = 8;
+constexpr int kWideMinItems = 512;
 
-// One work item: the kWaves stripes from kWaves * ct4 on of up to T row tiles of one expert
-// (T = 1: a small-bucket tile; T > 1: part of a large-bucket group, whose tiles share every
-// decoded operand).
+// One work item: the NW stripes from NW * ct4 on of up to T row tiles of one expert (T = 1: a
+// small-bucket tile; T > 1: part of a large-bucket group, whose tiles share every decoded
+// operand).
 template <int T>
 struct WorkItem {
   int expert, ct4, ntl;
   int row0[T], nrows[T];
 };
 
-// Work item `it` of this work-group (items are dealt round-robin over the XCDs, blockIdx % 8, each
-// XCD taking one contiguous run, in strides of the grid, so the stripe blocks of one tile, which
-// read the same A rows, run on one XCD). Returns 0 when there is none left, 1 for an item.
-template <int T>
+// The one-tile work list: the small-bucket tiles (with no large-bucket groups, every tile in
+// order), read through the constant address space.
+__device__ __forceinline__ bool use_small_list(const BwdArgs& a)
+{
+  return a.small_tiles && *(cint_ptr)a.n_groups > 0;
+}
+__device__ __forceinline__ int one_tile_count(const BwdArgs& a)
+{
+  return use_small_list(a) ? *(cint_ptr)a.n_small
+                           : a.tiles ? *(cint_ptr)a.n_tiles : (a.M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
+}
+
+// Work item `it` of this work-group among items of NW stripes (items are dealt round-robin over
+// the XCDs, blockIdx % 8, each XCD taking one contiguous run, in strides of the grid, so the stripe
+// blocks of one tile, which read the same A rows, run on one XCD). Returns 0 when there is none
+// left, 1 for an item.
+template <int T, int NW>
 __device__ __forceinline__ int decode_work(const BwdArgs& a, int it, WorkItem<T>& w)
 {
-  // the tile lists are only read here: scalar loads through the constant address space
   static_assert(T == 1, "large buckets take bwd_group_kernel");
-  // with no large-bucket groups the small-bucket list is every tile in order: skip it
-  const bool use_small = a.small_tiles && *(cint_ptr)a.n_groups > 0;
-  const int count = use_small ? *(cint_ptr)a.n_small
-                              : a.tiles ? *(cint_ptr)a.n_tiles : (a.M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
-  const int n_ct4 = (a.n_ct + kWaves - 1) / kWaves;
+  const bool use_small = use_small_list(a);
+  const int count = one_tile_count(a);
+  const int n_ct4 = (a.n_ct + NW - 1) / NW;
   const int total = count * n_ct4;
   const int per_xcd = (total + 7) >> 3;
   const int slot = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
@@ -141,7 +157,7 @@ struct Cfg {
 // a stripe is 4 KiB of codes read by four 16-byte loads per lane (each instruction 1 KiB
 // contiguous) and 256 B of scales read by one 8-byte load per lane, instead of eight 8-byte
 // loads from eight rows and eight scale-byte loads.
-template <int MODE, int T, bool BL>
+template <int MODE, int T, bool BL, int NW>
 __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w, uint8_t* abuf)
 {
   constexpr int kRing = Cfg<T>::kRing;
@@ -151,7 +167,7 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int ct = w.ct4 * kWaves + wave;  // this wave's stripe
+  const int ct = w.ct4 * NW + wave;  // this wave's stripe
   const bool stripe_ok = ct < a.n_ct;    // uniform: stripes past C only help with the A copies
   const int c0 = ct * kBwdColsPerTile;
   const int rtot = a.nseg * a.R;
@@ -238,9 +254,10 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
   // drain every load in flight at each barrier); each chunk is waited for explicitly.
   auto copy_chunk = [&](int chunk) {
     uint8_t* dst = abuf + (chunk & 1) * kChunkBytes;
+    static_assert(kChunk * T * 2 % NW == 0, "the A units split evenly over the waves");
 #pragma unroll
-    for (int k = 0; k < kChunk * T * 2 / kWaves; ++k) {
-      const int u = k * kWaves + wave;
+    for (int k = 0; k < kChunk * T * 2 / NW; ++k) {
+      const int u = k * NW + wave;
       const int si = u / (2 * T), tt = (u >> 1) % T, term = u & 1;
       const int so = min(chunk * kChunk + si, nsteps - 1) * kStepRows;
       // select tile tt's pointer without indexing (keeps pa in registers)
@@ -422,13 +439,27 @@ __device__ __forceinline__ void bwd_item(const BwdArgs& a, const WorkItem<T>& w,
 }
 
 // One work-group of kWaves waves per item (one row tile x kWaves stripes); the grid covers
-// every item. BL: the weights come from the backward layout.
+// every item. With `wide` the launch has an eight-stripe companion (bwd_wide_kernel) and each
+// kernel runs only when its item count suits it: this one when there are fewer than
+// kWideMinItems eight-stripe items. BL: the weights come from the backward layout.
 template <int MODE, bool BL>
-__global__ __launch_bounds__(64 * kWaves, 2) void bwd_kernel(BwdArgs a)
+__global__ __launch_bounds__(64 * kWaves, 2) void bwd_kernel(BwdArgs a, int wide)
 {
   __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * Cfg<1>::kChunkBytes];
+  if (wide && one_tile_count(a) * ((a.n_ct + kWideWaves - 1) / kWideWaves) >= kWideMinItems) return;
   WorkItem<1> w;
-  if (decode_work<1>(a, 0, w) == 1) bwd_item<MODE, 1, BL>(a, w, abuf);
+  if (decode_work<1, kWaves>(a, 0, w) == 1) bwd_item<MODE, 1, BL, kWaves>(a, w, abuf);
+}
+
+// The same items with eight stripes (one work-group per CU; the grid covers every item); it runs
+// only when there are at least kWideMinItems of them (else bwd_kernel takes the launch's items).
+template <int MODE, bool BL>
+__global__ __launch_bounds__(64 * kWideWaves, 1) void bwd_wide_kernel(BwdArgs a)
+{
+  __shared__ __attribute__((aligned(16))) uint8_t abuf[2 * Cfg<1>::kChunkBytes];
+  if (one_tile_count(a) * ((a.n_ct + kWideWaves - 1) / kWideWaves) < kWideMinItems) return;
+  WorkItem<1> w;
+  if (decode_work<1, kWideWaves>(a, 0, w) == 1) bwd_item<MODE, 1, BL, kWideWaves>(a, w, abuf);
 }
 
 // ---------------------------------------------------------------- large buckets
@@ -823,14 +854,26 @@ hipError_t launch_bwd(const BwdArgs& a, int mode, int max_tiles, hipStream_t s)
   }
   const bool bl = a.bl0 != nullptr && mode != kBwdPlain;
   if (bl && (!backward_layout_ok(a.R, a.C) || (a.nseg > 1 && !a.bl1))) return hipErrorInvalidValue;
-  const long long blocks = (total + 7) / 8 * 8;
+  // the W2 transposed product with whole eight-stripe items: both kernels are launched, and the
+  // routing's tile count (on the device) decides which of them does the work
+  const long long witems = (long long)max_tiles * (a.n_ct / kWideWaves);
+  const int wide = mode == kBwdDownT && bl && a.n_ct % kWideWaves == 0 && witems >= kWideMinItems;
+  long long blocks = (total + 7) / 8 * 8;
+  if (wide)  // bwd_kernel then runs only with fewer than kWideMinItems wide items: twice as many of its own
+    blocks = (std::min<long long>(total, 2LL * kWideMinItems) + 7) / 8 * 8;
   dim3 grid((unsigned)blocks), block(64 * kWaves);
-  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, false>), grid, block, 0, s, b);
-  else if (mode == kBwdDownT && bl) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, true>), grid, block, 0, s, b);
-  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, false>), grid, block, 0, s, b);
-  else if (bl) hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, true>), grid, block, 0, s, b);
-  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, false>), grid, block, 0, s, b);
+  if (mode == kBwdPlain) hipLaunchKernelGGL((bwd_kernel<kBwdPlain, false>), grid, block, 0, s, b, 0);
+  else if (mode == kBwdDownT && bl) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, true>), grid, block, 0, s, b, wide);
+  else if (mode == kBwdDownT) hipLaunchKernelGGL((bwd_kernel<kBwdDownT, false>), grid, block, 0, s, b, wide);
+  else if (bl) hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, true>), grid, block, 0, s, b, 0);
+  else hipLaunchKernelGGL((bwd_kernel<kBwdGateUpT, false>), grid, block, 0, s, b, 0);
   hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (wide) {
+    dim3 wgrid((unsigned)((witems + 7) / 8 * 8)), wblock(64 * kWideWaves);
+    hipLaunchKernelGGL((bwd_wide_kernel<kBwdDownT, true>), wgrid, wblock, 0, s, b);
+    e = hipGetLastError();
+  }
   if (e != hipSuccess || !split) return e;
   // groups come from experts of at least kGroupMinTiles tiles: at most max_tiles / kGroupMinTiles + 1
   const long long gtotal = ((long long)max_tiles / kGroupMinTiles + 1) * kGParts * ((a.C + kGCols - 1) / kGCols);
