@@ -2,9 +2,9 @@
 //
 // Each wave computes one 16-row x 64-column output tile over the whole K range
 // (kFwdGateUp: 16 rows x 32 gate features + the same 32 up features). A work-group holds the
-// four waves of four neighbouring column tiles of the same row tile: they share the tile's
-// activations, which the work-group copies into LDS once per super-chunk. Every weight byte
-// is read once per row tile.
+// four waves of four neighbouring column tiles of the same row tile (eight for the down product
+// from a forward layout): they share the tile's activations, which the work-group copies into
+// LDS once per super-chunk. Every weight byte is read once per row tile.
 //
 // Per super-chunk c (512 K elements) and lane (j = lane % 16, g = lane / 16), for each of the
 // 4 column groups of 16 weight rows:
@@ -48,7 +48,7 @@ struct FwdLds {
 
 struct WorkItem {
   int tile, expert, row0, nrows, ct;
-  int ct0;      // first column tile of the work-group (its four waves take ct0 .. ct0 + 3)
+  int ct0;      // first column tile of the work-group (its NW waves take ct0 .. ct0 + NW - 1)
   bool active;  // false: this wave's column tile is past the end; it only helps with the copies
 };
 
@@ -60,7 +60,7 @@ typedef const __attribute__((address_space(4))) int* cint_ptr;
 
 __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tiles, const int* small_tiles,
                                             const int* n_small, const int* n_groups, int M, int n_ct, int wave,
-                                            int it, WorkItem& w)
+                                            int it, WorkItem& w, int nw = kWavesPerGroup)
 {
   // The tile lists are written before this kernel and only read here: scalar loads through the
   // constant address space, which do not wait for this work-group's outstanding stores.
@@ -68,7 +68,7 @@ __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tile
   const bool use_small = small_tiles && *(cint_ptr)n_groups > 0;
   const int ntiles = use_small ? *(cint_ptr)n_small
                                : tiles ? *(cint_ptr)n_tiles : (M + kFwdRowsPerTile - 1) / kFwdRowsPerTile;
-  const int n_cg = (n_ct + kWavesPerGroup - 1) / kWavesPerGroup;
+  const int n_cg = (n_ct + nw - 1) / nw;
   const int total = ntiles * n_cg;
   const int per_xcd = (total + 7) >> 3;
   const int k = (int)(blockIdx.x >> 3) + it * (int)(gridDim.x >> 3);
@@ -77,7 +77,7 @@ __device__ __forceinline__ bool decode_work(const int4* tiles, const int* n_tile
   const int i = item / n_cg;
   const int t = use_small ? ((cint_ptr)small_tiles)[i] : i;
   w.tile = t;
-  w.ct0 = (item - i * n_cg) * kWavesPerGroup;
+  w.ct0 = (item - i * n_cg) * nw;
   const int ct = w.ct0 + wave;
   w.active = ct < n_ct;
   w.ct = w.active ? ct : n_ct - 1;
@@ -222,14 +222,14 @@ struct ASrc {
   }
 };
 
-// Epilogue of the fast path. The four waves stage the work-group's outputs in the (now idle)
+// Epilogue of the fast path. The waves stage the work-group's outputs in the (now idle)
 // activation buffers of LDS, then write them with 16-byte stores that cover whole runs of
 // memory: scattered 1-byte and 4-byte stores of the same data cost the weight stream about a
 // tenth of its bandwidth. The stores are non-temporal (streamed past the caches), which costs the
 // weight stream less than ordinary write-back stores. Lane (j, g) holds rows 4g+v (v = 0..3) of columns grp*16 + j.
 constexpr int kStagePitch = 260;  // floats per staged row: 256 + 4 keeps the row starts on distinct banks
 
-template <int MODE>
+template <int MODE, int NW = kWavesPerGroup>
 __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem& w, int wave, int lane,
                                                 const f32x4 (&acc)[4], const float (&tw)[4], FwdLds& lds)
 {
@@ -311,30 +311,35 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
     return;
   }
 
-  // kFwdPlain / kFwdDown: [row][256 columns of the work-group] fp32
+  // kFwdPlain / kFwdDown: [row][64 NW columns of the work-group] fp32
+  constexpr int kPitch = NW * 64 + 4;
+  static_assert(16 * kPitch * 4 <= (int)sizeof(lds.a), "the staged rows fit the activation buffers");
   float* ss = reinterpret_cast<float*>(lds.a[0]);
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const float wv = MODE == kFwdDown ? tw[v] : 1.0f;
 #pragma unroll
-    for (int grp = 0; grp < 4; ++grp) ss[(4 * g + v) * kStagePitch + wave * 64 + grp * 16 + j] = acc[grp][v] * wv;
+    for (int grp = 0; grp < 4; ++grp) ss[(4 * g + v) * kPitch + wave * 64 + grp * 16 + j] = acc[grp][v] * wv;
   }
   __syncthreads();
-  const int col = w.ct0 * kFwdColsPerTile + lane * 4;
   const bool vec = ((a.ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int r = it * 4 + wave;
+  for (int it = 0; it < 16 / NW; ++it) {
+    const int r = it * NW + wave;
     if (r >= w.nrows) continue;
-    const f32x4 val = *reinterpret_cast<const f32x4*>(ss + r * kStagePitch + lane * 4);
     const int orow = a.y_rows ? a.y_rows[w.row0 + r] : w.row0 + r;
     float* yr = a.y + (long long)orow * a.ldy;
-    if (vec && col + 4 <= a.R) {
-      __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(yr + col));
-    } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (col + e < a.R) yr[col + e] = val[e];
+    for (int h = 0; h < NW / 4; ++h) {
+      const int col = w.ct0 * kFwdColsPerTile + h * 256 + lane * 4;
+      const f32x4 val = *reinterpret_cast<const f32x4*>(ss + r * kPitch + h * 256 + lane * 4);
+      if (vec && col + 4 <= a.R) {
+        __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(yr + col));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (col + e < a.R) yr[col + e] = val[e];
+      }
     }
   }
 }
@@ -403,9 +408,13 @@ __device__ __forceinline__ void epilogue_direct(const FwdArgs& a, const WorkItem
 
 // One work item: the 16 x 64 tile (w.tile, w.ct) over all of K, then its epilogue.
 // FL: the weights come from the forward layout (fl0 / fl1), one 1 KiB block per load instruction
-template <int MODE, bool FAST, bool FL>
+// NW waves per work-group (column tiles per item): 4, or 8 for the down product from the forward
+// layout, whose work-groups then hold a CU alone and copy each tile's activations once per
+// 512 output columns instead of once per 256.
+template <int MODE, bool FAST, bool FL, int NW = kWavesPerGroup>
 __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, int wave, int lane)
 {
+  static_assert(NW == kWavesPerGroup || (FL && MODE == kFwdDown), "eight waves: the down product's forward layout path");
   static_assert(FAST || !FL, "the forward layout is read by the fast path only");
   __shared__ FwdLds lds;  // used by the fast path only
   const int j = lane & 15, g = lane >> 4;
@@ -478,8 +487,8 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
     // XT, the lanes' plane-0 dwords at 4 l and plane-1 dwords at 256 + 4 l
     auto issue_a = [&](int c, int buf) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int unit = 4 * wave + u;
+      for (int u = 0; u < 16 / NW; ++u) {
+        const int unit = (16 / NW) * wave + u;
         dma16_async(as.unit(c, unit), &lds.a[buf][unit * 1024]);
       }
       if (wave == 0) {
@@ -699,27 +708,27 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
 
   if constexpr (FAST) {
     __syncthreads();  // every wave is done with the last chunk's LDS data
-    epilogue_staged<MODE>(a, w, wave, lane, acc, tw, lds);
+    epilogue_staged<MODE, NW>(a, w, wave, lane, acc, tw, lds);
     return;
   }
 
   if (w.active) epilogue_direct<MODE>(a, w, lane, acc, tw);
 }
 
-template <int MODE, bool FAST, bool FL>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(FwdArgs a)
+template <int MODE, bool FAST, bool FL, int NW = kWavesPerGroup>
+__global__ __launch_bounds__(64 * NW, NW == kWavesPerGroup ? 2 : 1) void fwd_kernel(FwdArgs a)
 {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps control flow scalar
   WorkItem w;
-  for (int it = 0; decode_work(a.tiles, a.n_tiles, a.small_tiles, a.n_small, a.n_groups, a.M, a.n_ct, wave, it, w); ++it) {
+  for (int it = 0; decode_work(a.tiles, a.n_tiles, a.small_tiles, a.n_small, a.n_groups, a.M, a.n_ct, wave, it, w, NW); ++it) {
     // the previous item's reads of LDS are complete before this item's copies land there;
     // its output stores drain while this item's first loads are in flight
     if (FAST && it > 0) __syncthreads();
     // recompute lane-derived addresses per item instead of holding them across items
     int l = lane;
     asm volatile("" : "+v"(l));
-    fwd_item<MODE, FAST, FL>(a, w, wave, l);
+    fwd_item<MODE, FAST, FL, NW>(a, w, wave, l);
   }
 }
 
@@ -1271,6 +1280,9 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   const long long total = (long long)max_tiles * n_cg;
   if (total <= 0) return hipSuccess;
   const long long blocks = std::min<long long>((total + 7) / 8 * 8, resident_groups());
+  // the down product from the forward layout: eight column tiles per work-group, one per CU
+  const long long n_cg8 = (a.n_ct + 7) / 8;
+  const long long blocks8 = std::min<long long>(((long long)max_tiles * n_cg8 + 7) / 8 * 8, resident_groups() / 16 * 8);
   const bool fast = fast_path(a.R, a.K);
   // the bucket split needs the tile list and the fast path; otherwise every tile takes fwd_kernel
   const bool split = fwd_bucket_split(a.R, a.K) && a.tiles && a.small_tiles && a.groups;
@@ -1293,7 +1305,9 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
     else if (fast) MX_LAUNCH(kFwdGateUp, true, false);
     else MX_LAUNCH(kFwdGateUp, false, false);
   } else {
-    if (fl) MX_LAUNCH(kFwdDown, true, true);
+    if (fl && a.n_ct % 8 == 0)
+      hipLaunchKernelGGL((fwd_kernel<kFwdDown, true, true, 8>), dim3((unsigned)blocks8), dim3(512), 0, s, b);
+    else if (fl) MX_LAUNCH(kFwdDown, true, true);
     else if (fast) MX_LAUNCH(kFwdDown, true, false);
     else MX_LAUNCH(kFwdDown, false, false);
   }
