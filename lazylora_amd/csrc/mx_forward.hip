@@ -236,10 +236,15 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
   const int j = lane & 15, g = lane >> 4;
   const int t = wave * 64 + lane;
   if (MODE == kFwdGateUp) {
-    // act codes: [q = wave][plane][half][row 0..15][16 B] then scales [row][plane][q]; this is
-    // the AT byte order of the work-group's 128 features (super-chunk c, block group gl)
-    uint8_t* sq = lds.a[0];
-    float* ss = reinterpret_cast<float*>(lds.a[1]);  // [row][gate 128 | up 128] fp32
+    // Each group of four waves (half h of an eight-wave work-group) stages 128 features:
+    // act codes [q = wave % 4][plane][half][row 0..15][16 B] then scales [row][plane][q], the AT
+    // byte order of those features (super-chunk c, block group gl), and gate|up fp32 rows
+    // [row][gate 128 | up 128]; half 1 (eight waves, forward layout) stages its rows in the
+    // scale-window LDS, which the forward layout leaves unused.
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
+    const int h = NW == 8 ? wave >> 2 : 0, wq = wave & 3;
+    uint8_t* sq = lds.a[0] + h * 4608;
+    float* ss = reinterpret_cast<float*>(h == 0 ? lds.a[1] : lds.s[0]);
     const int F = a.R;
     // LoRA gate/up delta of each row's token: the four rows' token indices, then their sixteen
     // delta values, each requested together (two round trips to memory rather than eight)
@@ -270,16 +275,16 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
       }
       Quant2 q = quant2_block16(glu_fwd(ga, ua, a.act_kind), glu_fwd(gb, ub, a.act_kind));
       if (!w.active) q = Quant2{0, 0, 0, 0};  // features past F: the padding of the layout is zero
-      sq[((wave * 2 + 0) * 2 + 0) * 256 + i * 16 + j] = (uint8_t)q.hi;
-      sq[((wave * 2 + 0) * 2 + 1) * 256 + i * 16 + j] = (uint8_t)(q.hi >> 8);
-      sq[((wave * 2 + 1) * 2 + 0) * 256 + i * 16 + j] = (uint8_t)q.lo;
-      sq[((wave * 2 + 1) * 2 + 1) * 256 + i * 16 + j] = (uint8_t)(q.lo >> 8);
+      sq[((wq * 2 + 0) * 2 + 0) * 256 + i * 16 + j] = (uint8_t)q.hi;
+      sq[((wq * 2 + 0) * 2 + 1) * 256 + i * 16 + j] = (uint8_t)(q.hi >> 8);
+      sq[((wq * 2 + 1) * 2 + 0) * 256 + i * 16 + j] = (uint8_t)q.lo;
+      sq[((wq * 2 + 1) * 2 + 1) * 256 + i * 16 + j] = (uint8_t)(q.lo >> 8);
       if (j == 0) {
-        sq[4096 + i * 8 + wave] = (uint8_t)q.s_hi;
-        sq[4096 + i * 8 + 4 + wave] = (uint8_t)q.s_lo;
+        sq[4096 + i * 8 + wq] = (uint8_t)q.s_hi;
+        sq[4096 + i * 8 + 4 + wq] = (uint8_t)q.s_lo;
       }
       if (a.save) {
-        float* r = ss + i * kStagePitch + wave * 32 + j;
+        float* r = ss + i * kStagePitch + wq * 32 + j;
         r[0] = ga;
         r[16] = gb;
         r[128] = ua;
@@ -287,22 +292,23 @@ __device__ __forceinline__ void epilogue_staged(const FwdArgs& a, const WorkItem
       }
     }
     __syncthreads();
-    const int f_wg = w.ct0 * 32;  // first feature of the work-group, a multiple of 128
+    const int f_wg = w.ct0 * 32 + 128 * h;  // first feature of the half, a multiple of 128
     const int c = f_wg >> 9, gl = (f_wg >> 7) & 3;
     uint8_t* qbase = a.q_tiles + (long long)w.tile * at_tile_bytes(F) + (long long)c * kAtChunkBytes;
     {
-      const int run = t >> 5, off = (t & 31) * 16;  // run = q * 2 + plane: 512 B each
+      const int th = wq * 64 + lane;  // thread of the half
+      const int run = th >> 5, off = (th & 31) * 16;  // run = q * 2 + plane: 512 B each
       __builtin_nontemporal_store(*reinterpret_cast<const i32x4*>(sq + run * 512 + off),
                                   reinterpret_cast<i32x4*>(qbase + (run * 2 + (gl >> 1)) * 1024 + (gl & 1) * 512 + off));
-      if (t < 8)
-        *reinterpret_cast<i32x4*>(qbase + kAtCodeBytes + gl * 128 + t * 16) =
-            *reinterpret_cast<const i32x4*>(sq + 4096 + t * 16);
+      if (th < 8)
+        *reinterpret_cast<i32x4*>(qbase + kAtCodeBytes + gl * 128 + th * 16) =
+            *reinterpret_cast<const i32x4*>(sq + 4096 + th * 16);
     }
     if (a.save) {
       const int part = lane >> 5, idx = (lane & 31) * 4, f = f_wg + idx;
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        const int r = it * 4 + wave;
+        const int r = it * 4 + wq;
         if (r < w.nrows && f < F)
           __builtin_nontemporal_store(*reinterpret_cast<const f32x4*>(ss + r * kStagePitch + part * 128 + idx),
                                       reinterpret_cast<f32x4*>(a.save + (long long)(w.row0 + r) * 2 * F + part * F + f));
@@ -414,7 +420,7 @@ __device__ __forceinline__ void epilogue_direct(const FwdArgs& a, const WorkItem
 template <int MODE, bool FAST, bool FL, int NW = kWavesPerGroup>
 __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, int wave, int lane)
 {
-  static_assert(NW == kWavesPerGroup || (FL && MODE == kFwdDown), "eight waves: the down product's forward layout path");
+  static_assert(NW == kWavesPerGroup || (FL && MODE != kFwdPlain), "eight waves: the routed products' forward layout path");
   static_assert(FAST || !FL, "the forward layout is read by the fast path only");
   __shared__ FwdLds lds;  // used by the fast path only
   const int j = lane & 15, g = lane >> 4;
@@ -1301,7 +1307,9 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   if (mode == kFwdPlain) {
     if (fast) MX_LAUNCH(kFwdPlain, true, false); else MX_LAUNCH(kFwdPlain, false, false);
   } else if (mode == kFwdGateUp) {
-    if (fl) MX_LAUNCH(kFwdGateUp, true, true);
+    if (fl && a.n_ct % 8 == 0)
+      hipLaunchKernelGGL((fwd_kernel<kFwdGateUp, true, true, 8>), dim3((unsigned)blocks8), dim3(512), 0, s, b);
+    else if (fl) MX_LAUNCH(kFwdGateUp, true, true);
     else if (fast) MX_LAUNCH(kFwdGateUp, true, false);
     else MX_LAUNCH(kFwdGateUp, false, false);
   } else {
