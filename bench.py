@@ -56,7 +56,7 @@ EXPERT_BYTES = GATEUP_BYTES + DOWN_BYTES        # 23,396,352
 PHASE_BYTES = {"fwd_gateup": GATEUP_BYTES, "fwd_down": DOWN_BYTES,
                "bwd_down_t": DOWN_BYTES, "bwd_gateup_t": GATEUP_BYTES}
 PHASE_KERNEL = {"fwd_gateup": "fwd_kernel<kFwdGateUp>", "fwd_down": "fwd_kernel<kFwdDown>",
-                "bwd_down_t": "bwd_kernel<kBwdDownT>", "bwd_gateup_t": "bwd_kernel<kBwdGateUpT>"}
+                "bwd_down_t": "bwd_wide_kernel<kBwdDownT>", "bwd_gateup_t": "bwd_kernel<kBwdGateUpT>"}
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "routed_layer_config4_hbm_traffic.md")
