@@ -820,9 +820,12 @@ __global__ __launch_bounds__(256) void lora_finish_kernel(FinishArgs a)
 // out2[t, c] = scale_s * sum_{j < r} coef[t, coff_s + j] * F_s(c - lo_s, j) for c < Cexp, segment s
 // = (c >= lo_1) when there are two. A thread owns 4 consecutive columns (of one segment) and keeps
 // their factor values in registers (16-byte loads in either factor layout); a work-group takes
-// 1024 columns and kExpTokens tokens, whose coefficient rows it stages in LDS and reads as
-// broadcasts; each store instruction writes 1 KB of one row.
-constexpr int kExpTokens = 4;
+// 1024 columns and up to kExpTokens tokens (ExpandArgs::tpw), whose coefficient rows it stages in
+// LDS and reads as broadcasts; each store instruction writes 1 KB of one row. The factor values
+// are loaded once per work-group, so launches take as many tokens per work-group as still leave
+// kExpMinGroups work-groups.
+constexpr int kExpTokens = 16;
+constexpr int kExpMinGroups = 512;
 
 struct ExpandArgs {
   float* coef;  // coefficient rows [ntok, m]: read, or (with partial) written by the first column block
@@ -833,6 +836,7 @@ struct ExpandArgs {
   float* out;
   long long ldo;
   int Cexp;
+  int tpw;  // tokens per work-group, at most kExpTokens
   ExpandSpec e;
 };
 
@@ -841,8 +845,8 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(ExpandArgs a)
 {
   __shared__ __attribute__((aligned(16))) float sc[kExpTokens * 2 * kLoraMaxRank];
   const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
-  const int t0 = blockIdx.y * kExpTokens;
-  const int nt = min(kExpTokens, a.ntok - t0);
+  const int t0 = blockIdx.y * a.tpw;
+  const int nt = min(a.tpw, a.ntok - t0);
   const ExpandSpec& e = a.e;
   const int sg = ((e.nseg > 1) & (c >= e.lo[1])) ? 1 : 0;
   const bool cok = c < a.Cexp;
@@ -1202,7 +1206,10 @@ hipError_t launch_lora_expand(float* coef, int m, int ntok, int r, float* out, l
   }
   const int lo[2] = {0, Cseg}, hi[2] = {Cseg, Cexp};
   a.e = expand_spec(nseg, ef, ecoff, lo, hi, r);
-  dim3 grid((unsigned)((Cexp / 4 + 255) / 256), (unsigned)((ntok + kExpTokens - 1) / kExpTokens)), block(256);
+  const int ncb = (Cexp / 4 + 255) / 256;
+  a.tpw = kExpTokens;
+  while (a.tpw > 4 && (long long)ncb * ((ntok + a.tpw - 1) / a.tpw) < kExpMinGroups) a.tpw /= 2;
+  dim3 grid((unsigned)ncb, (unsigned)((ntok + a.tpw - 1) / a.tpw)), block(256);
   if (r > 16) {
     if (km) hipLaunchKernelGGL((lora_expand_kernel<32, true>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((lora_expand_kernel<32, false>), grid, block, 0, s, a);
