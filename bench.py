@@ -55,7 +55,7 @@ DOWN_BYTES = D * F // 2 + D * F // 32           # w2: 7,798,784
 EXPERT_BYTES = GATEUP_BYTES + DOWN_BYTES        # 23,396,352
 PHASE_BYTES = {"fwd_gateup": GATEUP_BYTES, "fwd_down": DOWN_BYTES,
                "bwd_down_t": DOWN_BYTES, "bwd_gateup_t": GATEUP_BYTES}
-PHASE_KERNEL = {"fwd_gateup": "fwd_kernel<kFwdGateUp>", "fwd_down": "fwd_kernel<kFwdDown>",
+PHASE_KERNEL = {"fwd_gateup": "fwd_fused_kernel<kFwdGateUp>", "fwd_down": "fwd_fused_kernel<kFwdDown>",
                 "bwd_down_t": "bwd_wide_kernel<kBwdDownT>", "bwd_gateup_t": "bwd_kernel<kBwdGateUpT>"}
 
 

@@ -2,9 +2,10 @@
 //
 // Each wave computes one 16-row x 64-column output tile over the whole K range
 // (kFwdGateUp: 16 rows x 32 gate features + the same 32 up features). A work-group holds the
-// four waves of four neighbouring column tiles of the same row tile (eight for the down product
-// from a forward layout): they share the tile's activations, which the work-group copies into
-// LDS once per super-chunk. Every weight byte is read once per row tile.
+// four waves of four neighbouring column tiles of the same row tile (eight for the routed
+// products from a forward layout, which then run their large-bucket items in the same launch,
+// fwd_fused_kernel): they share the tile's activations, which the work-group copies into LDS
+// once per super-chunk. Every weight byte is read once per row tile.
 //
 // Per super-chunk c (512 K elements) and lane (j = lane % 16, g = lane / 16), for each of the
 // 4 column groups of 16 weight rows:
@@ -414,15 +415,14 @@ __device__ __forceinline__ void epilogue_direct(const FwdArgs& a, const WorkItem
 
 // One work item: the 16 x 64 tile (w.tile, w.ct) over all of K, then its epilogue.
 // FL: the weights come from the forward layout (fl0 / fl1), one 1 KiB block per load instruction
-// NW waves per work-group (column tiles per item): 4, or 8 for the down product from the forward
-// layout, whose work-groups then hold a CU alone and copy each tile's activations once per
-// 512 output columns instead of once per 256.
+// NW waves per work-group (column tiles per item): 4, or 8 for the routed products from the
+// forward layout, whose work-groups then hold a CU alone and copy each tile's activations once
+// per 8 column tiles instead of once per 4. lds: the work-group's copies and staging (fast path).
 template <int MODE, bool FAST, bool FL, int NW = kWavesPerGroup>
-__device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, int wave, int lane)
+__device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, int wave, int lane, FwdLds& lds)
 {
   static_assert(NW == kWavesPerGroup || (FL && MODE != kFwdPlain), "eight waves: the routed products' forward layout path");
   static_assert(FAST || !FL, "the forward layout is read by the fast path only");
-  __shared__ FwdLds lds;  // used by the fast path only
   const int j = lane & 15, g = lane >> 4;
   const int nb = a.K / kGroup;
   const int nsc = at_nchunks(a.K);
@@ -724,6 +724,7 @@ __device__ __forceinline__ void fwd_item(const FwdArgs& a, const WorkItem& w, in
 template <int MODE, bool FAST, bool FL, int NW = kWavesPerGroup>
 __global__ __launch_bounds__(64 * NW, NW == kWavesPerGroup ? 2 : 1) void fwd_kernel(FwdArgs a)
 {
+  __shared__ FwdLds lds;  // used by the fast path only
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps control flow scalar
   WorkItem w;
@@ -734,7 +735,7 @@ __global__ __launch_bounds__(64 * NW, NW == kWavesPerGroup ? 2 : 1) void fwd_ker
     // recompute lane-derived addresses per item instead of holding them across items
     int l = lane;
     asm volatile("" : "+v"(l));
-    fwd_item<MODE, FAST, FL, NW>(a, w, wave, l);
+    fwd_item<MODE, FAST, FL, NW>(a, w, wave, l, lds);
   }
 }
 
@@ -1261,6 +1262,48 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void fwd_wide_kernel(FwdArgs a)
   queue_leave(a.wcounter);
 }
 
+// Both bucket kinds of a routed product from the forward layout in one launch of eight-wave
+// work-groups (one per CU, the shape of both kernels above): each work-group runs its one-tile
+// items (fwd_kernel<MODE, true, true, 8>) and then takes large-bucket items from the work queue
+// (fwd_wide_kernel), so the large items fill the slots that the one-tile items' last round leaves
+// idle, and a routing without large buckets pays for no second launch. Same items, same
+// arithmetic: the results are those of the two launches.
+union FusedLds {
+  FwdLds f;
+  WideLds w;
+};
+
+template <int MODE>
+__global__ __launch_bounds__(64 * kWgWaves, 1) void fwd_fused_kernel(FwdArgs a)
+{
+  static_assert(kWgWaves == 8, "the one-tile items run in eight-wave work-groups");
+  __shared__ FusedLds lds;
+  __shared__ int s_item;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  WorkItem w;
+  for (int it = 0; decode_work(a.tiles, a.n_tiles, a.small_tiles, a.n_small, a.n_groups, a.M, a.n_ct, wave, it, w, 8); ++it) {
+    if (it > 0) __syncthreads();
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    fwd_item<MODE, true, true, 8>(a, w, wave, l, lds.f);
+  }
+  const int ng = *(cint_ptr)a.n_wgroups;
+  if (ng == 0) return;  // no large buckets: the work queue is not touched
+  const int nfb = (a.n_ct + kWgWaves - 1) / kWgWaves;
+  const int total = ng * nfb;
+  for (;;) {
+    const int item = queue_next(a.wcounter, &s_item);  // also: every wave is done with the LDS before
+    if (item >= total) break;
+    const int gi = item / nfb, fb = item - gi * nfb;
+    const cint_ptr gg = (cint_ptr)(a.wgroups + gi);
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    fwd_wide_item<MODE>(a, gg[0], gg[1], gg[2], fb, wave, l, lds.w);
+  }
+  queue_leave(a.wcounter);
+}
+
 // Work-groups that fit on the device at once (two per CU: the LDS and register budgets of
 // fwd_kernel), rounded down to a multiple of the 8 XCDs.
 int resident_groups()
@@ -1302,10 +1345,16 @@ hipError_t launch_fwd(const FwdArgs& a, int mode, int max_tiles, hipStream_t s)
   // (and its byte count fits a buffer resource, as for the checkpoint layout)
   const bool fl = fast && mode != kFwdPlain && a.fl0 && (mode != kFwdGateUp || a.fl1) &&
                   forward_layout_bytes(a.R, a.K) < (1LL << 32);
+  // both bucket kinds in one launch: eight-wave one-tile items and wide large-bucket items
+  const bool fused = fl && a.n_ct % 8 == 0 && split && b.wgroups && b.wcounter;
   dim3 grid((unsigned)blocks), block(64 * kWavesPerGroup);
 #define MX_LAUNCH(M, F, L) hipLaunchKernelGGL((fwd_kernel<M, F, L>), grid, block, 0, s, b)
   if (mode == kFwdPlain) {
     if (fast) MX_LAUNCH(kFwdPlain, true, false); else MX_LAUNCH(kFwdPlain, false, false);
+  } else if (fused) {
+    if (mode == kFwdGateUp) hipLaunchKernelGGL((fwd_fused_kernel<kFwdGateUp>), dim3((unsigned)blocks8), dim3(512), 0, s, b);
+    else hipLaunchKernelGGL((fwd_fused_kernel<kFwdDown>), dim3((unsigned)blocks8), dim3(512), 0, s, b);
+    return hipGetLastError();
   } else if (mode == kFwdGateUp) {
     if (fl && a.n_ct % 8 == 0)
       hipLaunchKernelGGL((fwd_kernel<kFwdGateUp, true, true, 8>), dim3((unsigned)blocks8), dim3(512), 0, s, b);
