@@ -119,21 +119,36 @@ __host__ __device__ inline long long x3_row_bytes(int K) { return (long long)at_
 MX_DEV float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
 MX_DEV uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 
-// max over the 16 lanes of a lane group (lanes 16n..16n+15)
+// Reductions over the 16 lanes of a lane group (lanes 16n..16n+15, one DPP row), as a butterfly
+// on DPP lane moves inside the VALU (a cross-lane shuffle would be an LDS permute with its round
+// trip): quad_perm [1,0,3,2] gives lane ^ 1 and [2,3,0,1] lane ^ 2; after those two steps every
+// quad holds one value, so row_half_mirror (7 - lane within 8) brings the other quad's value as
+// lane ^ 4 would, and row_mirror (15 - lane) then the other half-row's as lane ^ 8 would. Every
+// lane adds the same two operands at each step, so all 16 end with the same bits.
+template <int CTRL>
+MX_DEV float dpp_lane(float v)
+{
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+
 MX_DEV float group16_max(float v)
 {
-  v = fmaxf(v, __shfl_xor(v, 1, 64));
-  v = fmaxf(v, __shfl_xor(v, 2, 64));
-  v = fmaxf(v, __shfl_xor(v, 4, 64));
-  v = fmaxf(v, __shfl_xor(v, 8, 64));
+  v = fmaxf(v, dpp_lane<kDppXor1>(v));
+  v = fmaxf(v, dpp_lane<kDppXor2>(v));
+  v = fmaxf(v, dpp_lane<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_lane<kDppMirror>(v));
   return v;
 }
 MX_DEV float group16_sum(float v)
 {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
-  v += __shfl_xor(v, 8, 64);
+  v += dpp_lane<kDppXor1>(v);
+  v += dpp_lane<kDppXor2>(v);
+  v += dpp_lane<kDppHalfMirror>(v);
+  v += dpp_lane<kDppMirror>(v);
   return v;
 }
 
