@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(void* out, const uint8_t* 
   }
 }
 
-constexpr int kQuantResidentBlocks = 1024;  // resident grid of quant_tiles over the large buckets
+constexpr int kQuantResidentBlocks = 1536;  // resident grid of quant_tiles over the large buckets: six per CU
 
 // ---------------------------------------------------------------- routing
 // (token, slot) pairs are bucketed by expert: counts -> exclusive offsets -> placement.
