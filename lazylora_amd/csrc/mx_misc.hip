@@ -266,6 +266,25 @@ __device__ __forceinline__ int wave_bucket_add(int* counter, int e, bool valid)
   return pos;
 }
 
+// An LDS counter add for route_one_kernel: when every valid lane of the wave routes to one expert
+// (tokens sorted by expert), one atomic for the wave; otherwise one per lane (distinct experts
+// across the wave, the usual case, gain nothing from aggregation). Called by the whole wave.
+__device__ __forceinline__ int lds_bucket_add(int* counter, int e, bool valid)
+{
+  const int lane = (int)(threadIdx.x & 63);
+  const uint64_t vm = __builtin_amdgcn_ballot_w64(valid);
+  if (vm == 0) return -1;
+  const int leader = __builtin_ctzll(vm);
+  const int el = __builtin_amdgcn_readlane(e, leader);
+  if (__builtin_amdgcn_ballot_w64(valid && e == el) == vm) {  // uniform
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&counter[el], __popcll(vm));
+    base = __builtin_amdgcn_readlane(base, leader);
+    return valid ? base + __popcll(vm & ((1ull << lane) - 1ull)) : -1;
+  }
+  return valid ? atomicAdd(&counter[e], 1) : -1;
+}
+
 __global__ __launch_bounds__(256) void route_count_kernel(const void* idx, int idx64, int P, int E, int* counts,
                                                           int* meta)
 {
@@ -369,9 +388,13 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int* counts, int
 // The whole routing in one work-group (P <= kRouteOneP pairs, E <= kRouteOneE experts): counts
 // with LDS atomics, the scan above (cursors in LDS), then the placement with LDS atomics; all 16
 // meta words are written. Replaces five launches (two clears, count, scan, place) when the pairs
-// are few.
+// are few. A wave whose pairs all go to one expert (tokens sorted by expert) adds to its counter
+// once rather than serialising 64 atomics on one address, and up to kRouteStageP pairs the
+// placed token and weight of each bucket position are staged in LDS and written out in position
+// order (contiguous stores) rather than scattered from the one CU.
 constexpr int kRouteOneP = 65536;
 constexpr int kRouteOneE = 8192;
+constexpr int kRouteStageP = 8192;
 
 __global__ __launch_bounds__(1024) void route_one_kernel(const void* idx, int idx64, const float* w, int P, int k,
                                                          int E, int* counts, int* offsets, int4* tiles,
@@ -380,8 +403,11 @@ __global__ __launch_bounds__(1024) void route_one_kernel(const void* idx, int id
 {
   __shared__ int s[6][1024];
   __shared__ int s_cnt[kRouteOneE];
+  __shared__ int s_tok[kRouteStageP];
+  __shared__ float s_w[kRouteStageP];
   __shared__ int s_bad;
   const int t = threadIdx.x;
+  const bool stage = P <= kRouteStageP;
   for (int e = t; e < E; e += 1024) s_cnt[e] = 0;
   if (t == 0) s_bad = 0;
   __syncthreads();
@@ -394,10 +420,11 @@ __global__ __launch_bounds__(1024) void route_one_kernel(const void* idx, int id
       raw[u] = p < P ? read_idx(idx, idx64, p) : 0;
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (p0 + u * 1024 + t >= P) continue;
-      if (raw[u] >= 0 && raw[u] < E) atomicAdd(&s_cnt[raw[u]], 1);
-      else s_bad = 1;
+    for (int u = 0; u < 8; ++u) {  // wave-aggregated: pairs of one expert in a wave add once
+      const bool in = p0 + u * 1024 + t < P;
+      const bool valid = in && raw[u] >= 0 && raw[u] < E;
+      if (in && !valid) s_bad = 1;
+      lds_bucket_add(s_cnt, valid ? raw[u] : 0, valid);
     }
   }
   __syncthreads();
@@ -420,15 +447,29 @@ __global__ __launch_bounds__(1024) void route_one_kernel(const void* idx, int id
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int p = p0 + u * 1024 + t;
+      const bool valid = p < P && raw[u] >= 0 && raw[u] < E;
+      const int pos = lds_bucket_add(s_cnt, valid ? raw[u] : 0, valid);
       if (p >= P) continue;
-      if (raw[u] < 0 || raw[u] >= E) {
+      if (!valid) {
         pair_of[p] = -1;
         continue;
       }
-      const int pos = atomicAdd(&s_cnt[raw[u]], 1);
-      pair_token[pos] = p / k;
-      pair_w[pos] = wv[u];
+      if (stage) {
+        s_tok[pos] = p / k;
+        s_w[pos] = wv[u];
+      } else {
+        pair_token[pos] = p / k;
+        pair_w[pos] = wv[u];
+      }
       pair_of[p] = pos;
+    }
+  }
+  if (stage) {
+    __syncthreads();
+    const int placed = s[0][1023];  // the scan's total: pairs with a valid expert id
+    for (int i = t; i < placed; i += 1024) {
+      pair_token[i] = s_tok[i];
+      pair_w[i] = s_w[i];
     }
   }
 }
