@@ -497,13 +497,17 @@ MX_DEV void rowouter_task(const PassJob& J, int t, float* lds)
       // outer product, and the step's tile into LDS (rows 4u + q, columns 4i .. 4i + 3)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const bool ok = (sb + 16 * st + 4 * u + q < q1) & (row[st][u] >= 0) & (c < J.K);
+        // the lane's row (q) and its columns (i) are checked apart: the coefficient it supplies
+        // belongs to rank i of row q, whatever its own columns are, so only the elements of
+        // columns past K are zeroed (they also feed the row dot through the tile)
+        const bool row_ok = (sb + 16 * st + 4 * u + q < q1) & (row[st][u] >= 0);
+        const bool ok = row_ok & (c < J.K);
         f32x4 xv = quad_decode<KIND>(x[st][u], J.src.act_kind);
 #pragma unroll
         for (int e = 0; e < 4; ++e) xv[e] = ok ? xv[e] : 0.f;
 #pragma unroll
         for (int jt = 0; jt < JT; ++jt) {
-          const float cj = ok ? wq[st][u] * cv[st][u][jt] : 0.f;
+          const float cj = row_ok ? wq[st][u] * cv[st][u][jt] : 0.f;
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[jt][e] = mfma4(cj, xv[e], acc[jt][e]);
         }

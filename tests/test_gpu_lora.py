@@ -102,6 +102,16 @@ def test_large_buckets_with_lora(k, act):
     run_case(k, 4, 1024, 512, 0, 1, 16, act, seed=47, scale_lo=118, scale_hi=122, sizes=[150, 70, 30, 6])
 
 
+@pytest.mark.parametrize("F,r", [(352, 16), (352, 32), (416, 16)])
+def test_ffn_not_a_multiple_of_64(k, F, r):
+    """F = 352 or 416: the last 64-column block of the fused pass over the gate/up gradients is
+    part valid. Its waves supply the coefficients of every rank whatever their own columns are,
+    so the B_gate / B_up gradients of the last features keep ranks 8..15 (and 24..31); only the
+    elements of the columns past F are zeroed."""
+    case(f"2 experts 256x{F}, 120 tokens top-2, LoRA r={r}")
+    run_case(k, 2, 256, F, 120, 2, r, "swiglu", seed=48 + r)
+
+
 def test_expert_shape_of_the_reference(k):
     """Adapters on experts of the BASELINE shape (2048 x 7168): the long reductions (K = 7168)
     and the wide expansions run at their real sizes."""
