@@ -5,10 +5,12 @@ lora_layer.py:104-139, :178-226).
 Each configuration draws the hidden and FFN sizes (multiples of 32: some multiples of 512 and
 256, where the layer's forward and backward layout copies apply, some not), the expert count,
 tokens, top-k, activation, the activations' dtype, the LoRA rank (0 = off), which layout copies
-the layer carries, and uniform or Zipf-skewed routing (the latter makes large buckets, which take
-the grouped work-groups). The forward, the backward recomputing the forward and, with LoRA, the
-six adapter gradients are held to the path's bar (rel-L2 <= 5e-3, cosine >= 0.9999); the
-backward reusing the forward's saved state must equal the recomputing one bit for bit."""
+the layer carries, and the routing: uniform, Zipf-skewed (large buckets, which take the grouped
+work-groups) or top-1 with the tokens sorted by expert (whole waves of the routing kernel then
+add to one expert's counter at once). The forward, the backward recomputing the forward and,
+with LoRA, the six adapter gradients are held to the path's bar (rel-L2 <= 5e-3, cosine >=
+0.9999); the backward reusing the forward's saved state must equal the recomputing one bit for
+bit."""
 import types
 
 import numpy as np
@@ -20,7 +22,7 @@ from tests.conftest import assert_close
 
 pytestmark = pytest.mark.gpu
 
-N_CONFIGS = 20
+N_CONFIGS = 120
 
 
 @pytest.fixture(scope="module")
@@ -33,19 +35,23 @@ def k():
 
 def draw(i):
     rng = np.random.default_rng(7000 + i)
-    E = int(rng.integers(1, 13))
+    E = int(rng.integers(1, 17))
+    D = int(rng.choice([160, 256, 512, 544, 1024, 1056, 2048]))
+    F = int(rng.choice([96, 128, 256, 352, 512, 608, 1024, 2048]))
+    routing = str(rng.choice(["uniform", "uniform", "zipf", "sorted"]))
+    n_max = 64 if D * F > (1 << 20) else 300  # the float64 oracle's time
     return dict(
         seed=7000 + i,
-        D=int(rng.choice([256, 512, 544, 1024, 1056])),
-        F=int(rng.choice([128, 256, 352, 512, 1024])),
+        D=D,
+        F=F,
         E=E,
-        topk=int(rng.integers(1, min(E, 8) + 1)),
-        N=int(rng.integers(1, 193)),
+        topk=1 if routing == "sorted" else int(rng.integers(1, min(E, 8) + 1)),
+        N=int(rng.integers(1, n_max + 1)),
         act=str(rng.choice(["swiglu", "situ"])),
         bf16=bool(rng.random() < 0.3),
         r=int(rng.choice([0, 0, 1, 8, 16, 32])),
         layouts=str(rng.choice(["none", "forward", "both"])),
-        zipf=bool(rng.random() < 0.4),
+        routing=routing,
     )
 
 
@@ -54,7 +60,7 @@ CONFIGS = [draw(i) for i in range(N_CONFIGS)]
 
 def label(c):
     return (f"D{c['D']}-F{c['F']}-E{c['E']}-k{c['topk']}-N{c['N']}-{c['act']}-{'bf16' if c['bf16'] else 'f32'}"
-            f"-r{c['r']}-{c['layouts']}-{'zipf' if c['zipf'] else 'uniform'}")
+            f"-r{c['r']}-{c['layouts']}-{c['routing']}")
 
 
 def adapters_of(lo):
@@ -70,10 +76,14 @@ def test_routed_layer_config(k, c):
     rng = np.random.default_rng(c["seed"])
     D, F, E, N, topk, act = c["D"], c["F"], c["E"], c["N"], c["topk"], c["act"]
     ex = oracle.random_experts(rng, E, D, F, 118, 122)
-    logits = rng.standard_normal((N, E)).astype(np.float32)
-    if c["zipf"]:
-        logits = logits + oracle.zipf_offsets(rng, E)[None, :]
-    idx, w = oracle.softmax_topk(logits, topk)
+    if c["routing"] == "sorted":
+        idx = np.sort(rng.integers(0, E, N)).astype(np.int64)[:, None]
+        w = rng.uniform(0.5, 1.5, (N, 1)).astype(np.float32)
+    else:
+        logits = rng.standard_normal((N, E)).astype(np.float32)
+        if c["routing"] == "zipf":
+            logits = logits + oracle.zipf_offsets(rng, E)[None, :]
+        idx, w = oracle.softmax_topk(logits, topk)
     h = rng.standard_normal((N, D)).astype(np.float32)
     g = rng.standard_normal((N, D)).astype(np.float32)
     lo = oracle.random_lora(rng, D, F, c["r"]) if c["r"] else None
@@ -104,3 +114,32 @@ def test_routed_layer_config(k, c):
         for name, a, b in zip(("gate_A", "gate_B", "up_A", "up_B", "down_A", "down_B"), rec[2], want[2]):
             assert a.shape == b.shape, name
             assert_close(a.cpu().numpy(), b, f"grad {name} {label(c)}")
+
+
+def draw_product(i):
+    rng = np.random.default_rng(9000 + i)
+    return dict(seed=9000 + i, M=int(rng.integers(1, 300)), K=32 * int(rng.integers(1, 129)),
+                R=int(rng.integers(1, 700)), lo=int(rng.integers(100, 125)))
+
+
+PRODUCTS = [draw_product(i) for i in range(60)]
+
+
+@pytest.mark.parametrize("c", PRODUCTS, ids=[f"M{c['M']}-K{c['K']}-R{c['R']}-s{c['lo']}" for c in PRODUCTS])
+def test_products_config(k, clib, c):
+    """mxfp4_gemm (y = x W^T, two-term e4m3 activations) and mxfp4_gemm_t (y = dy W, exact bf16
+    weights, two bf16 terms of dy) at random shapes, scales 2^(lo-127) .. 2^(lo-123), against
+    the C restatement of the reference's products (mxfp4_gemm.c:64-129)."""
+    print(f"\n[case] product sweep M={c['M']} K={c['K']} R={c['R']}", flush=True)
+    rng = np.random.default_rng(c["seed"])
+    M, K, R = c["M"], c["K"], c["R"]
+    p, s = oracle.random_mx(rng, (R, K), c["lo"], c["lo"] + 4)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    dy = rng.standard_normal((M, R)).astype(np.float32)
+    P, S = torch.from_numpy(p).cuda(), torch.from_numpy(s).cuda()
+    got = k.gemm(torch.from_numpy(x).cuda(), P, S).cpu().numpy()
+    assert got.shape == (M, R)
+    assert_close(got, clib.gemm(x, p, s), f"gemm {M}x{K}x{R}")
+    got_t = k.gemm_t(torch.from_numpy(dy).cuda(), P, S).cpu().numpy()
+    assert got_t.shape == (M, K)
+    assert_close(got_t, clib.gemm_t(dy, p, s), f"gemm_t {M}x{K}x{R}", rel=2e-5, cos=0.99999999)
