@@ -111,12 +111,13 @@ __global__ __launch_bounds__(256) void router_topk_bwd_kernel(float* __restrict_
   const float* row = logits + (long long)token * E;
 
   int e = -1;
-  float s = 0.f, g = 0.f;
+  float s = 0.f, sm = 0.f, g = 0.f;  // sm = sigmoid(-x) = 1 - s, without the cancellation of 1 - s
   if (lane < top_k) {
     const long long v = topk_idx[(long long)token * top_k + lane];
     if (v >= 0 && v < E) {
       e = (int)v;
       s = 1.0f / (1.0f + expf(-row[e]));
+      sm = 1.0f / (1.0f + expf(row[e]));
       g = grad_w[(long long)token * top_k + lane];
     }
   }
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(256) void router_topk_bwd_kernel(float* __restrict_
   } else {
     ds = scale * g;
   }
-  const float val = ds * s * (1.0f - s);
+  const float val = ds * s * sm;  // sigmoid'(x) = s (1 - s), its small factor computed directly
 
   float out[PER_LANE];
 #pragma unroll

@@ -143,3 +143,41 @@ def test_products_config(k, clib, c):
     got_t = k.gemm_t(torch.from_numpy(dy).cuda(), P, S).cpu().numpy()
     assert got_t.shape == (M, K)
     assert_close(got_t, clib.gemm_t(dy, p, s), f"gemm_t {M}x{K}x{R}", rel=2e-5, cos=0.99999999)
+
+
+def draw_router(i):
+    rng = np.random.default_rng(11000 + i)
+    E = int(rng.choice([int(rng.integers(1, 129)), int(rng.integers(129, 1025)), int(rng.integers(1025, 4097))]))
+    return dict(seed=11000 + i, N=int(rng.integers(1, 600)), E=E, top_k=int(rng.integers(1, min(E, 64) + 1)),
+                renorm=bool(rng.random() < 0.7), scale=float(rng.choice([1.0, 2.5, 0.7])),
+                bias=bool(rng.random() < 0.6))
+
+
+ROUTERS = [draw_router(i) for i in range(40)]
+
+
+@pytest.mark.parametrize("c", ROUTERS, ids=[f"N{c['N']}-E{c['E']}-k{c['top_k']}-{'renorm' if c['renorm'] else 'raw'}"
+                                           f"-s{c['scale']}-{'bias' if c['bias'] else 'nobias'}" for c in ROUTERS])
+def test_router_config(k, c):
+    """mxfp4_router_topk and its backward at random widths (moe_router.py:55-135): indices exact
+    where float64 leaves no near-tie (sets where it does), weights to 1e-5 relative, dL/dlogits
+    to 1e-4 against oracle.router_select_backward at the kernel's own choice."""
+    from tests.test_gpu_router import compare_selection
+    print(f"\n[case] router sweep {c}", flush=True)
+    rng = np.random.default_rng(c["seed"])
+    N, E, top_k, scale, renorm = c["N"], c["E"], c["top_k"], c["scale"], c["renorm"]
+    logits = (2.0 * rng.standard_normal((N, E))).astype(np.float32)
+    bias = (0.05 * rng.standard_normal(E)).astype(np.float32) if c["bias"] else None
+    Lg = torch.from_numpy(logits).cuda()
+    idx, w = k.router_topk(Lg, torch.from_numpy(bias).cuda() if c["bias"] else None, top_k, scale, renorm)
+    idx_h, w_h = idx.cpu().numpy(), w.cpu().numpy()
+    assert idx_h.shape == (N, top_k) and ((idx_h >= 0) & (idx_h < E)).all()
+    assert all(len(set(r)) == top_k for r in idx_h.tolist())
+    # rows whose top k + 1 biased scores hold an fp32 near-tie are compared as sets (many, at wide
+    # E and large k, where the scores crowd below 1); every other row index for index
+    loose = compare_selection(idx_h, w_h, logits, bias, top_k, scale, renorm)
+    print(f"rows compared as sets: {loose} of {N}")
+    g = rng.standard_normal((N, top_k)).astype(np.float32)
+    got = k.router_topk_backward(Lg, idx, torch.from_numpy(g).cuda(), scale, renorm).cpu().numpy()
+    want = oracle.router_select_backward(logits, idx_h, g, scale, renorm)
+    assert np.allclose(got, want, rtol=1e-4, atol=1e-7), np.abs(got - want).max()
