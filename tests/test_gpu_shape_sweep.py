@@ -181,3 +181,48 @@ def test_router_config(k, c):
     got = k.router_topk_backward(Lg, idx, torch.from_numpy(g).cuda(), scale, renorm).cpu().numpy()
     want = oracle.router_select_backward(logits, idx_h, g, scale, renorm)
     assert np.allclose(got, want, rtol=1e-4, atol=1e-7), np.abs(got - want).max()
+
+
+def draw_block(i):
+    rng = np.random.default_rng(13000 + i)
+    E = int(rng.integers(2, 17))
+    return dict(seed=13000 + i, H=int(rng.choice([128, 256, 384, 512])), Dl=32 * int(rng.integers(2, 17)),
+                Fm=32 * int(rng.integers(1, 9)), E=E, top_k=int(rng.integers(1, min(E, 8) + 1)),
+                Ds=32 * int(rng.integers(1, 5)), N=int(rng.integers(1, 97)),
+                latent_norm=bool(rng.random() < 0.7), renorm=bool(rng.random() < 0.7),
+                scale=float(rng.choice([1.0, 2.5])), r=int(rng.choice([0, 0, 4, 16])))
+
+
+BLOCKS = [draw_block(i) for i in range(16)]
+
+
+@pytest.mark.parametrize("c", BLOCKS, ids=[f"H{c['H']}-Dl{c['Dl']}-F{c['Fm']}-E{c['E']}-k{c['top_k']}-N{c['N']}"
+                                          f"-norm{int(c['latent_norm'])}-renorm{int(c['renorm'])}-r{c['r']}"
+                                          for c in BLOCKS])
+def test_latent_block_config(k, c):
+    """The latent MoE block (lazy_trainer.py:689-737: router, shared expert, latent down / up
+    projections, routed MXFP4 experts with the layer's LoRA adapters, RMSNorm of the routed sum)
+    at random widths against oracle.latent_moe_forward on the same MXFP4 bytes; the router's
+    choice equal to the oracle's (row sets where float64 sees a near-tie)."""
+    from tests.test_gpu_latent_moe import block_from
+    print(f"\n[case] latent block sweep {c}", flush=True)
+    rng = np.random.default_rng(c["seed"])
+    H, Dl, Fm, E, Ds, N = c["H"], c["Dl"], c["Fm"], c["E"], c["Ds"], c["N"]
+    ex = oracle.random_experts(rng, E, Dl, Fm, 121, 125)
+    g = lambda *s: rng.standard_normal(s) * 0.05
+    p = {"gate_weight": g(E, H), "e_score_correction_bias": g(E), "shared_w1_weight": g(Ds, H),
+         "shared_w3_weight": g(Ds, H), "shared_w2_weight": g(H, Ds), "down_weight": g(Dl, H) * 4,
+         "up_weight": g(H, Dl), "norm_weight": 1 + g(Dl), "top_k": c["top_k"], "routed_scale": c["scale"],
+         "renorm": int(c["renorm"]), "latent_norm": int(c["latent_norm"]), "rms_eps": 1e-5, "hidden": H}
+    lo = oracle.random_lora(rng, Dl, Fm, c["r"]) if c["r"] else None
+    # the layer's adapter bundle, as the reference's LayerLoRABundle (routed adapters only)
+    bundle = types.SimpleNamespace(**dict(zip(("gate_lora", "up_lora", "down_lora"), adapters_of(lo)))) if lo else None
+    blk = block_from(p, ex, lora=bundle)
+    x = rng.standard_normal((N, H))
+    out, idx, w = blk.forward(torch.tensor(x, dtype=torch.float32, device="cuda"))
+    want, idx64, w64 = oracle.latent_moe_forward(x.astype(np.float32), p, experts=ex, lora=lo)
+    got_idx = idx.cpu().numpy()
+    same = [sorted(a) == sorted(b) for a, b in zip(got_idx.tolist(), np.asarray(idx64).tolist())]
+    assert sum(not s for s in same) <= max(1, N // 50), "router choices differ from the oracle"
+    if all(same):
+        assert_close(out.detach().cpu().numpy(), want, f"latent block {c}")
