@@ -110,3 +110,33 @@ def test_workspace_chain(k, D, F, E, layouts, n_max, calls):
                 assert_close(a.cpu().numpy(), b, f"grad {nm} {name}")
     del L
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("M,K,R", [(1, 7168, 2048), (37, 1024, 96), (256, 7168, 2048), (70, 544, 352)])
+def test_product_workspaces_hold_no_state(k, M, K, R):
+    """mxfp4_gemm and mxfp4_gemm_t with their workspaces filled with random bytes give the same
+    bits as with fresh ones (the workspace holds the activation tiles, written before they are
+    read)."""
+    from lazylora_amd.native import _stream
+    print(f"\n[case] product workspaces filled with random bytes, M={M} K={K} R={R}", flush=True)
+    rng = np.random.default_rng(M + K + R)
+    pk = torch.from_numpy(rng.integers(0, 256, (R, K // 2), dtype=np.uint8)).cuda()
+    sc = torch.from_numpy(rng.integers(118, 123, (R, K // 32), dtype=np.uint8)).cuda()
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    dy = torch.from_numpy(rng.standard_normal((M, R)).astype(np.float32)).cuda()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(M * K + R)
+    dev = x.device
+    for _ in range(2):
+        nws = k.lib.mxfp4_gemm_workspace_size(M, K, R)
+        ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev).random_(0, 256, generator=gen)
+        y = torch.empty((M, R), dtype=torch.float32, device=dev)
+        assert k.lib.mxfp4_gemm(y.data_ptr(), x.data_ptr(), pk.data_ptr(), sc.data_ptr(), M, K, R, ws.data_ptr(),
+                                nws, _stream(dev)) == 0
+        assert torch.equal(y, k.gemm(x, pk, sc))
+        nws = k.lib.mxfp4_gemm_t_workspace_size(M, K, R)
+        ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev).random_(0, 256, generator=gen)
+        yt = torch.zeros((M, K), dtype=torch.float32, device=dev)
+        assert k.lib.mxfp4_gemm_t(yt.data_ptr(), dy.data_ptr(), pk.data_ptr(), sc.data_ptr(), M, K, R,
+                                  ws.data_ptr(), nws, _stream(dev)) == 0
+        assert torch.equal(yt, k.gemm_t(dy, pk, sc))
