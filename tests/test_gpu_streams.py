@@ -2,7 +2,9 @@
 of every entry point in include/lazylora_mxfp4.h). Each call below runs on a second stream
 (default priority) whose inputs are produced on that stream right before the call, behind a long
 chain of unrelated work, without any synchronisation; a launch on another stream would read them
-before they are written. Results must equal the default stream's bit for bit."""
+before they are written. Results must equal the default stream's bit for bit. Two calls
+interleaved on two streams must also give what each gives alone (no kernel waits on another
+work-group, and each call's counters and queues live in its own workspace)."""
 import types
 
 import numpy as np
@@ -109,3 +111,49 @@ def test_layouts_and_products_on_a_side_stream(k):
     torch.cuda.synchronize()
     assert torch.equal(y, want_y) and torch.equal(yt, want_yt)
     assert torch.equal(out, want_out)
+
+
+def test_concurrent_calls_on_two_streams(k):
+    """Two routed layers' forward and backward (each with its own workspace; one with large buckets,
+    so its resident grouped work-groups and work queues share the GPU with the other call's
+    kernels) interleaved on two streams with no synchronisation between them, three times over:
+    every result equals the same call made alone."""
+    from lazylora_amd.experts import ExpertLayer
+    print("\n[case] two routed calls interleaved on two streams", flush=True)
+    rng = np.random.default_rng(503)
+    jobs = []
+    for E, D, F, N, topk, skew in ((8, 1024, 512, 160, 2, True), (16, 512, 256, 200, 4, False)):
+        ex = oracle.random_experts(rng, E, D, F, 118, 122)
+        L = ExpertLayer(*[torch.from_numpy(np.ascontiguousarray(a)).cuda()
+                          for a in (ex.w1p, ex.w1s, ex.w3p, ex.w3s, ex.w2p, ex.w2s)])
+        L.prepare_forward_layout()
+        logits = rng.standard_normal((N, E)).astype(np.float32)
+        if skew:
+            logits = logits + oracle.zipf_offsets(rng, E)[None, :]
+        idx, w = oracle.softmax_topk(logits, topk)
+        t = [torch.from_numpy(a).cuda() for a in (rng.standard_normal((N, D)).astype(np.float32), idx, w,
+                                                  rng.standard_normal((N, D)).astype(np.float32))]
+        ws = torch.empty(k.moe_workspace_bytes(N, topk, E, D, F), dtype=torch.uint8, device="cuda")
+        jobs.append((L, t, ws))
+
+    def run(L, t, ws):
+        H, I, W, G = t
+        out = k.routed_forward(H, I, W, L, save_for_backward=True, workspace=ws)
+        gh, gw = k.routed_backward(H, I, W, L, G, reuse_forward=True, workspace=ws)
+        return out, gh, gw
+
+    alone = [run(*j) for j in jobs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for _ in range(3):
+        got = [None, None]
+        for i in (0, 1):
+            with torch.cuda.stream(streams[i]):
+                got[i] = run(*jobs[i])
+        for s in streams:
+            torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        for a, b in zip(got, alone):
+            assert all(torch.equal(x, y) for x, y in zip(a, b))
