@@ -11,6 +11,7 @@ add to one expert's counter at once). The forward, the backward recomputing the 
 with LoRA, the six adapter gradients are held to the path's bar (rel-L2 <= 5e-3, cosine >=
 0.9999); the backward reusing the forward's saved state must equal the recomputing one bit for
 bit."""
+import os
 import types
 
 import numpy as np
@@ -22,7 +23,9 @@ from tests.conftest import assert_close
 
 pytestmark = pytest.mark.gpu
 
-N_CONFIGS = 120
+# LAZYLORA_SWEEP_SCALE=n draws n times as many cases of each kind (the first ones unchanged)
+SCALE = max(1, int(os.environ.get("LAZYLORA_SWEEP_SCALE", "1")))
+N_CONFIGS = 120 * SCALE
 
 
 @pytest.fixture(scope="module")
@@ -122,7 +125,7 @@ def draw_product(i):
                 R=int(rng.integers(1, 700)), lo=int(rng.integers(100, 125)))
 
 
-PRODUCTS = [draw_product(i) for i in range(60)]
+PRODUCTS = [draw_product(i) for i in range(60 * SCALE)]
 
 
 @pytest.mark.parametrize("c", PRODUCTS, ids=[f"M{c['M']}-K{c['K']}-R{c['R']}-s{c['lo']}" for c in PRODUCTS])
@@ -153,7 +156,7 @@ def draw_router(i):
                 bias=bool(rng.random() < 0.6))
 
 
-ROUTERS = [draw_router(i) for i in range(40)]
+ROUTERS = [draw_router(i) for i in range(40 * SCALE)]
 
 
 @pytest.mark.parametrize("c", ROUTERS, ids=[f"N{c['N']}-E{c['E']}-k{c['top_k']}-{'renorm' if c['renorm'] else 'raw'}"
@@ -193,7 +196,7 @@ def draw_block(i):
                 scale=float(rng.choice([1.0, 2.5])), r=int(rng.choice([0, 0, 4, 16])))
 
 
-BLOCKS = [draw_block(i) for i in range(16)]
+BLOCKS = [draw_block(i) for i in range(16 * SCALE)]
 
 
 @pytest.mark.parametrize("c", BLOCKS, ids=[f"H{c['H']}-Dl{c['Dl']}-F{c['Fm']}-E{c['E']}-k{c['top_k']}-N{c['N']}"
