@@ -19,7 +19,7 @@ import pytest
 import torch
 
 import oracle
-from tests.conftest import assert_close
+from tests.conftest import REL_L2_TOL, assert_close
 
 pytestmark = pytest.mark.gpu
 
@@ -72,6 +72,44 @@ def adapters_of(lo):
                                        dropout_rate=0.0) for A, B, s in lo.adapters())
 
 
+def dot_scale(h, idx, ex, g, act, lo):
+    """Per (token, slot): ||g_t|| * ||down_e(h_t)|| / sqrt(D), the size of the dot product
+    grad_w[t, slot] = <g_t, down_e(h_t)> for unrelated vectors (float64; ids outside [0, E): 0)."""
+    scale = np.zeros(idx.shape)
+    D = h.shape[1]
+    for e in np.unique(idx):
+        if e < 0 or e >= ex.E:
+            continue
+        t, sl = np.nonzero(idx == e)
+        W1, W3, W2 = ex.dense(int(e))
+        x = np.asarray(h[t], np.float64)
+        gate, up = x @ W1.T, x @ W3.T
+        if lo is not None:
+            (ag, bg, sg), (au, bu, su), _ = lo.adapters()
+            gate, up = gate + oracle.lora_delta(x, ag, bg, sg), up + oracle.lora_delta(x, au, bu, su)
+        a = oracle.glu_forward(gate, up, act)
+        down = a @ W2.T
+        if lo is not None:
+            down = down + oracle.lora_delta(a, lo.down_A, lo.down_B, lo.down_s)
+        scale[t, sl] = np.linalg.norm(np.asarray(g[t], np.float64), axis=1) * np.linalg.norm(down, axis=1) / np.sqrt(D)
+    return scale
+
+
+def assert_grad_w_close(got, want, scale, label):
+    """grad_w at the path's bar; where the dot products cancel as a whole (||want|| below a quarter
+    of ||scale||: a few slots whose <g, down> is much smaller than such dots usually are, e.g. one
+    token at top-1), the error is measured against ||scale|| instead, since the relative error of a
+    cancelling dot is no measure of the products' precision."""
+    wn, sn = float(np.linalg.norm(want)), float(np.linalg.norm(scale))
+    if wn >= 0.25 * sn:
+        assert_close(got, want, label)
+        return
+    err = float(np.linalg.norm(np.asarray(got, np.float64) - want))
+    print(f"{label}: cancelling dots (||want|| {wn:.3e}, ||scale|| {sn:.3e}): error / ||scale|| {err / sn:.3e}")
+    assert np.all(np.isfinite(np.asarray(got))), f"{label}: non-finite values"
+    assert err <= REL_L2_TOL * sn, f"{label}: error {err:.3e} > {REL_L2_TOL:.1e} x ||scale|| {sn:.3e}"
+
+
 @pytest.mark.parametrize("c", CONFIGS, ids=[label(c) for c in CONFIGS])
 def test_routed_layer_config(k, c):
     print(f"\n[case] shape sweep {label(c)}", flush=True)
@@ -112,7 +150,7 @@ def test_routed_layer_config(k, c):
     assert_close(out.cpu().numpy(), oracle.routed_forward(h, idx, w, ex, act, lora=lo), f"fwd {label(c)}")
     want = oracle.routed_backward(h, idx, w, ex, g, act, lora=lo)
     assert_close(rec[0].cpu().numpy(), want[0], f"grad_h {label(c)}")
-    assert_close(rec[1].cpu().numpy(), want[1], f"grad_w {label(c)}")
+    assert_grad_w_close(rec[1].cpu().numpy(), want[1], dot_scale(h, idx, ex, g, act, lo), f"grad_w {label(c)}")
     if mods:
         for name, a, b in zip(("gate_A", "gate_B", "up_A", "up_B", "down_A", "down_B"), rec[2], want[2]):
             assert a.shape == b.shape, name
