@@ -113,6 +113,50 @@ def assert_grad_w_close(got, want, scale, label):
     assert err <= REL_L2_TOL * sn, f"{label}: error {err:.3e} > {REL_L2_TOL:.1e} x ||scale|| {sn:.3e}"
 
 
+def lora_a_scales(h, idx, w, ex, g, act, lo):
+    """Natural sizes (Frobenius norms) of the gate_A and up_A gradients, sum over tokens t of
+    c_t (x) x_t with c_tj = s * sum over the token's pairs of <B[:, j], d_gate_p> (d_up for up_A,
+    lora_layer.py:178-226): each such dot has the natural size s ||B[:, j]|| ||d_gate_p|| / sqrt(F),
+    so an entry's is sqrt(sum_t (that for c_tj)^2 x_td^2). d_gate, d_up per pair in float64 as the
+    routed backward makes them (ids outside [0, E) add nothing)."""
+    N, D = h.shape
+    F = ex.F
+    sq = np.zeros((2, N))  # per token: sum over j of (natural size of c_tj)^2, gate and up
+    Bn = [np.linalg.norm(np.asarray(B, np.float64), axis=0) for B in (lo.gate_B, lo.up_B)]
+    for e in np.unique(idx):
+        if e < 0 or e >= ex.E:
+            continue
+        t, sl = np.nonzero(idx == e)
+        W1, W3, W2 = ex.dense(int(e))
+        x = np.asarray(h[t], np.float64)
+        gate = x @ W1.T + oracle.lora_delta(x, lo.gate_A, lo.gate_B, lo.gate_s)
+        up = x @ W3.T + oracle.lora_delta(x, lo.up_A, lo.up_B, lo.up_s)
+        a = oracle.glu_forward(gate, up, act)
+        d_down = np.asarray(g[t], np.float64) * np.asarray(w[t, sl], np.float64)[:, None]
+        d_act = d_down @ W2 + oracle.lora_gradients(d_down, a, lo.down_A, lo.down_B, lo.down_s)[2]
+        d_gate, d_up = oracle.glu_backward(d_act, gate, up, act)
+        for i, (dv, sc) in enumerate(((d_gate, lo.gate_s), (d_up, lo.up_s))):
+            np.add.at(sq[i], t, sc * sc * float(np.sum(Bn[i] ** 2)) * np.sum(dv * dv, axis=1) / F)
+    xn2 = np.sum(np.asarray(h, np.float64) ** 2, axis=1)
+    return [float(np.sqrt(np.sum(sq[i] * xn2))) for i in range(2)]
+
+
+def assert_scaled_close(got, want, scale, label):
+    """The path's bar with the error measured against max(||want||, scale), scale the natural size
+    of a result made of dot products: the error of a computed dot follows that size, not the dot's
+    value, so where the dots cancel their relative error is no measure of the products' precision;
+    for many terms ||want|| is about the scale and this is the rel-L2 bar, checked with the cosine
+    where ||want|| is the larger."""
+    wn = float(np.linalg.norm(want))
+    if wn >= scale:
+        assert_close(got, want, label)
+        return
+    err = float(np.linalg.norm(np.asarray(got, np.float64) - want))
+    print(f"{label}: cancelling dots (||want|| {wn:.3e}, scale {scale:.3e}): error / scale {err / scale:.3e}")
+    assert np.all(np.isfinite(np.asarray(got))), f"{label}: non-finite values"
+    assert err <= REL_L2_TOL * scale, f"{label}: error {err:.3e} > {REL_L2_TOL:.1e} x scale {scale:.3e}"
+
+
 @pytest.mark.parametrize("c", CONFIGS, ids=[label(c) for c in CONFIGS])
 def test_routed_layer_config(k, c):
     print(f"\n[case] shape sweep {label(c)}", flush=True)
@@ -155,9 +199,13 @@ def test_routed_layer_config(k, c):
     assert_close(rec[0].cpu().numpy(), want[0], f"grad_h {label(c)}")
     assert_grad_w_close(rec[1].cpu().numpy(), want[1], dot_scale(h, idx, ex, g, act, lo), f"grad_w {label(c)}")
     if mods:
+        sa = dict(zip(("gate_A", "up_A"), lora_a_scales(h, idx, w, ex, g, act, lo)))
         for name, a, b in zip(("gate_A", "gate_B", "up_A", "up_B", "down_A", "down_B"), rec[2], want[2]):
             assert a.shape == b.shape, name
-            assert_close(a.cpu().numpy(), b, f"grad {name} {label(c)}")
+            if name in sa:
+                assert_scaled_close(a.cpu().numpy(), b, sa[name], f"grad {name} {label(c)}")
+            else:
+                assert_close(a.cpu().numpy(), b, f"grad {name} {label(c)}")
 
 
 def draw_product(i):
